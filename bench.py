@@ -1,0 +1,316 @@
+"""Benchmark of the matrix-multiply hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (XLM-RoBERTa-large layer at seq=512, fp32):
+one "step" is the four linear layers of one encoder layer, back to back on
+one stream, operands resident in HBM:
+    QKV      X[512x1024] . W[1024x3072]
+    out      X[512x1024] . W[1024x1024]
+    FFN-up   X[512x1024] . W[1024x4096]
+    FFN-down H[512x4096] . W[4096x1024]
+Inputs: SplitMix64/Box-Muller, X,H ~ N(0,1) (seed 1001), W ~ N(0, 0.02)
+(seed 2002 + index).  `value` = 2*M*N*K summed over the step / step time.
+
+The same JSON line also carries:
+  roofline      the GEMM kernel against the fp32 MFMA peak (157.3 TFLOP/s),
+                from HIP events around each launch on the launch stream;
+  gemv          quantized decoder GEMVs (configs 3 and 4 at M <= 8) in GB/s
+                against 8 TB/s, rotating over >= 1 GB of distinct weight
+                copies so neither L2 nor the 256 MB Infinity Cache serves them;
+  qgemm, config1  the other configs' large-M products;
+  cpu_baseline  the reference's CPU path (the oracle's restatement of the
+                ops.zig fallback, test infrastructure) on the same workload.
+Prints exactly one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+XLMR_SHAPES = [  # (name, M, N, K)
+    ("qkv", 512, 3072, 1024),
+    ("out", 512, 1024, 1024),
+    ("ffn_up", 512, 4096, 1024),
+    ("ffn_down", 512, 1024, 4096),
+]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true", help="only the headline workload")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    return p.parse_args()
+
+
+class Timer:
+    """Times a launch sequence replayed from a HIP graph, with HIP events
+    recorded on the stream the graph runs on.  `launch(stream_ptr)` issues
+    the kernels on the given stream; it is run once eagerly (so workspaces
+    exist) and captured once."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time_ms(self, launch, reps: int, per_replay: int = 1) -> float:
+        t = self.torch
+        side = t.cuda.Stream()
+        with t.cuda.stream(side):
+            launch(side.cuda_stream)
+        t.cuda.synchronize()
+        g = t.cuda.CUDAGraph()
+        with t.cuda.graph(g, stream=side):
+            launch(side.cuda_stream)
+        t.cuda.synchronize()
+        cur = t.cuda.current_stream()
+        g.replay()
+        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        s.record(cur)
+        for _ in range(reps):
+            g.replay()
+        e.record(cur)
+        e.synchronize()
+        return s.elapsed_time(e) / (reps * per_replay)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        log("bench.py: only --gpus 1 is supported (single-GPU hot-path build)")
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from tomoul_amd import _abi, synth
+
+    _abi.init()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+    timer = Timer(torch)
+    log(f"device: {_abi.device_name()}")
+
+    def to_dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+    # ---------------------------------------------------------------- headline
+    x = to_dev(synth.normal_matrix(1001, 512, 1024))
+    h = to_dev(synth.normal_matrix(1001, 512, 4096))
+    ws = [to_dev(synth.normal_matrix(2002 + i, K, N, 0.02)) for i, (_, M, N, K) in enumerate(XLMR_SHAPES)]
+    outs = [torch.empty((M, N), dtype=torch.float32, device=dev) for (_, M, N, K) in XLMR_SHAPES]
+    ins = [x, x, x, h]
+    launches = []
+    for i, (name, M, N, K) in enumerate(XLMR_SHAPES):
+        a_p, b_p, c_p = ins[i].data_ptr(), ws[i].data_ptr(), outs[i].data_ptr()
+        launches.append((name, M, N, K,
+                         lambda st, M=M, N=N, K=K, a_p=a_p, b_p=b_p, c_p=c_p:
+                         _abi.gemm_dev(_abi.FMT_F32, M, N, K, a_p, b_p, c_p, stream=st)))
+    step_flops = sum(2.0 * M * N * K for (_, M, N, K) in XLMR_SHAPES)
+
+    def step(st=sptr):
+        for (_, _, _, _, fn) in launches:
+            fn(st)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # correctness guard against a float64 torch product on the GPU
+    max_rel = 0.0
+    for i, (name, M, N, K) in enumerate(XLMR_SHAPES):
+        ref = (ins[i].double() @ ws[i].double())
+        max_rel = max(max_rel, float((outs[i].double() - ref).abs().max() / ref.abs().max()))
+    log(f"headline max rel err vs f64: {max_rel:.3e}")
+
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ev_ms = ev0.elapsed_time(ev1)
+    ms_per_step = wall_ms / args.steps
+    value = step_flops / (ms_per_step * 1e-3) / 1e12
+    log(f"headline: {ms_per_step * 1e3:.1f} us/step wall, {ev_ms / args.steps * 1e3:.1f} us/step events, "
+        f"{value:.2f} TFLOP/s")
+
+    # per-launch durations of the GEMM kernel (events around each launch)
+    per_shape = {}
+    tot_fl, tot_ms = 0.0, 0.0
+    for (name, M, N, K, fn) in launches:
+        ms = timer.time_ms(fn, 50)
+        fl = 2.0 * M * N * K
+        per_shape[name] = {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2), "tflops": round(fl / ms / 1e9, 2)}
+        tot_fl += fl
+        tot_ms += ms
+    achieved = tot_fl / tot_ms / 1e9
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": "gemm_mfma_kernel (fp32, 16x16x4 f32 MFMA)", "per_shape": per_shape}
+    log(f"roofline: {json.dumps(roofline)}")
+
+    result = {
+        "metric": "GEMM TFLOP/s + quant GEMV HBM GB/s (as % of MI355X peak), 1 GPU",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (SplitMix64/Box-Muller, X~N(0,1), W~N(0,0.02))",
+        "config": {"workload": "XLM-R-large layer linears, seq=512, fp32: 512x1024.1024x3072, "
+                               "512x1024.1024x1024, 512x1024.1024x4096, 512x4096.4096x1024",
+                   "parallelism": "single GPU"},
+        "max_rel_err_vs_f64": max_rel,
+        "roofline": roofline,
+    }
+
+    if not args.no_extras:
+        result["gemv"] = bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np)
+        result["qgemm"] = bench_qgemm(torch, dev, sptr, timer, _abi, synth, np)
+        result["config1"] = bench_config1(torch, dev, sptr, timer, _abi, synth, np)
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+
+    print(json.dumps(result), flush=True)
+
+
+def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
+    """Configs 3 (Q8_0, M in {1, 8}) and 4 (Q4_0 pair, M in {1, 4, 8}).
+
+    Algorithmic bytes per launch = weight bytes + 4 (scale) + 4*M*K + 4*M*N.
+    Each timed pass walks >= 1 GB of distinct weight copies."""
+    out = {}
+    rot_bytes = 1 << 30
+
+    def run(fmt, K, N, Ms, seed, label):
+        w = synth.normal_matrix(seed, K, N, 0.02)
+        wt = torch.from_numpy(w).to(dev)
+        wbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+        q = torch.empty(wbytes, dtype=torch.uint8, device=dev)
+        sc = torch.empty(1, dtype=torch.float32, device=dev)
+        _abi.quantize_dev(fmt, K * N, wt.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
+        torch.cuda.synchronize()
+        scale = float(sc.item())
+        ncopy = max(2, rot_bytes // wbytes)
+        copies = q.repeat(ncopy).view(ncopy, wbytes)
+        del wt
+        res = {}
+        for M in Ms:
+            x = torch.from_numpy(synth.normal_matrix(1001, M, K)).to(dev)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            ptrs = [copies[i].data_ptr() for i in range(ncopy)]
+
+            def sweep(st):
+                for p in ptrs:
+                    _abi.gemm_dev(fmt, M, N, K, x.data_ptr(), p, y.data_ptr(), scale=scale, stream=st)
+
+            ms = timer.time_ms(sweep, 3, per_replay=ncopy)
+            alg = wbytes + 4 + 4 * M * K + 4 * M * N
+            gbs = alg / (ms * 1e-3) / 1e9
+            res[f"M{M}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": alg}
+            log(f"gemv {label} M={M}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+        del copies
+        torch.cuda.empty_cache()
+        return res
+
+    out["q8_1024x4096"] = run(_abi.FMT_Q8_0, 1024, 4096, [1, 8], 2002, "q8 1024x4096")
+    out["q4_1280x5120"] = run(_abi.FMT_Q4_0, 1280, 5120, [1, 4, 8], 2002, "q4 1280x5120")
+    out["q4_5120x1280"] = run(_abi.FMT_Q4_0, 5120, 1280, [1, 4, 8], 2003, "q4 5120x1280")
+    return out
+
+
+def bench_qgemm(torch, dev, sptr, timer, _abi, synth, np):
+    """Config 3 at M in {128, 512}: Q8_0 W[1024x4096] (MFMA path)."""
+    res = {}
+    K, N = 1024, 4096
+    w = torch.from_numpy(synth.normal_matrix(2002, K, N, 0.02)).to(dev)
+    q = torch.empty(K * N, dtype=torch.uint8, device=dev)
+    sc = torch.empty(1, dtype=torch.float32, device=dev)
+    _abi.quantize_dev(_abi.FMT_Q8_0, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
+    torch.cuda.synchronize()
+    scale = float(sc.item())
+    for M in (128, 512):
+        x = torch.from_numpy(synth.normal_matrix(1001, M, K)).to(dev)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        fn = lambda st: _abi.gemm_dev(_abi.FMT_Q8_0, M, N, K, x.data_ptr(), q.data_ptr(),  # noqa: E731
+                                      y.data_ptr(), scale=scale, stream=st)
+        ms = timer.time_ms(fn, 50)
+        tf = 2.0 * M * N * K / ms / 1e9
+        res[f"q8_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+        log(f"qgemm q8 M={M}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
+    return res
+
+
+def bench_config1(torch, dev, sptr, timer, _abi, synth, np):
+    """Config 1: Whisper-tiny MLP X[1500x384] . W[384x1536] + bias (fused)."""
+    x = torch.from_numpy(synth.normal_matrix(1001, 1500, 384)).to(dev)
+    w = torch.from_numpy(synth.normal_matrix(2002, 384, 1536, 0.02)).to(dev)
+    b = torch.from_numpy(synth.normal(3003, 1536, 0.0, 0.02)).to(dev)
+    y = torch.empty((1500, 1536), dtype=torch.float32, device=dev)
+    fn = lambda st: _abi.gemm_dev(_abi.FMT_F32, 1500, 1536, 384, x.data_ptr(), w.data_ptr(),  # noqa: E731
+                                  y.data_ptr(), bias_ptr=b.data_ptr(), stream=st)
+    ms = timer.time_ms(fn, 100)
+    tf = 2.0 * 1500 * 1536 * 384 / ms / 1e9
+    log(f"config1: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
+    return {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+
+
+def cpu_baseline(budget_s: float):
+    """The reference's fp32 CPU path (oracle restatement of the register-
+    blocked ops.zig fallback, single-threaded as in the reference) on the
+    headline step; repeated until about `budget_s` seconds are spent."""
+    from oracle import oracle as orc
+    from tomoul_amd import synth
+
+    xs = synth.normal_matrix(1001, 512, 1024)
+    hs = synth.normal_matrix(1001, 512, 4096)
+    wts = [synth.normal_matrix(2002 + i, K, N, 0.02) for i, (_, M, N, K) in enumerate(XLMR_SHAPES)]
+    ins = [xs, xs, xs, hs]
+    step_flops = sum(2.0 * M * N * K for (_, M, N, K) in XLMR_SHAPES)
+    orc.lib()
+    steps, t_tot = 0, 0.0
+    while t_tot < budget_s and steps < 50:
+        t0 = time.perf_counter()
+        for i in range(4):
+            orc.matmul(ins[i], wts[i])
+        t_tot += time.perf_counter() - t0
+        steps += 1
+    tf = step_flops * steps / t_tot / 1e12
+    log(f"cpu baseline: {steps} steps in {t_tot:.1f} s, {tf * 1e3:.2f} GFLOP/s (1 thread)")
+    return {"value": round(tf, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{steps} full headline steps (4 GEMMs, {step_flops / 1e9:.2f} GFLOP each) with the "
+                      f"oracle's restatement of the ops.zig:277-414 fallback, 1 thread, -O3 AVX2, "
+                      f"{t_tot:.1f} s; zblas (the reference default) is not vendored and cannot be timed",
+            "host_cpus": os.cpu_count()}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,158 @@
+/*
+ * tomoul_hip.h -- C ABI of the MI355X (gfx950) matrix-multiply backend.
+ *
+ * A drop-in for the backends behind Tomoul's ops.matmul / ops.matmulBias /
+ * ops.matmulParallel / ops.matvec and quantization.matmulF32Q8Simd /
+ * matmulF32Q8KSimd / matmulF32Q4Simd.  Every pointer argument of the
+ * "host" entry points is a plain host pointer, exactly as the Zig call sites
+ * pass slices today; the "_dev" entry points take device pointers that are
+ * already resident in HBM plus a hipStream_t (passed as void*).
+ *
+ * Matrices are row-major: A is [M,K] (lda = K), B is [K,N] (ldb = N) -- the
+ * [in, out] layout every reference caller hands over -- and C is [M,N]
+ * (ldc = N).  Quantized B uses the reference's in-memory layouts unchanged:
+ *   Q8_0  int8  q[K*N] + one f32 scale            (quantization.zig:39-90)
+ *   Q8_K  int8  q[K*N] + f32 scales[ceil(K*N/32)],
+ *         scale of element (k,j) = scales[(k*N+j)/block]
+ *                                                 (quantization.zig:327-403)
+ *   Q4_0  uint8 packed[ceil(K*N/2)] + one f32 scale; element e is the low
+ *         nibble of byte e/2 when e is even, the high nibble when odd, read
+ *         as a two's-complement 4-bit value   (quantization.zig:627-717)
+ * The format ids equal the .tl header's quant-format byte
+ * (src/core/loader.zig:23-29).
+ *
+ * Return value: 0 on success, a negative TML_ERR_* code otherwise; the
+ * message of the last failure on the calling thread is available from
+ * tml_hip_last_error().  Sizes are int64_t; a negative size is
+ * TML_ERR_INVALID_SHAPE, M == 0 or N == 0 is a successful no-op.
+ *
+ * Threading: calls are thread-compatible, not thread-safe (as the reference's
+ * callers: one model-forward thread, src/core/ops.zig:485).  All calls on
+ * one device share that device's split-K workspace, so "_dev" calls issued
+ * concurrently on different streams of the same device race; issue them on
+ * one stream.
+ */
+#ifndef TOMOUL_HIP_H
+#define TOMOUL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The first three mirror the reference's OpsError /
+ * QuantError members (src/core/ops.zig:47-52, quantization.zig:25-30). */
+#define TML_OK 0
+#define TML_ERR_INVALID_SHAPE (-1)  /* OpsError.InvalidShape                  */
+#define TML_ERR_SHAPE_MISMATCH (-2) /* OpsError.ShapeMismatch                 */
+#define TML_ERR_OUT_OF_MEMORY (-3)  /* OpsError.OutOfMemory (device memory)   */
+#define TML_ERR_INVALID_FORMAT (-4) /* QuantError.InvalidFormat               */
+#define TML_ERR_INVALID_ARG (-5)    /* null pointer, bad block size, ...      */
+#define TML_ERR_NO_DEVICE (-6)      /* no usable HIP device                   */
+#define TML_ERR_HIP (-7)            /* a HIP runtime call failed              */
+
+/* Weight formats (= .tl quant-format byte, src/core/loader.zig:23-29). */
+#define TML_FMT_F32 0
+#define TML_FMT_Q8_0 1
+#define TML_FMT_Q4_0 2
+#define TML_FMT_Q8_K 3
+
+/* ---------------------------------------------------------------- setup */
+
+/* Selects the current HIP device and creates the library's stream.  Called
+ * implicitly by every entry point; calling it first surfaces device errors
+ * early.  No counterpart in the reference (zblas needs no init). */
+int tml_hip_init(void);
+
+/* Frees every device buffer, registered weight and stream of the library. */
+void tml_hip_shutdown(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *tml_hip_last_error(void);
+
+/* Writes the device name (e.g. "AMD Instinct MI355X") into buf. */
+int tml_hip_device_name(char *buf, size_t len);
+
+/* ---------------------------------------------------- host-pointer API */
+
+/* C = alpha * A.B + beta * C.  Replaces zblas.sgemm(m, n, k, a, b, c, alpha,
+ * beta) at src/core/ops.zig:273 and :513, and blas.sgemm -> cblas_sgemm
+ * (RowMajor, NoTrans, NoTrans, lda=K, ldb=N, ldc=N) at src/core/blas.zig:68-94
+ * (call sites src/core/ops.zig:269, :448, :516).  With beta == 0 the input
+ * contents of C are ignored (BLAS convention). */
+int tml_hip_sgemm(int64_t M, int64_t N, int64_t K, const float *A, const float *B, float *C, float alpha,
+                  float beta);
+
+/* C = A.B + bias[N] broadcast over rows.  Replaces zblas.sgemmBias(m, n, k,
+ * a, b, bias.ptr, c) at src/core/ops.zig:442 (ops.matmulBias,
+ * src/core/ops.zig:422-471). */
+int tml_hip_sgemm_bias(int64_t M, int64_t N, int64_t K, const float *A, const float *B, const float *bias,
+                       float *C);
+
+/* y[M] = alpha * A[M,N].x[N] + beta * y.  Replaces zblas.sgemv(m, n, a, x,
+ * y, alpha, beta) at src/core/ops.zig:630 (ops.matvec, :611-642). */
+int tml_hip_sgemv(int64_t M, int64_t N, const float *A, const float *x, float *y, float alpha, float beta);
+
+/* C = A . dequant(Q8_0 B).  Replaces zblas.sgemmQ8(m, n, k, a, b.data,
+ * scale, c) at src/core/quantization.zig:236 (matmulF32Q8Simd, :207-314). */
+int tml_hip_sgemm_q8(int64_t M, int64_t N, int64_t K, const float *A, const int8_t *Bq, float scale, float *C);
+
+/* C = A . dequant(Q8_K B).  Replaces zblas.sgemmQ8K(m, n, k, a, b.data,
+ * b.scales, b.block_size, c) at src/core/quantization.zig:555
+ * (matmulF32Q8KSimd, :528-617).  scales holds ceil(K*N/block) values;
+ * block must be positive (the reference always uses 32). */
+int tml_hip_sgemm_q8k(int64_t M, int64_t N, int64_t K, const float *A, const int8_t *Bq, const float *scales,
+                      int64_t block, float *C);
+
+/* C = A . dequant(Q4_0 B), Bp holding ceil(K*N/2) packed bytes.  Replaces
+ * the in-tree loop of matmulF32Q4Simd (src/core/quantization.zig:829-957);
+ * the reference has no zblas entry for Q4_0.  Unlike the reference's 32-wide
+ * SIMD loop, odd N is handled exactly (every element is addressed as
+ * k*N + j). */
+int tml_hip_sgemm_q4(int64_t M, int64_t N, int64_t K, const float *A, const uint8_t *Bp, float scale, float *C);
+
+/* Host-pointer form of tml_hip_quantize_dev below (synchronous): the GPU
+ * replacement for the load-time quantizers quantizeQ8 / quantizeQ8K /
+ * quantizeQ4 (src/core/quantization.zig:98-129, :406-446, :721-754) that
+ * produce the in-memory layouts consumed above. */
+int tml_hip_quantize(int fmt, int64_t n, const float *w, void *q, float *scales);
+
+/* Weight residency.  Weights are immutable after load in the reference
+ * (AttentionWeights / TransformerBlockWeights own them until deinit,
+ * src/core/attention.zig:54-86), so a host buffer registered here is copied
+ * to HBM once; later host-pointer calls whose B (or Q8_K scales) pointer and
+ * size match a registered buffer use the resident copy instead of uploading
+ * it again.  Registering an already registered pointer refreshes the copy.
+ * No counterpart in the reference. */
+int tml_hip_weight_register(const void *host, size_t bytes);
+int tml_hip_weight_release(const void *host);
+
+/* ------------------------------------------------------ device-pointer API */
+
+/* The compute entry point behind every call above, on resident operands:
+ *   C = alpha * (A . dequant(B)) + beta * C + bias
+ * fmt       TML_FMT_*; B points at the f32 / int8 / packed-int4 data.
+ * scale     per-tensor scale of Q8_0 / Q4_0 (ignored for F32 and Q8_K).
+ * scales    device pointer to the Q8_K block scales (NULL otherwise).
+ * block     Q8_K block size (ignored otherwise).
+ * bias      device pointer to N floats, or NULL.
+ * stream    hipStream_t to launch on (NULL = the null stream).
+ * All pointers are device pointers.  Asynchronous: returns after the launch. */
+int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                     const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
+                     void *stream);
+
+/* On-device quantizers, bit-identical to the reference's Zig quantizers
+ * (quantizeQ8 quantization.zig:98-129, quantizeQ8K :406-446, quantizeQ4
+ * :721-754).  w holds n floats; q receives n int8 (Q8_0 / Q8_K) or
+ * ceil(n/2) packed bytes (Q4_0); scales receives 1 float (Q8_0 / Q4_0) or
+ * ceil(n/32) floats (Q8_K).  Device pointers, asynchronous on stream. */
+int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TOMOUL_HIP_H */

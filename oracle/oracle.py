@@ -1,0 +1,261 @@
+"""ctypes view of the CPU oracle (oracle/oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker or the timed CPU baseline.  The
+product package (tomoul_amd) never imports this module.
+
+Every wrapper takes and returns numpy arrays; shapes follow the reference's
+row-major [M,K] x [K,N] convention (src/core/ops.zig:235-264).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+
+
+def build() -> str:
+    """Compile oracle.c with its Makefile (a few seconds)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        build()
+    L = ctypes.CDLL(_LIB_PATH)
+    sig = {
+        "orc_splitmix64_next": (ctypes.c_uint64, [ctypes.POINTER(ctypes.c_uint64)]),
+        "orc_fill_normal": (None, [ctypes.c_uint64, _i64, ctypes.c_double, ctypes.c_double, _f32p]),
+        "orc_matmul_f32_naive": (None, [_i64, _i64, _i64, _f32p, _f32p, _f32p]),
+        "orc_matmul_f32": (None, [_i64, _i64, _i64, _f32p, _f32p, _f32p]),
+        "orc_matmul_f32_mt": (None, [_i64, _i64, _i64, _f32p, _f32p, _f32p, ctypes.c_int]),
+        "orc_matmul_bias_f32": (None, [_i64, _i64, _i64, _f32p, _f32p, _f32p, _f32p]),
+        "orc_sgemm": (None, [_i64, _i64, _i64, _f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_float]),
+        "orc_matmul_f64": (None, [_i64, _i64, _i64, _f32p, _f32p, _f64p]),
+        "orc_matvec": (None, [_i64, _i64, _f32p, _f32p, _f32p]),
+        "orc_quantize_q8": (None, [_i64, _f32p, _i8p, ctypes.POINTER(ctypes.c_float)]),
+        "orc_dequantize_q8": (None, [_i64, _i8p, ctypes.c_float, _f32p]),
+        "orc_quantize_q8k": (None, [_i64, _f32p, _i8p, _f32p]),
+        "orc_dequantize_q8k": (None, [_i64, _i8p, _f32p, _i64, _f32p]),
+        "orc_q4_get": (ctypes.c_int8, [_u8p, _i64]),
+        "orc_q4_set": (None, [_u8p, _i64, ctypes.c_int8]),
+        "orc_quantize_q4": (None, [_i64, _f32p, _u8p, ctypes.POINTER(ctypes.c_float)]),
+        "orc_dequantize_q4": (None, [_i64, _u8p, ctypes.c_float, _f32p]),
+        "orc_matmul_q8": (None, [_i64, _i64, _i64, _f32p, _i8p, ctypes.c_float, _f32p]),
+        "orc_matmul_q8k": (None, [_i64, _i64, _i64, _f32p, _i8p, _f32p, _i64, _f32p]),
+        "orc_matmul_q4": (None, [_i64, _i64, _i64, _f32p, _u8p, ctypes.c_float, _f32p]),
+        "orc_matmul_q8_mt": (None, [_i64, _i64, _i64, _f32p, _i8p, ctypes.c_float, _f32p, ctypes.c_int]),
+        "orc_matmul_q4_mt": (None, [_i64, _i64, _i64, _f32p, _u8p, ctypes.c_float, _f32p, ctypes.c_int]),
+        "orc_max_threads": (ctypes.c_int, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def _mkn(a: np.ndarray, b: np.ndarray):
+    assert a.ndim == 2 and b.ndim == 2 and a.shape[1] == b.shape[0], (a.shape, b.shape)
+    return a.shape[0], b.shape[1], a.shape[1]
+
+
+# ---------------------------------------------------------------- generator
+def splitmix64_stream(seed: int, count: int) -> list[int]:
+    st = ctypes.c_uint64(seed)
+    return [lib().orc_splitmix64_next(ctypes.byref(st)) for _ in range(count)]
+
+
+def fill_normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().orc_fill_normal(seed, n, mean, std, out)
+    return out
+
+
+# ---------------------------------------------------------------- fp32 GEMM
+def matmul(a, b) -> np.ndarray:
+    """ops.matmul fallback semantics (src/core/ops.zig:277-414)."""
+    a, b = _f32(a), _f32(b)
+    m, n, k = _mkn(a, b)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_f32(m, n, k, a, b, c)
+    return c
+
+
+def matmul_naive(a, b) -> np.ndarray:
+    a, b = _f32(a), _f32(b)
+    m, n, k = _mkn(a, b)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_f32_naive(m, n, k, a, b, c)
+    return c
+
+
+def matmul_mt(a, b, nthreads: int) -> np.ndarray:
+    a, b = _f32(a), _f32(b)
+    m, n, k = _mkn(a, b)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_f32_mt(m, n, k, a, b, c, int(nthreads))
+    return c
+
+
+def matmul_bias(a, b, bias) -> np.ndarray:
+    """ops.matmulBias fallback (src/core/ops.zig:446-468)."""
+    a, b, bias = _f32(a), _f32(b), _f32(bias)
+    m, n, k = _mkn(a, b)
+    assert bias.shape == (n,)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_bias_f32(m, n, k, a, b, bias, c)
+    return c
+
+
+def sgemm(a, b, c, alpha: float, beta: float) -> np.ndarray:
+    """cblas_sgemm row-major semantics bound at src/core/blas.zig:68-94."""
+    a, b = _f32(a), _f32(b)
+    m, n, k = _mkn(a, b)
+    out = _f32(c).copy() if c is not None else np.zeros((m, n), np.float32)
+    lib().orc_sgemm(m, n, k, a, b, out, alpha, beta)
+    return out
+
+
+def matmul_f64(a, b) -> np.ndarray:
+    a, b = _f32(a), _f32(b)
+    m, n, k = _mkn(a, b)
+    c = np.empty((m, n), dtype=np.float64)
+    lib().orc_matmul_f64(m, n, k, a, b, c)
+    return c
+
+
+def matvec(a, x) -> np.ndarray:
+    a, x = _f32(a), _f32(x)
+    assert a.ndim == 2 and x.shape == (a.shape[1],)
+    y = np.empty(a.shape[0], dtype=np.float32)
+    lib().orc_matvec(a.shape[0], a.shape[1], a, x, y)
+    return y
+
+
+# ---------------------------------------------------------------- quantizers
+def quantize_q8(w) -> tuple[np.ndarray, float]:
+    w = _f32(w)
+    q = np.empty(w.shape, dtype=np.int8)
+    s = ctypes.c_float()
+    lib().orc_quantize_q8(w.size, w.reshape(-1), q.reshape(-1), ctypes.byref(s))
+    return q, s.value
+
+
+def dequantize_q8(q, scale: float) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    out = np.empty(q.shape, dtype=np.float32)
+    lib().orc_dequantize_q8(q.size, q.reshape(-1), scale, out.reshape(-1))
+    return out
+
+
+def quantize_q8k(w) -> tuple[np.ndarray, np.ndarray]:
+    w = _f32(w)
+    q = np.empty(w.shape, dtype=np.int8)
+    scales = np.empty((w.size + 31) // 32, dtype=np.float32)
+    lib().orc_quantize_q8k(w.size, w.reshape(-1), q.reshape(-1), scales)
+    return q, scales
+
+
+def dequantize_q8k(q, scales, block: int = 32) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    out = np.empty(q.shape, dtype=np.float32)
+    lib().orc_dequantize_q8k(q.size, q.reshape(-1), _f32(scales), block, out.reshape(-1))
+    return out
+
+
+def quantize_q4(w) -> tuple[np.ndarray, float]:
+    """Returns (packed bytes of length ceil(n/2), scale)."""
+    w = _f32(w)
+    packed = np.empty((w.size + 1) // 2, dtype=np.uint8)
+    s = ctypes.c_float()
+    lib().orc_quantize_q4(w.size, w.reshape(-1), packed, ctypes.byref(s))
+    return packed, s.value
+
+
+def q4_get(packed, idx: int) -> int:
+    return int(lib().orc_q4_get(np.ascontiguousarray(packed, dtype=np.uint8), idx))
+
+
+def q4_set(packed: np.ndarray, idx: int, value: int) -> None:
+    assert packed.dtype == np.uint8 and packed.flags["C_CONTIGUOUS"]
+    lib().orc_q4_set(packed, idx, value)
+
+
+def dequantize_q4(packed, n: int, scale: float) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().orc_dequantize_q4(n, np.ascontiguousarray(packed, dtype=np.uint8), scale, out)
+    return out
+
+
+# ---------------------------------------------------------------- quantized matmuls
+def matmul_q8(a, q, scale: float) -> np.ndarray:
+    """matmulF32Q8 (src/core/quantization.zig:158-203)."""
+    a = _f32(a)
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    m, n, k = _mkn(a, q)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_q8(m, n, k, a, q, scale, c)
+    return c
+
+
+def matmul_q8k(a, q, scales, block: int = 32) -> np.ndarray:
+    """matmulF32Q8K (src/core/quantization.zig:477-525)."""
+    a = _f32(a)
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    m, n, k = _mkn(a, q)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_q8k(m, n, k, a, q, _f32(scales), block, c)
+    return c
+
+
+def matmul_q4(a, packed, k: int, n: int, scale: float) -> np.ndarray:
+    """matmulF32Q4 (src/core/quantization.zig:778-824); packed holds K*N nibbles."""
+    a = _f32(a)
+    assert a.ndim == 2 and a.shape[1] == k
+    m = a.shape[0]
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_q4(m, n, k, a, np.ascontiguousarray(packed, dtype=np.uint8), scale, c)
+    return c
+
+
+def matmul_q8_mt(a, q, scale: float, nthreads: int) -> np.ndarray:
+    a = _f32(a)
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    m, n, k = _mkn(a, q)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_q8_mt(m, n, k, a, q, scale, c, int(nthreads))
+    return c
+
+
+def matmul_q4_mt(a, packed, k: int, n: int, scale: float, nthreads: int) -> np.ndarray:
+    a = _f32(a)
+    m = a.shape[0]
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_q4_mt(m, n, k, a, np.ascontiguousarray(packed, dtype=np.uint8), scale, c, int(nthreads))
+    return c
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())

@@ -1,0 +1,95 @@
+"""CPU checks of the boundary: the built library loads, exports every
+function include/tomoul_hip.h declares, and the host-side mirrors validate
+shapes (raising the reference's errors) before any device work.  No GPU
+compute is issued here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from tomoul_amd import _abi, ops, quantization as qz
+from tomoul_amd.tensor import Tensor
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tomoul_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tml_hip_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for required in ("tml_hip_sgemm", "tml_hip_sgemm_bias", "tml_hip_sgemv", "tml_hip_sgemm_q8",
+                     "tml_hip_sgemm_q8k", "tml_hip_sgemm_q4", "tml_hip_gemm_dev", "tml_hip_quantize_dev"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_abi.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    # and the Python binding covers exactly the declared set
+    assert sorted(_abi.SIGNATURES) == declared_functions()
+
+
+def test_exported_symbols_have_c_linkage():
+    out = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (tml_hip_\w+)$", out, flags=re.M))
+    assert set(declared_functions()) <= exported
+
+
+def test_no_device_is_an_error_code_not_a_crash():
+    # Without a GPU the library reports TML_ERR_NO_DEVICE (callers fall back
+    # the way the reference HAL does); with one, init succeeds.
+    code = _abi.lib().tml_hip_init()
+    has_gpu = os.path.exists("/dev/kfd") and code == 0
+    if not has_gpu:
+        assert code == _abi.TML_ERR_NO_DEVICE
+        assert b"device" in _abi.lib().tml_hip_last_error()
+        a = np.ones((2, 2), np.float32)
+        with pytest.raises(_abi.TmlError) as e:
+            _abi.sgemm(2, 2, 2, a, a, a)
+        assert e.value.code == _abi.TML_ERR_NO_DEVICE
+
+
+def test_mirror_shape_errors():
+    # src/core/ops.zig:236-249, 425-434 and quantization.zig:172-180
+    with pytest.raises(ops.OpsError.ShapeMismatch):
+        ops.matmul(Tensor.init((2, 3)), Tensor.init((2, 2)))
+    with pytest.raises(ops.OpsError.InvalidShape):
+        ops.matmul(Tensor.init((6,)), Tensor.init((6, 1)))
+    with pytest.raises(ops.OpsError.InvalidShape):
+        ops.matmulBias(Tensor.init((2, 3)), Tensor.init((3, 2)), Tensor.init((1, 2)))
+    with pytest.raises(ops.OpsError.ShapeMismatch):
+        ops.matmulBias(Tensor.init((2, 3)), Tensor.init((3, 2)), Tensor.init((3,)))
+    with pytest.raises(ops.OpsError.ShapeMismatch):
+        ops.matvec(Tensor.init((2, 3)), Tensor.init((2,)))
+    q = qz.QuantizedTensorQ8(1.0, np.zeros(6, np.int8), (2, 3))
+    with pytest.raises(qz.QuantError.ShapeMismatch):
+        qz.matmulF32Q8Simd(Tensor.init((4, 4)), q)
+    with pytest.raises(qz.QuantError.InvalidShape):
+        qz.matmulF32Q8Simd(Tensor.init((4,)), q)
+
+
+def test_q4_container_accessors():
+    # quantization.zig:1185-1214 on the product container
+    t = qz.QuantizedTensorQ4.init((8,))
+    vals = [-7, -3, 0, 3, 7, -1, 1, -2]
+    for i, v in enumerate(vals):
+        t.set(i, v)
+    assert [t.get(i) for i in range(8)] == vals
+    assert t.data.tolist() == [0xD9, 0x30, 0xF7, 0xE1]
+    assert t.compressionRatio() > 3.0
+
+
+def test_tensor_container():
+    t = Tensor.init((2, 3))
+    assert t.data.dtype == np.float32 and not t.data.any() and t.shape == (2, 3)
+    with pytest.raises(ValueError):
+        Tensor(np.zeros(5, np.float32), (2, 3))

@@ -1,0 +1,302 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Tolerances: fp32 paths max relative error
+max|G-R|/max|R| <= 1e-4 against the reference's fp32 fallback semantics;
+quantized paths <= 1e-3 against the reference's dequantize-then-fp32-
+accumulate scalar loops (matmulF32Q8 / Q8K / Q4).  Quantizers and integer
+products are compared bitwise.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import elementwise_ok, rel_err
+from tomoul_amd import _abi, ops, quantization as qz, synth
+from tomoul_amd.tensor import Tensor
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+Q_TOL = 1e-3
+NT = min(16, os.cpu_count() or 1)
+
+
+def T(a):
+    return Tensor.from_numpy(np.asarray(a, dtype=np.float32))
+
+
+def rnd(seed, m, n, std=1.0):
+    return synth.normal_matrix(seed, m, n, std)
+
+
+# ------------------------------------------------------------- reference KATs
+def test_kat_matmul_2x3_3x2():
+    # src/core/ops.zig:969-1005
+    c = ops.matmul(T([[1, 2, 3], [4, 5, 6]]), T([[7, 8], [9, 10], [11, 12]]))
+    assert c.shape == (2, 2)
+    assert c.data.tolist() == [58.0, 64.0, 139.0, 154.0]
+
+
+def test_kat_linear_compat():
+    # src/core/ops.zig:937-967: [1,1,1] . W^T with W = [[1,2,3],[4,5,6]]
+    w_t = np.array([[1, 2, 3], [4, 5, 6]], dtype=np.float32).T.copy()
+    c = ops.matmul(T([[1, 1, 1]]), T(w_t))
+    assert c.data.tolist() == [6.0, 15.0]
+
+
+def test_kat_identity_and_demo():
+    # src/core/ops.zig:1023-1046 and src/main.zig:141-148
+    assert ops.matmul(T([[1, 2], [3, 4]]), T([[1, 0], [0, 1]])).data.tolist() == [1, 2, 3, 4]
+    assert ops.matmul(T([[1, 2, 3]]), T([[1, 2], [3, 4], [5, 6]])).data.tolist() == [22.0, 28.0]
+
+
+def test_kat_matvec():
+    # src/core/ops.zig:1048-1076
+    y = ops.matvec(T([[1, 2, 3], [4, 5, 6]]), Tensor.initWithData((3,), [1, 2, 3]))
+    assert y.shape == (2,) and y.data.tolist() == [14.0, 32.0]
+
+
+def test_shape_errors_before_device():
+    # src/core/ops.zig:1007-1021
+    with pytest.raises(ops.OpsError.ShapeMismatch):
+        ops.matmul(Tensor.init((2, 3)), Tensor.init((2, 2)))
+    with pytest.raises(ops.OpsError.InvalidShape):
+        ops.matmul(Tensor.init((2, 3, 1)), Tensor.init((3, 2)))
+    with pytest.raises(ops.OpsError.ShapeMismatch):
+        ops.matmulBias(Tensor.init((2, 3)), Tensor.init((3, 2)), Tensor.init((3,)))
+
+
+def test_abi_error_codes():
+    a = np.zeros((2, 2), np.float32)
+    with pytest.raises(_abi.TmlError) as e:
+        _abi.sgemm(-1, 2, 2, a, a, a)
+    assert e.value.code == _abi.TML_ERR_INVALID_SHAPE
+    with pytest.raises(_abi.TmlError) as e:
+        _abi.check(_abi.lib().tml_hip_gemm_dev(9, 2, 2, 2, 1, 1, 1.0, None, 32, None, 1, 1.0, 0.0, None))
+    assert e.value.code == _abi.TML_ERR_INVALID_FORMAT
+    _abi.sgemm(0, 5, 3, a, a, a)  # empty output: no-op
+
+
+def test_exact_small_integers(orc):
+    # Products of small integers are exact in f32 whatever the summation
+    # order, so the GPU result must equal the oracle bitwise.
+    rng = np.random.default_rng(7)
+    for (m, n, k) in [(5, 7, 9), (64, 64, 64), (130, 70, 50), (3, 1000, 40)]:
+        a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+        b = rng.integers(-4, 5, size=(k, n)).astype(np.float32)
+        got = ops.matmul(T(a), T(b)).numpy()
+        np.testing.assert_array_equal(got, orc.matmul(a, b))
+
+
+# ------------------------------------------------------------------ fp32 GEMM
+FP32_SHAPES = [
+    (1, 1, 1), (1, 4096, 1024), (2, 33, 17), (4, 100, 64), (8, 1280, 5120), (9, 64, 64),
+    (17, 33, 65), (64, 64, 64), (100, 200, 300), (128, 128, 128), (127, 129, 131),
+    (1500, 1536, 384),                     # config 1 (Whisper-tiny MLP)
+    (512, 3072, 1024), (512, 1024, 1024),  # config 2 (XLM-R large)
+    (512, 4096, 1024), (512, 1024, 4096),
+]
+
+
+@pytest.mark.parametrize("m,n,k", FP32_SHAPES)
+def test_sgemm_vs_oracle(orc, m, n, k):
+    a = rnd(1001, m, k)
+    b = rnd(2002, k, n, 0.02)
+    ref = orc.matmul_mt(a, b, NT)
+    got = ops.matmul(T(a), T(b)).numpy()
+    err = rel_err(got, ref)
+    print(f"sgemm {m}x{n}x{k}: rel {err:.3e}")
+    assert err <= FP32_TOL
+    assert elementwise_ok(got, ref, 1e-4)
+
+
+def test_sgemm_bias_config1(orc):
+    a, b = rnd(1001, 1500, 384), rnd(2002, 384, 1536, 0.02)
+    bias = synth.normal(3003, 1536, 0.0, 0.02)
+    ref = orc.matmul_bias(a, b, bias)
+    got = ops.matmulBias(T(a), T(b), Tensor.from_numpy(bias)).numpy()
+    assert rel_err(got, ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("m", [1, 3, 8, 40])
+def test_sgemm_bias_small(orc, m):
+    a, b = rnd(11, m, 96), rnd(12, 96, 130, 0.02)
+    bias = synth.normal(13, 130, 0.0, 0.02)
+    got = ops.matmulBias(T(a), T(b), Tensor.from_numpy(bias)).numpy()
+    assert rel_err(got, orc.matmul_bias(a, b, bias)) <= FP32_TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(4, 64, 32), (70, 96, 48)])
+@pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.5, 2.0), (-1.0, 1.0)])
+def test_sgemm_alpha_beta(orc, m, n, k, alpha, beta):
+    a, b = rnd(21, m, k), rnd(22, k, n)
+    c0 = rnd(23, m, n)
+    c = c0.copy()
+    _abi.sgemm(m, n, k, a, b, c, alpha, beta)
+    ref = orc.sgemm(a, b, c0, alpha, beta)
+    assert rel_err(c, ref) <= FP32_TOL
+
+
+def test_sgemm_beta_zero_ignores_nan(orc):
+    a, b = rnd(31, 10, 20), rnd(32, 20, 30)
+    c = np.full((10, 30), np.nan, np.float32)
+    _abi.sgemm(10, 30, 20, a, b, c, 1.0, 0.0)
+    assert np.isfinite(c).all()
+
+
+def test_sgemv_vs_oracle(orc):
+    a = rnd(41, 300, 517)
+    x = synth.normal(42, 517)
+    y = np.zeros(300, np.float32)
+    _abi.sgemv(300, 517, a, x, y)
+    assert rel_err(y, orc.matvec(a, x)) <= FP32_TOL
+
+
+def test_unaligned_views(orc):
+    # Operands that are not 16-byte aligned take the generic path.
+    buf_a = np.zeros(1 + 33 * 20, np.float32)
+    buf_b = np.zeros(1 + 20 * 44, np.float32)
+    a = buf_a[1:].reshape(33, 20)
+    b = buf_b[1:].reshape(20, 44)
+    a[:] = rnd(51, 33, 20)
+    b[:] = rnd(52, 20, 44)
+    assert a.ctypes.data % 16 != 0
+    c = np.zeros((33, 44), np.float32)
+    _abi.sgemm(33, 44, 20, a, b, c)
+    assert rel_err(c, orc.matmul(a, b)) <= FP32_TOL
+
+
+# ------------------------------------------------------------- quantizers
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 1000, 1024 * 4096])
+def test_quantize_q8_bitexact(orc, n):
+    w = synth.normal(2002, n, 0.0, 0.02)
+    q_ref, s_ref = orc.quantize_q8(w)
+    q = qz.quantizeQ8(Tensor(w, (n,)))
+    assert np.float32(q.scale) == np.float32(s_ref)
+    np.testing.assert_array_equal(q.data, q_ref)
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 1001, 1280 * 5120])
+def test_quantize_q4_bitexact(orc, n):
+    w = synth.normal(2003, n, 0.0, 0.02)
+    p_ref, s_ref = orc.quantize_q4(w)
+    q = qz.quantizeQ4(Tensor(w, (n,)))
+    assert np.float32(q.scale) == np.float32(s_ref)
+    np.testing.assert_array_equal(q.data, p_ref)
+
+
+@pytest.mark.parametrize("n", [1, 32, 100, 64 * 32, 1024 * 4096 + 17])
+def test_quantize_q8k_bitexact(orc, n):
+    w = synth.normal(2004, n, 0.0, 0.02)
+    w[: min(n, 32)] = 0.0  # an all-zero first block -> scale 1
+    q_ref, s_ref = orc.quantize_q8k(w)
+    q = qz.quantizeQ8K(Tensor(w, (n,)))
+    np.testing.assert_array_equal(q.scales, s_ref)
+    np.testing.assert_array_equal(q.data, q_ref)
+
+
+def test_quantize_kats():
+    # quantization.zig:1022-1038, 1120-1144, 1239-1255, 1337-1360 and the
+    # half-away-from-zero tie rule (127 * 0.5/127 = 0.5 -> 1, -0.5 -> -1).
+    q = qz.quantizeQ8(Tensor.initWithData((5,), [100, -100, 0, 50, -50]))
+    assert q.data[:3].tolist() == [127, -127, 0]
+    assert abs(q.scale - 100 / 127) < 1e-4
+    z = qz.quantizeQ8(Tensor.init((10,)))
+    assert z.scale == 1.0 and not z.data.any()
+    q4 = qz.quantizeQ4(Tensor.initWithData((5,), [100, -100, 0, 50, -50]))
+    assert [q4.get(i) for i in range(3)] == [7, -7, 0]
+    assert abs(q4.scale - 100 / 7) < 1e-4
+    z4 = qz.quantizeQ4(Tensor.init((10,)))
+    assert z4.scale == 1.0 and not z4.data.any()
+    t = qz.quantizeQ8(Tensor.initWithData((3,), [127.0, 0.5, -0.5]))
+    assert t.data.tolist() == [127, 1, -1]
+
+
+# ------------------------------------------------------ weight-only matmuls
+Q8_CASES = [(1, 4096, 1024), (8, 4096, 1024), (128, 4096, 1024), (512, 4096, 1024),  # config 3
+            (3, 100, 50), (16, 96, 70), (4, 16, 32)]
+
+
+@pytest.mark.parametrize("m,n,k", Q8_CASES)
+def test_q8_vs_oracle(orc, m, n, k):
+    a = rnd(1001, m, k)
+    w = rnd(2002, k, n, 0.02)
+    q, s = orc.quantize_q8(w)
+    ref = orc.matmul_q8_mt(a, q, s, NT)
+    got = qz.matmulF32Q8Simd(T(a), qz.QuantizedTensorQ8(s, q, (k, n))).numpy()
+    err = rel_err(got, ref)
+    print(f"q8 {m}x{n}x{k}: rel {err:.3e}")
+    assert err <= Q_TOL
+
+
+Q4_CASES = [(1, 5120, 1280), (4, 5120, 1280), (8, 5120, 1280),   # config 4
+            (1, 1280, 5120), (4, 1280, 5120), (8, 1280, 5120),
+            (5, 33, 20), (40, 130, 64), (128, 5120, 1280)]
+
+
+@pytest.mark.parametrize("m,n,k", Q4_CASES)
+def test_q4_vs_oracle(orc, m, n, k):
+    a = rnd(1001, m, k)
+    w = rnd(2002, k, n, 0.02)
+    p, s = orc.quantize_q4(w)
+    ref = orc.matmul_q4_mt(a, p, k, n, s, NT)
+    got = qz.matmulF32Q4Simd(T(a), qz.QuantizedTensorQ4(s, p, (k, n))).numpy()
+    err = rel_err(got, ref)
+    print(f"q4 {m}x{n}x{k}: rel {err:.3e}")
+    assert err <= Q_TOL
+
+
+Q8K_CASES = [(1, 4096, 1024), (8, 512, 512), (16, 512, 512), (4, 32, 64), (130, 96, 40), (2, 33, 7)]
+
+
+@pytest.mark.parametrize("m,n,k", Q8K_CASES)
+def test_q8k_vs_oracle(orc, m, n, k):
+    a = rnd(1001, m, k)
+    w = rnd(2002, k, n, 0.02)
+    q, sc = orc.quantize_q8k(w)
+    ref = orc.matmul_q8k(a, q, sc, 32)
+    got = qz.matmulF32Q8KSimd(T(a), qz.QuantizedTensorQ8K(sc, q, (k, n))).numpy()
+    err = rel_err(got, ref)
+    print(f"q8k {m}x{n}x{k}: rel {err:.3e}")
+    assert err <= Q_TOL
+
+
+def test_q4_exact_integer_products(orc):
+    # Integer activations times int4 weights with scale 1: every partial sum
+    # is an integer below 2^24, so the GPU result must be exact.
+    rng = np.random.default_rng(3)
+    for m in (1, 4, 8, 33):
+        k, n = 256, 512
+        a = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
+        qv = rng.integers(-7, 8, size=k * n)
+        p = np.zeros((k * n + 1) // 2, np.uint8)
+        for i in range(0, k * n, 2):
+            p[i // 2] = (qv[i] & 0xF) | ((qv[i + 1] & 0xF) << 4)
+        got = np.zeros((m, n), np.float32)
+        _abi.sgemm_q4(m, n, k, a, p, 1.0, got)
+        np.testing.assert_array_equal(got, orc.matmul_q4(a, p, k, n, 1.0))
+
+
+def test_gemv_deterministic():
+    a = rnd(61, 1, 1024)
+    w = rnd(62, 1024, 4096, 0.02)
+    q = qz.quantizeQ8(Tensor.from_numpy(w))
+    r0 = qz.matmulF32Q8Simd(T(a), q).data.copy()
+    for _ in range(5):
+        np.testing.assert_array_equal(qz.matmulF32Q8Simd(T(a), q).data, r0)
+
+
+def test_registered_weight_path(orc):
+    a = rnd(71, 8, 512)
+    w = rnd(72, 512, 768, 0.02)
+    q, s = orc.quantize_q8(w)
+    c0 = np.zeros((8, 768), np.float32)
+    _abi.sgemm_q8(8, 768, 512, a, q, s, c0)
+    _abi.weight_register(q)
+    try:
+        c1 = np.zeros((8, 768), np.float32)
+        _abi.sgemm_q8(8, 768, 512, a, q, s, c1)
+        np.testing.assert_array_equal(c0, c1)
+    finally:
+        _abi.weight_release(q)

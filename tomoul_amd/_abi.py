@@ -1,0 +1,161 @@
+"""ctypes binding of include/tomoul_hip.h (libtomoul_hip.so).
+
+This is the Python-side counterpart of the Zig shim a Tomoul build would use
+(`extern "c"` declarations, the src/core/blas.zig:24-54 pattern).  Loading
+fails loudly when the library has not been built: there is no CPU fallback.
+Host-pointer calls take numpy arrays; "_dev" calls take raw device pointers
+(ints, e.g. torch's tensor.data_ptr()) and a hipStream_t as an int.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtomoul_hip.so")
+
+TML_OK = 0
+TML_ERR_INVALID_SHAPE = -1
+TML_ERR_SHAPE_MISMATCH = -2
+TML_ERR_OUT_OF_MEMORY = -3
+TML_ERR_INVALID_FORMAT = -4
+TML_ERR_INVALID_ARG = -5
+TML_ERR_NO_DEVICE = -6
+TML_ERR_HIP = -7
+
+FMT_F32, FMT_Q8_0, FMT_Q4_0, FMT_Q8_K = 0, 1, 2, 3
+
+# Every symbol the header declares, with its ctypes signature.
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_f = ctypes.c_float
+SIGNATURES = {
+    "tml_hip_init": (ctypes.c_int, []),
+    "tml_hip_shutdown": (None, []),
+    "tml_hip_last_error": (ctypes.c_char_p, []),
+    "tml_hip_device_name": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t]),
+    "tml_hip_sgemm": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _vp, _f, _f]),
+    "tml_hip_sgemm_bias": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "tml_hip_sgemv": (ctypes.c_int, [_i64, _i64, _vp, _vp, _vp, _f, _f]),
+    "tml_hip_sgemm_q8": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _f, _vp]),
+    "tml_hip_sgemm_q8k": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "tml_hip_sgemm_q4": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _f, _vp]),
+    "tml_hip_quantize": (ctypes.c_int, [ctypes.c_int, _i64, _vp, _vp, _vp]),
+    "tml_hip_weight_register": (ctypes.c_int, [_vp, ctypes.c_size_t]),
+    "tml_hip_weight_release": (ctypes.c_int, [_vp]),
+    "tml_hip_gemm_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp, _f, _f,
+                                        _vp]),
+    "tml_hip_quantize_dev": (ctypes.c_int, [ctypes.c_int, _i64, _vp, _vp, _vp, _vp]),
+}
+
+
+class TmlError(RuntimeError):
+    """A negative status from the C ABI; .code is the TML_ERR_* value."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"tomoul_hip error {code}: {msg}")
+        self.code = code
+
+
+class LibraryNotBuilt(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises LibraryNotBuilt if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryNotBuilt(f"{LIB_PATH} is missing; build it with `python -m tomoul_amd.build` "
+                              "(there is no CPU fallback)")
+    L = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def check(code: int) -> None:
+    if code != TML_OK:
+        msg = lib().tml_hip_last_error().decode(errors="replace")
+        raise TmlError(code, msg)
+
+
+def _ptr(a: np.ndarray | None) -> int | None:
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "arrays passed to the C ABI must be C-contiguous"
+    return a.ctypes.data
+
+
+def init() -> None:
+    check(lib().tml_hip_init())
+
+
+def shutdown() -> None:
+    lib().tml_hip_shutdown()
+
+
+def device_name() -> str:
+    buf = ctypes.create_string_buffer(256)
+    check(lib().tml_hip_device_name(buf, 256))
+    return buf.value.decode()
+
+
+# ------------------------------------------------------------- host pointers
+def sgemm(m: int, n: int, k: int, a: np.ndarray, b: np.ndarray, c: np.ndarray, alpha: float = 1.0,
+          beta: float = 0.0) -> None:
+    check(lib().tml_hip_sgemm(m, n, k, _ptr(a), _ptr(b), _ptr(c), alpha, beta))
+
+
+def sgemm_bias(m: int, n: int, k: int, a: np.ndarray, b: np.ndarray, bias: np.ndarray, c: np.ndarray) -> None:
+    check(lib().tml_hip_sgemm_bias(m, n, k, _ptr(a), _ptr(b), _ptr(bias), _ptr(c)))
+
+
+def sgemv(m: int, n: int, a: np.ndarray, x: np.ndarray, y: np.ndarray, alpha: float = 1.0,
+          beta: float = 0.0) -> None:
+    check(lib().tml_hip_sgemv(m, n, _ptr(a), _ptr(x), _ptr(y), alpha, beta))
+
+
+def sgemm_q8(m: int, n: int, k: int, a: np.ndarray, q: np.ndarray, scale: float, c: np.ndarray) -> None:
+    check(lib().tml_hip_sgemm_q8(m, n, k, _ptr(a), _ptr(q), scale, _ptr(c)))
+
+
+def sgemm_q8k(m: int, n: int, k: int, a: np.ndarray, q: np.ndarray, scales: np.ndarray, block: int,
+              c: np.ndarray) -> None:
+    check(lib().tml_hip_sgemm_q8k(m, n, k, _ptr(a), _ptr(q), _ptr(scales), block, _ptr(c)))
+
+
+def sgemm_q4(m: int, n: int, k: int, a: np.ndarray, packed: np.ndarray, scale: float, c: np.ndarray) -> None:
+    check(lib().tml_hip_sgemm_q4(m, n, k, _ptr(a), _ptr(packed), scale, _ptr(c)))
+
+
+def quantize(fmt: int, w: np.ndarray, q: np.ndarray, scales: np.ndarray) -> None:
+    check(lib().tml_hip_quantize(fmt, w.size, _ptr(w), _ptr(q), _ptr(scales)))
+
+
+def weight_register(a: np.ndarray) -> None:
+    check(lib().tml_hip_weight_register(_ptr(a), a.nbytes))
+
+
+def weight_release(a: np.ndarray) -> None:
+    check(lib().tml_hip_weight_release(_ptr(a)))
+
+
+# ----------------------------------------------------------- device pointers
+def gemm_dev(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr: int, *, scale: float = 1.0,
+             scales_ptr: int | None = None, block: int = 32, bias_ptr: int | None = None, alpha: float = 1.0,
+             beta: float = 0.0, stream: int | None = None) -> None:
+    check(lib().tml_hip_gemm_dev(fmt, m, n, k, a_ptr, b_ptr, scale, scales_ptr, block, bias_ptr, c_ptr, alpha,
+                                 beta, stream))
+
+
+def quantize_dev(fmt: int, n: int, w_ptr: int, q_ptr: int, scales_ptr: int, stream: int | None = None) -> None:
+    check(lib().tml_hip_quantize_dev(fmt, n, w_ptr, q_ptr, scales_ptr, stream))

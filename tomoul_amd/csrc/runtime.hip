@@ -1,0 +1,391 @@
+// runtime.hip -- the C ABI of include/tomoul_hip.h: argument validation,
+// per-device state (stream, staging buffers, split-K workspace, registered
+// weights) and routing to the kernel families:
+//   M <= 8            -> gemv.hip  (B streamed once, HBM-bound)
+//   M >  8            -> gemm_mfma.hip (LDS-tiled fp32 MFMA, compute-bound)
+// The host-pointer entry points wrap the device-pointer one: upload operands
+// (or reuse a registered weight), launch, download C, synchronise.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+
+#include "tml_internal.hpp"
+
+namespace tml {
+
+Status hip_status(hipError_t e, const char *what) {
+    const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? TML_ERR_OUT_OF_MEMORY
+                     : (e == hipErrorNoDevice || e == hipErrorInvalidDevice) ? TML_ERR_NO_DEVICE
+                                                                              : TML_ERR_HIP;
+    return Status::Err(code, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int env_int(const char *name, int dflt) {
+    const char *v = std::getenv(name);
+    if (v == nullptr || *v == '\0') return dflt;
+    return std::atoi(v);
+}
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int report(const Status &s) {
+    g_last_error = s.ok() ? std::string() : s.msg;
+    return s.code;
+}
+
+// A device allocation that only grows.
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    Status ensure(size_t n) {
+        if (n <= bytes) return Status::Ok();
+        if (p) {
+            TML_HIP_TRY(hipFree(p));
+            p = nullptr;
+            bytes = 0;
+        }
+        TML_HIP_TRY(hipMalloc(&p, n));
+        bytes = n;
+        return Status::Ok();
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+};
+
+struct Registered {
+    void *dev = nullptr;
+    size_t bytes = 0;
+};
+
+struct DeviceCtx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    DevBuf a, b, c, bias, scales, qtmp;  // staging of the host-pointer API
+    DevBuf ws, counters;                 // split-K workspace (gemv)
+    std::unordered_map<const void *, Registered> weights;
+};
+
+std::mutex g_mu;
+std::unordered_map<int, DeviceCtx *> g_ctx;
+
+Status current_ctx(DeviceCtx **out) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) return Status::Err(TML_ERR_NO_DEVICE, "no HIP device available");
+    int dev = 0;
+    TML_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_ctx.find(dev);
+    if (it != g_ctx.end()) {
+        *out = it->second;
+        return Status::Ok();
+    }
+    DeviceCtx *c = new DeviceCtx();
+    c->device = dev;
+    e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_status(e, "hipStreamCreateWithFlags");
+    }
+    g_ctx[dev] = c;
+    *out = c;
+    return Status::Ok();
+}
+
+// Grow the split-K workspace to what this problem needs; new counters are
+// zeroed (kernels leave them zero when they finish).
+Status ensure_workspace(DeviceCtx *c, const MatmulArgs &m, hipStream_t s, Workspace *ws) {
+    size_t pf = 0, nc = 0;
+    gemv_workspace_need(m, &pf, &nc);
+    if (pf > 0) {
+        TML_TRY(c->ws.ensure(pf * sizeof(float)));
+        if (c->counters.bytes < nc * sizeof(unsigned)) {
+            // The old counters may still be in use by queued kernels on
+            // another stream; finish all work on the device before growing.
+            TML_HIP_TRY(hipDeviceSynchronize());
+            TML_TRY(c->counters.ensure(nc * sizeof(unsigned)));
+            TML_HIP_TRY(hipMemsetAsync(c->counters.p, 0, c->counters.bytes, s));
+        }
+    }
+    ws->partials = (float *)c->ws.p;
+    ws->partial_floats = c->ws.bytes / sizeof(float);
+    ws->counters = (unsigned *)c->counters.p;
+    ws->counter_count = c->counters.bytes / sizeof(unsigned);
+    return Status::Ok();
+}
+
+bool valid_fmt(int fmt) {
+    return fmt == TML_FMT_F32 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0 || fmt == TML_FMT_Q8_K;
+}
+
+// Bytes of a K x N weight in format fmt.
+size_t weight_bytes(int fmt, int64_t K, int64_t N) {
+    const size_t e = (size_t)K * (size_t)N;
+    switch (fmt) {
+        case TML_FMT_F32: return e * 4;
+        case TML_FMT_Q4_0: return (e + 1) / 2;
+        default: return e;
+    }
+}
+
+Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B,
+                float scale, const float *scales, int64_t block, const float *bias, float *C, float alpha,
+                float beta, hipStream_t s) {
+    if (!valid_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
+    if (M < 0 || N < 0 || K < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
+    if (M == 0 || N == 0) return Status::Ok();
+    if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr)))
+        return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
+    if (fmt == TML_FMT_Q8_K && (block <= 0 || (K > 0 && scales == nullptr)))
+        return Status::Err(TML_ERR_INVALID_ARG, "Q8_K needs scales and a positive block size");
+    MatmulArgs m;
+    m.M = M; m.N = N; m.K = K;
+    m.A = A; m.B = B; m.scales = scales; m.block = fmt == TML_FMT_Q8_K ? block : 1;
+    m.bias = bias; m.C = C; m.beta = beta; m.fmt = fmt;
+    m.alpha_eff = (fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0) ? alpha * scale : alpha;
+    if (M <= kGemvMaxM) {
+        Workspace ws;
+        TML_TRY(ensure_workspace(c, m, s, &ws));
+        return launch_gemv(m, ws, s);
+    }
+    return launch_gemm_mfma(m, s);
+}
+
+// Resident copy of a registered host buffer of at least `bytes`, or null.
+const void *resident(DeviceCtx *c, const void *host, size_t bytes) {
+    auto it = c->weights.find(host);
+    if (it == c->weights.end() || it->second.bytes < bytes) return nullptr;
+    return it->second.dev;
+}
+
+Status upload(DeviceCtx *c, DevBuf &buf, const void *host, size_t bytes, const void **dev) {
+    if (bytes == 0) {
+        *dev = nullptr;
+        return Status::Ok();
+    }
+    if (const void *r = resident(c, host, bytes)) {
+        *dev = r;
+        return Status::Ok();
+    }
+    TML_TRY(buf.ensure(bytes));
+    TML_HIP_TRY(hipMemcpyAsync(buf.p, host, bytes, hipMemcpyHostToDevice, c->stream));
+    *dev = buf.p;
+    return Status::Ok();
+}
+
+// Host-pointer call: stage operands, run, copy C back, wait.
+Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                 const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta) {
+    if (!valid_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
+    if (M < 0 || N < 0 || K < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
+    if (M == 0 || N == 0) return Status::Ok();
+    if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr)))
+        return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
+    if (fmt == TML_FMT_Q8_K && (block <= 0 || (K > 0 && scales == nullptr)))
+        return Status::Err(TML_ERR_INVALID_ARG, "Q8_K needs scales and a positive block size");
+    DeviceCtx *c = nullptr;
+    TML_TRY(current_ctx(&c));
+    const void *dA = nullptr, *dB = nullptr, *dS = nullptr, *dBias = nullptr;
+    TML_TRY(upload(c, c->a, A, (size_t)M * K * sizeof(float), &dA));
+    TML_TRY(upload(c, c->b, B, weight_bytes(fmt, K, N), &dB));
+    if (fmt == TML_FMT_Q8_K && K > 0) {
+        const size_t ns = ((size_t)K * N + block - 1) / block;
+        TML_TRY(upload(c, c->scales, scales, ns * sizeof(float), &dS));
+    }
+    if (bias) TML_TRY(upload(c, c->bias, bias, (size_t)N * sizeof(float), &dBias));
+    const size_t cbytes = (size_t)M * N * sizeof(float);
+    TML_TRY(c->c.ensure(cbytes));
+    if (beta != 0.0f) TML_HIP_TRY(hipMemcpyAsync(c->c.p, C, cbytes, hipMemcpyHostToDevice, c->stream));
+    TML_TRY(gemm_dev(c, fmt, M, N, K, (const float *)dA, dB, scale, (const float *)dS, block,
+                     (const float *)dBias, (float *)c->c.p, alpha, beta, c->stream));
+    TML_HIP_TRY(hipMemcpyAsync(C, c->c.p, cbytes, hipMemcpyDeviceToHost, c->stream));
+    TML_HIP_TRY(hipStreamSynchronize(c->stream));
+    return Status::Ok();
+}
+
+Status quantize_dev(DeviceCtx *c, int fmt, int64_t n, const float *w, void *q, float *scales, hipStream_t s) {
+    if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K)
+        return Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0 or Q8_K");
+    if (n < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative element count");
+    if (scales == nullptr || (n > 0 && (w == nullptr || q == nullptr)))
+        return Status::Err(TML_ERR_INVALID_ARG, "null pointer");
+    if (n == 0) {
+        // The reference's all-zero rule: an empty Q8_0 / Q4_0 tensor gets
+        // scale 1 (max|v| == 0); Q8_K has no blocks.
+        if (fmt != TML_FMT_Q8_K) {
+            const float one = 1.0f;
+            TML_HIP_TRY(hipMemcpyAsync(scales, &one, sizeof one, hipMemcpyHostToDevice, s));
+            TML_HIP_TRY(hipStreamSynchronize(s));
+        }
+        return Status::Ok();
+    }
+    TML_TRY(c->qtmp.ensure(quantize_tmp_floats(fmt, n) * sizeof(float) + 16));
+    return launch_quantize(fmt, n, w, q, scales, (float *)c->qtmp.p, s);
+}
+
+}  // namespace
+}  // namespace tml
+
+using namespace tml;
+
+extern "C" {
+
+int tml_hip_init(void) {
+    DeviceCtx *c = nullptr;
+    return report(current_ctx(&c));
+}
+
+void tml_hip_shutdown(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (auto &kv : g_ctx) {
+        DeviceCtx *c = kv.second;
+        int prev = 0;
+        (void)hipGetDevice(&prev);
+        (void)hipSetDevice(c->device);
+        (void)hipDeviceSynchronize();
+        for (auto &w : c->weights) (void)hipFree(w.second.dev);
+        c->a.release(); c->b.release(); c->c.release(); c->bias.release();
+        c->scales.release(); c->qtmp.release(); c->ws.release(); c->counters.release();
+        if (c->stream) (void)hipStreamDestroy(c->stream);
+        (void)hipSetDevice(prev);
+        delete c;
+    }
+    g_ctx.clear();
+}
+
+const char *tml_hip_last_error(void) { return g_last_error.c_str(); }
+
+int tml_hip_device_name(char *buf, size_t len) {
+    if (buf == nullptr || len == 0) return report(Status::Err(TML_ERR_INVALID_ARG, "null buffer"));
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, c->device);
+    if (e != hipSuccess) return report(hip_status(e, "hipGetDeviceProperties"));
+    std::snprintf(buf, len, "%s", prop.name);
+    return report(Status::Ok());
+}
+
+int tml_hip_sgemm(int64_t M, int64_t N, int64_t K, const float *A, const float *B, float *C, float alpha,
+                  float beta) {
+    return report(host_gemm(TML_FMT_F32, M, N, K, A, B, 1.0f, nullptr, 0, nullptr, C, alpha, beta));
+}
+
+int tml_hip_sgemm_bias(int64_t M, int64_t N, int64_t K, const float *A, const float *B, const float *bias,
+                       float *C) {
+    if (bias == nullptr && M > 0 && N > 0) return report(Status::Err(TML_ERR_INVALID_ARG, "null bias"));
+    return report(host_gemm(TML_FMT_F32, M, N, K, A, B, 1.0f, nullptr, 0, bias, C, 1.0f, 0.0f));
+}
+
+int tml_hip_sgemv(int64_t M, int64_t N, const float *A, const float *x, float *y, float alpha, float beta) {
+    // y[M] = A[M,N] . x[N] is the GEMM C[M,1] = A[M,K=N] . B[K=N,1] with
+    // B = x read as an N x 1 row-major matrix (no copy or transpose needed).
+    return report(host_gemm(TML_FMT_F32, M, 1, N, A, x, 1.0f, nullptr, 0, nullptr, y, alpha, beta));
+}
+
+int tml_hip_sgemm_q8(int64_t M, int64_t N, int64_t K, const float *A, const int8_t *Bq, float scale, float *C) {
+    return report(host_gemm(TML_FMT_Q8_0, M, N, K, A, Bq, scale, nullptr, 0, nullptr, C, 1.0f, 0.0f));
+}
+
+int tml_hip_sgemm_q8k(int64_t M, int64_t N, int64_t K, const float *A, const int8_t *Bq, const float *scales,
+                      int64_t block, float *C) {
+    return report(host_gemm(TML_FMT_Q8_K, M, N, K, A, Bq, 1.0f, scales, block, nullptr, C, 1.0f, 0.0f));
+}
+
+int tml_hip_sgemm_q4(int64_t M, int64_t N, int64_t K, const float *A, const uint8_t *Bp, float scale, float *C) {
+    return report(host_gemm(TML_FMT_Q4_0, M, N, K, A, Bp, scale, nullptr, 0, nullptr, C, 1.0f, 0.0f));
+}
+
+int tml_hip_quantize(int fmt, int64_t n, const float *w, void *q, float *scales) {
+    if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K)
+        return report(Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0 or Q8_K"));
+    if (n < 0) return report(Status::Err(TML_ERR_INVALID_SHAPE, "negative element count"));
+    if (scales == nullptr || (n > 0 && (w == nullptr || q == nullptr)))
+        return report(Status::Err(TML_ERR_INVALID_ARG, "null pointer"));
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    const size_t qbytes = fmt == TML_FMT_Q4_0 ? (size_t)(n + 1) / 2 : (size_t)n;
+    const size_t nscales = fmt == TML_FMT_Q8_K ? (size_t)(n + 31) / 32 : 1;
+    auto run = [&]() -> Status {
+        TML_TRY(c->a.ensure((size_t)n * sizeof(float) + 16));
+        TML_TRY(c->b.ensure(qbytes + 16));
+        TML_TRY(c->scales.ensure(nscales * sizeof(float) + 16));
+        if (n > 0) TML_HIP_TRY(hipMemcpyAsync(c->a.p, w, (size_t)n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        TML_TRY(quantize_dev(c, fmt, n, (const float *)c->a.p, c->b.p, (float *)c->scales.p, c->stream));
+        if (qbytes > 0) TML_HIP_TRY(hipMemcpyAsync(q, c->b.p, qbytes, hipMemcpyDeviceToHost, c->stream));
+        if (fmt != TML_FMT_Q8_K || n > 0)
+            TML_HIP_TRY(hipMemcpyAsync(scales, c->scales.p, nscales * sizeof(float), hipMemcpyDeviceToHost,
+                                       c->stream));
+        TML_HIP_TRY(hipStreamSynchronize(c->stream));
+        return Status::Ok();
+    };
+    return report(run());
+}
+
+int tml_hip_weight_register(const void *host, size_t bytes) {
+    if (host == nullptr || bytes == 0) return report(Status::Err(TML_ERR_INVALID_ARG, "null or empty weight"));
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    auto run = [&]() -> Status {
+        auto it = c->weights.find(host);
+        if (it != c->weights.end() && it->second.bytes != bytes) {
+            TML_HIP_TRY(hipStreamSynchronize(c->stream));
+            TML_HIP_TRY(hipFree(it->second.dev));
+            c->weights.erase(it);
+            it = c->weights.end();
+        }
+        if (it == c->weights.end()) {
+            Registered r;
+            TML_HIP_TRY(hipMalloc(&r.dev, bytes));
+            r.bytes = bytes;
+            it = c->weights.emplace(host, r).first;
+        }
+        TML_HIP_TRY(hipMemcpyAsync(it->second.dev, host, bytes, hipMemcpyHostToDevice, c->stream));
+        TML_HIP_TRY(hipStreamSynchronize(c->stream));
+        return Status::Ok();
+    };
+    return report(run());
+}
+
+int tml_hip_weight_release(const void *host) {
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    auto it = c->weights.find(host);
+    if (it == c->weights.end()) return report(Status::Err(TML_ERR_INVALID_ARG, "weight not registered"));
+    auto run = [&]() -> Status {
+        TML_HIP_TRY(hipStreamSynchronize(c->stream));
+        TML_HIP_TRY(hipFree(it->second.dev));
+        c->weights.erase(it);
+        return Status::Ok();
+    };
+    return report(run());
+}
+
+int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                     const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
+                     void *stream) {
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    return report(gemm_dev(c, fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, (hipStream_t)stream));
+}
+
+int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream) {
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    return report(quantize_dev(c, fmt, n, w, q, scales, (hipStream_t)stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+// Internal declarations shared by the HIP translation units of libtomoul_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/tomoul_hip.h"
+
+namespace tml {
+
+// Status carrying a TML_ERR_* code and a message; ok() when code == TML_OK.
+struct Status {
+    int code = TML_OK;
+    std::string msg;
+    bool ok() const { return code == TML_OK; }
+    static Status Ok() { return {}; }
+    static Status Err(int c, std::string m) { return {c, std::move(m)}; }
+};
+
+Status hip_status(hipError_t e, const char *what);
+
+#define TML_HIP_TRY(expr)                                              \
+    do {                                                               \
+        hipError_t _e = (expr);                                        \
+        if (_e != hipSuccess) return ::tml::hip_status(_e, #expr);     \
+    } while (0)
+
+#define TML_TRY(expr)                                                  \
+    do {                                                               \
+        ::tml::Status _s = (expr);                                     \
+        if (!_s.ok()) return _s;                                       \
+    } while (0)
+
+// One GEMM / GEMV problem on device-resident operands:
+//   C = alpha_eff * (A . Bdeq) + beta * C + bias
+// where Bdeq is the f32 value of B's element (for Q8_0 / Q4_0 the integer
+// value; their per-tensor scale is folded into alpha_eff).
+struct MatmulArgs {
+    int64_t M, N, K;
+    const float *A;        // [M,K] row-major
+    const void *B;         // [K,N] row-major in format fmt
+    const float *scales;   // Q8_K block scales (device) or nullptr
+    int64_t block;         // Q8_K block size
+    const float *bias;     // [N] or nullptr
+    float *C;              // [M,N] row-major
+    float alpha_eff;       // alpha * per-tensor scale
+    float beta;
+    int fmt;
+};
+
+// Split-K workspace handed to kernels that reduce across workgroups.
+struct Workspace {
+    float *partials = nullptr;      // nsplit * M * N floats
+    size_t partial_floats = 0;
+    unsigned *counters = nullptr;   // one per output segment, zero between launches
+    size_t counter_count = 0;
+};
+
+// Kernel-family launchers (asynchronous).  Each validates that the problem
+// fits what its kernels assume before launching.
+Status launch_gemm_mfma(const MatmulArgs &a, hipStream_t s);
+Status launch_gemv(const MatmulArgs &a, const Workspace &ws, hipStream_t s);
+// Workspace needed by launch_gemv for this problem.
+void gemv_workspace_need(const MatmulArgs &a, size_t *partial_floats, size_t *counters);
+Status launch_quantize(int fmt, int64_t n, const float *w, void *q, float *scales, float *tmp_max,
+                       hipStream_t s);
+size_t quantize_tmp_floats(int fmt, int64_t n);
+
+// Largest M routed to the GEMV family (skinny decoder shapes).
+constexpr int64_t kGemvMaxM = 8;
+
+// Tuning overrides for experiments (0 = heuristic).  Read from the
+// TML_GEMM_TILE / TML_GEMV_SPLIT environment variables once.
+int env_int(const char *name, int dflt);
+
+}  // namespace tml

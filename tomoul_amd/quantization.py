@@ -1,0 +1,169 @@
+"""Weight-only quantized matmuls of src/core/quantization.zig on the GPU.
+
+Containers keep the reference's in-memory layouts ([K,N] row-major):
+  QuantizedTensorQ8   scale + int8 data          (quantization.zig:39-90)
+  QuantizedTensorQ8K  f32 scale per 32 flattened elements + int8 data
+                                                  (quantization.zig:327-403)
+  QuantizedTensorQ4   scale + packed nibbles, low nibble = even index
+                                                  (quantization.zig:627-711)
+quantizeQ8 / quantizeQ8K / quantizeQ4 run the bit-exact on-device quantizers;
+matmulF32Q8Simd / matmulF32Q8KSimd / matmulF32Q4Simd run the GPU GEMV (M <= 8)
+or MFMA GEMM (M > 8).  Errors mirror QuantError (quantization.zig:25-30).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import _abi
+from .tensor import Tensor
+
+BLOCK_SIZE = 32  # quantization.zig:322
+
+
+class QuantError(Exception):
+    pass
+
+
+class InvalidShape(QuantError):
+    pass
+
+
+class ShapeMismatch(QuantError):
+    pass
+
+
+QuantError.InvalidShape = InvalidShape
+QuantError.ShapeMismatch = ShapeMismatch
+
+
+def _numel(shape) -> int:
+    n = 1
+    for s in shape:
+        n *= int(s)
+    return n
+
+
+class QuantizedTensorQ8:
+    def __init__(self, scale: float, data: np.ndarray, shape):
+        self.scale = float(scale)
+        self.data = np.ascontiguousarray(data, dtype=np.int8).reshape(-1)
+        self.shape = tuple(int(s) for s in shape)
+
+    def numel(self) -> int:
+        return _numel(self.shape)
+
+    def sizeBytes(self) -> int:  # noqa: N802
+        return 4 + self.data.size
+
+    def compressionRatio(self) -> float:  # noqa: N802
+        return self.numel() * 4 / self.sizeBytes()
+
+
+class QuantizedTensorQ8K:
+    def __init__(self, scales: np.ndarray, data: np.ndarray, shape, block_size: int = BLOCK_SIZE):
+        self.scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+        self.data = np.ascontiguousarray(data, dtype=np.int8).reshape(-1)
+        self.shape = tuple(int(s) for s in shape)
+        self.block_size = int(block_size)
+        self.num_blocks = self.scales.size
+        self.element_count = _numel(self.shape)
+
+    def numel(self) -> int:
+        return self.element_count
+
+    def sizeBytes(self) -> int:  # noqa: N802
+        return self.scales.size * 4 + self.data.size
+
+    def compressionRatio(self) -> float:  # noqa: N802
+        return self.numel() * 4 / self.sizeBytes()
+
+
+class QuantizedTensorQ4:
+    def __init__(self, scale: float, data: np.ndarray, shape):
+        self.scale = float(scale)
+        self.data = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+        self.shape = tuple(int(s) for s in shape)
+        self.element_count = _numel(self.shape)
+
+    @classmethod
+    def init(cls, shape) -> "QuantizedTensorQ4":
+        n = _numel(shape)
+        return cls(0.0, np.zeros((n + 1) // 2, dtype=np.uint8), shape)
+
+    def numel(self) -> int:
+        return self.element_count
+
+    def sizeBytes(self) -> int:  # noqa: N802
+        return 4 + self.data.size
+
+    def compressionRatio(self) -> float:  # noqa: N802
+        return self.numel() * 4 / self.sizeBytes()
+
+    def get(self, idx: int) -> int:
+        """Nibble accessor (quantization.zig:682-695): two's-complement i4."""
+        b = int(self.data[idx // 2])
+        nib = (b & 0x0F) if idx % 2 == 0 else (b >> 4)
+        return nib - 16 if nib & 0x08 else nib
+
+    def set(self, idx: int, value: int) -> None:
+        """Nibble store, clamped to [-7, 7] (quantization.zig:698-710)."""
+        v = max(-7, min(7, int(value))) & 0x0F
+        i = idx // 2
+        b = int(self.data[i])
+        self.data[i] = (b & 0xF0) | v if idx % 2 == 0 else (b & 0x0F) | (v << 4)
+
+
+# ---------------------------------------------------------------- quantizers
+def quantizeQ8(t: Tensor) -> QuantizedTensorQ8:  # noqa: N802
+    q = np.empty(t.numel(), dtype=np.int8)
+    s = np.empty(1, dtype=np.float32)
+    _abi.quantize(_abi.FMT_Q8_0, t.data, q, s)
+    return QuantizedTensorQ8(float(s[0]), q, t.shape)
+
+
+def quantizeQ8K(t: Tensor) -> QuantizedTensorQ8K:  # noqa: N802
+    n = t.numel()
+    q = np.empty(n, dtype=np.int8)
+    s = np.empty(max((n + BLOCK_SIZE - 1) // BLOCK_SIZE, 1), dtype=np.float32)
+    _abi.quantize(_abi.FMT_Q8_K, t.data, q, s)
+    return QuantizedTensorQ8K(s[: (n + BLOCK_SIZE - 1) // BLOCK_SIZE], q, t.shape)
+
+
+def quantizeQ4(t: Tensor) -> QuantizedTensorQ4:  # noqa: N802
+    n = t.numel()
+    q = np.empty(max((n + 1) // 2, 1), dtype=np.uint8)
+    s = np.empty(1, dtype=np.float32)
+    _abi.quantize(_abi.FMT_Q4_0, t.data, q, s)
+    return QuantizedTensorQ4(float(s[0]), q[: (n + 1) // 2], t.shape)
+
+
+# ---------------------------------------------------------------- matmuls
+def _shape(a: Tensor, b):
+    if len(a.shape) != 2 or len(b.shape) != 2:
+        raise InvalidShape(f"matmul needs 2-D tensors, got {a.shape} and {b.shape}")
+    m, k = a.shape
+    kb, n = b.shape
+    if k != kb:
+        raise ShapeMismatch(f"inner dimensions differ: {a.shape} x {b.shape}")
+    return m, n, k
+
+
+def matmulF32Q8Simd(a: Tensor, b: QuantizedTensorQ8) -> Tensor:  # noqa: N802
+    m, n, k = _shape(a, b)
+    out = Tensor.init((m, n))
+    _abi.sgemm_q8(m, n, k, a.data, b.data, b.scale, out.data)
+    return out
+
+
+def matmulF32Q8KSimd(a: Tensor, b: QuantizedTensorQ8K) -> Tensor:  # noqa: N802
+    m, n, k = _shape(a, b)
+    out = Tensor.init((m, n))
+    _abi.sgemm_q8k(m, n, k, a.data, b.data, b.scales, b.block_size, out.data)
+    return out
+
+
+def matmulF32Q4Simd(a: Tensor, b: QuantizedTensorQ4) -> Tensor:  # noqa: N802
+    m, n, k = _shape(a, b)
+    out = Tensor.init((m, n))
+    _abi.sgemm_q4(m, n, k, a.data, b.data, b.scale, out.data)
+    return out
