@@ -2,33 +2,34 @@
 //
 //   C[M,N] = alpha * A[M,K] . Bdeq[K,N] + beta * C + bias[N]
 //
-// At M <= 8 the product is HBM-bound on B, so the kernel is built around
-// streaming B once with full-width loads:
+// At M <= 8 the product is bound by streaming B once from HBM; at the
+// decoder sizes (3-4 MB of weights) a launch is latency-bound, so the design
+// minimises dependent memory round trips:
 //   * B stays in its stored [K,N] layout (N contiguous; src/core/
-//     quantization.zig:193-197).  Each lane owns E consecutive columns and
-//     loads VB bytes of one row per instruction (VB = 16, 8 or 4); CL = 128/VB
-//     neighbouring lanes cover one 128-byte row segment, the other RL = 64/CL
-//     lane groups of the wave take other rows.  A workgroup (4 waves) owns
-//     one column segment and a range of rows ("split"); every lane issues all
-//     of its row loads before it touches any of them.
+//     quantization.zig:193-197).  A workgroup owns a column strip of CL*VB
+//     bytes of every row and walks all K rows of it: each lane loads VB
+//     bytes (16, 8 or 4) of one row per instruction, CL lanes span the strip
+//     and the 64/CL lane groups of each wave take different rows.  Rows are
+//     fetched in batches of U per lane, two batches in flight, with
+//     branch-free clamped addresses so the compiler keeps the batch's loads
+//     outstanding together; the activations of each row are fetched in the
+//     same batch.
 //   * Dequantization happens in registers (sign-extending bit-field
 //     extracts); Q8_0 / Q4_0 per-tensor scales are applied once in the
 //     epilogue, Q8_K block scales per row chunk.
-//   * A's rows of the split are staged in LDS as [k][m] so a lane fetches
-//     the M activations of its row with ds_read_b128.
-//   * Reduction: lane groups of a wave with __shfl_xor, the 4 waves through
-//     LDS, and the splits of a column segment through a workspace: every
-//     workgroup stores its partial, the last one to arrive (device-scope
-//     counter) sums the partials in split order and writes C, so results do
-//     not depend on scheduling.  The counter is reset by that workgroup.
+//   * Reduction over the rows of a strip: __shfl_xor across the lane groups
+//     of a wave, then the 4 waves through LDS.
+//   * Only when the output is too narrow to give enough strips is K split
+//     across workgroups; then wave 0 of each workgroup stores its partial,
+//     and the last workgroup of the strip to arrive (device-scope counter)
+//     sums the partials in split order and writes C, so results do not
+//     depend on scheduling.  That workgroup resets the counter.
 #include "tml_internal.hpp"
 
 namespace tml {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerBatch = 8;
-constexpr int kMaxStagedFloats = 8192;  // LDS budget of the staged A slice (32 KiB)
 
 struct GemvKArgs {
     int M, N, K;
@@ -60,25 +61,29 @@ __device__ __forceinline__ float sext4(uint32_t word, int nib) {
     return (float)((int32_t)(word << (28 - 4 * nib)) >> 28);
 }
 
-// Vector path: one VB-byte load per row (host guarantees N % E == 0 and
-// VB-byte alignment, so a chunk is either wholly inside B or past its end).
+// Vector path: one VB-byte load of row k at column n.  Branch-free: a chunk
+// past the end of the row (last segment, N % SC != 0) re-reads column 0 and
+// is zeroed, so every lane issues the same straight-line loads and the
+// compiler can keep a whole batch of them in flight.  Host guarantees
+// N % E == 0 and VB-byte alignment.
 template <int FMT, int VB>
 __device__ __forceinline__ void load_row(const GemvKArgs &a, int k, int n, Raw<VB> &r) {
-    const size_t e = (size_t)k * a.N + n;
     const bool in = n < a.N;
+    const size_t e = (size_t)k * a.N + (in ? n : 0);
     const void *p = FMT == TML_FMT_F32 ? (const void *)((const float *)a.B + e)
                   : FMT == TML_FMT_Q4_0 ? (const void *)((const uint8_t *)a.B + e / 2)
                                         : (const void *)((const int8_t *)a.B + e);
     if constexpr (VB == 16) {
-        uint4 v = in ? *(const uint4 *)p : make_uint4(0, 0, 0, 0);
-        r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+        const uint4 v = *(const uint4 *)p;
+        r.w[0] = in ? v.x : 0u; r.w[1] = in ? v.y : 0u; r.w[2] = in ? v.z : 0u; r.w[3] = in ? v.w : 0u;
     } else if constexpr (VB == 8) {
-        uint2 v = in ? *(const uint2 *)p : make_uint2(0, 0);
-        r.w[0] = v.x; r.w[1] = v.y;
+        const uint2 v = *(const uint2 *)p;
+        r.w[0] = in ? v.x : 0u; r.w[1] = in ? v.y : 0u;
     } else {
-        r.w[0] = in ? *(const uint32_t *)p : 0u;
+        const uint32_t v = *(const uint32_t *)p;
+        r.w[0] = in ? v : 0u;
     }
-    if constexpr (FMT == TML_FMT_Q8_K) r.s = in ? a.scales[e / a.block] : 0.0f;
+    if constexpr (FMT == TML_FMT_Q8_K) r.s = a.scales[e / a.block];
 }
 
 // Generic path: element-wise loads with bounds, any N and alignment; the
@@ -120,19 +125,14 @@ __device__ __forceinline__ void decode_row(const Raw<VB> &r, float *w) {
     }
 }
 
-template <int FMT, int MR, int VB, bool VEC>
+template <int FMT, int MR, int VB, int CL, int U, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
     constexpr int E = GemvFmt<FMT, VB>::E;
-    constexpr int CL = 128 / VB;       // column lanes per row segment
     constexpr int RL = 64 / CL;        // row lanes per wave
     constexpr int SC = CL * E;         // columns per segment
     constexpr int ROWSTEP = 4 * RL;    // rows per step of the workgroup
-    constexpr int U = kRowsPerBatch;   // rows per lane per batch
 
-    extern __shared__ __attribute__((aligned(16))) float smem[];
-    float *xs = smem;                  // [krows][MR]
-    float *red = smem;                 // reused after the main loop: [4][MR][SC]
-    __shared__ int s_last;
+    __shared__ __attribute__((aligned(16))) float red[4 * MR * SC];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -143,8 +143,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
     const int split = blockIdx.x / a.nseg;
     const int n = seg * SC + cl * E;
     const int k0 = split * a.krows;
-    const int k1 = min(a.K, k0 + a.krows);
-    const int nk = k1 - k0;
+    const int nk = min(a.K, k0 + a.krows) - k0;             // >= 1 (host)
     const int nb = (nk + U * ROWSTEP - 1) / (U * ROWSTEP);  // batches (uniform)
 
     float acc[MR][E];
@@ -153,74 +152,58 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[m][e] = 0.0f;
 
-    // Row kk (relative to k0) of batch b, slot u.
-    auto row_of = [&](int b, int u) { return R + (b * U + u) * ROWSTEP; };
-    auto load_batch = [&](Raw<VB> *raw, int b) {
+    // One batch = U rows per lane: B chunks plus the M activations of each
+    // row.  Rows past the split re-read row k0 and get zero activations.
+    Raw<VB> w0[U], w1[U];
+    float x0[U][MR], x1[U][MR];
+    auto load_batch = [&](Raw<VB> *w, float (*x)[MR], int b) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int kk = row_of(b, u);
-            if (kk < nk) load_row<FMT, VB>(a, k0 + kk, n, raw[u]);
-        }
-    };
-    auto compute_batch = [&](const Raw<VB> *raw, int b) {
+            const int kk = R + (b * U + u) * ROWSTEP;
+            const bool valid = kk < nk;
+            const int k = k0 + (valid ? kk : 0);
+            if constexpr (VEC) load_row<FMT, VB>(a, k, n, w[u]);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int kk = row_of(b, u);
-            if (kk < nk) {
-                float w[E];
-                if constexpr (VEC) decode_row<FMT, VB>(raw[u], w);
-                else load_elems<FMT, E>(a, k0 + kk, n, w);
-                float x[MR];
-                if constexpr (MR % 4 == 0) {
-#pragma unroll
-                    for (int m = 0; m < MR; m += 4) {
-                        const float4 t = *(const float4 *)&xs[kk * MR + m];
-                        x[m] = t.x; x[m + 1] = t.y; x[m + 2] = t.z; x[m + 3] = t.w;
-                    }
-                } else {
-#pragma unroll
-                    for (int m = 0; m < MR; ++m) x[m] = xs[kk * MR + m];
-                }
-#pragma unroll
-                for (int m = 0; m < MR; ++m)
-#pragma unroll
-                    for (int e = 0; e < E; ++e) acc[m][e] += x[m] * w[e];
+            for (int m = 0; m < MR; ++m) {
+                const bool ok = valid && m < a.M;
+                const float v = a.A[(size_t)(m < a.M ? m : 0) * a.K + k];
+                x[u][m] = ok ? v : 0.0f;
             }
         }
     };
+    auto compute_batch = [&](const Raw<VB> *w, const float (*x)[MR], int b) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float wv[E];
+            if constexpr (VEC) {
+                decode_row<FMT, VB>(w[u], wv);
+            } else {
+                const int kk = R + (b * U + u) * ROWSTEP;
+                load_elems<FMT, E>(a, k0 + (kk < nk ? kk : 0), n, wv);
+            }
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc[m][e] += x[u][m] * wv[e];
+        }
+    };
 
-    // 1. Issue the first batch of B loads, then stage A[:, k0:k1] in LDS
-    //    as [k][m] (zero for m >= M) while they are in flight.
-    Raw<VB> raw0[VEC ? U : 1], raw1[VEC ? U : 1];
-    if constexpr (VEC) load_batch(raw0, 0);
-    for (int i = tid; i < nk * MR; i += kThreads) {
-        const int kk = i / MR, m = i % MR;
-        xs[kk * MR + m] = m < a.M ? a.A[(size_t)m * a.K + k0 + kk] : 0.0f;
-    }
-    __syncthreads();
-
-    // 2. Stream B: two register batches in flight.
+    // Stream B with two batches in flight.
+    load_batch(w0, x0, 0);
     for (int b = 0; b < nb; b += 2) {
-        if constexpr (VEC) {
-            if (b + 1 < nb) load_batch(raw1, b + 1);
-        }
-        compute_batch(raw0, b);
-        if constexpr (VEC) {
-            if (b + 2 < nb) load_batch(raw0, b + 2);
-        }
-        if (b + 1 < nb) compute_batch(raw1, b + 1);
+        if (b + 1 < nb) load_batch(w1, x1, b + 1);
+        compute_batch(w0, x0, b);
+        if (b + 2 < nb) load_batch(w0, x0, b + 2);
+        if (b + 1 < nb) compute_batch(w1, x1, b + 1);
     }
 
-    // 3. Reduce over the RL row lanes of the wave.
+    // Reduce over the RL row lanes of the wave, then over the 4 waves.
 #pragma unroll
     for (int off = CL; off < 64; off <<= 1)
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
             for (int e = 0; e < E; ++e) acc[m][e] += __shfl_xor(acc[m][e], off);
-
-    // 4. Reduce over the 4 waves through LDS.
-    __syncthreads();  // xs is dead; reuse the space
     if (rl == 0) {
 #pragma unroll
         for (int m = 0; m < MR; ++m)
@@ -246,25 +229,26 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
         return;
     }
 
-    // 5. Split-K: publish this split's partial; the last workgroup of the
-    //    segment to arrive sums all partials in split order.
-    for (int o = tid; o < MR * SC; o += kThreads) {
+    // Split-K: wave 0 alone publishes this split's partial and, if this
+    // workgroup is the last of its segment to arrive, sums all partials in
+    // split order.  Its device-scope fence orders its own partial stores
+    // before its counter increment (release) and its partial loads after it
+    // (acquire), so one fence per workgroup suffices.
+    if (wave != 0) return;
+    for (int o = lane; o < MR * SC; o += 64) {
         const int m = o / SC, c = o % SC, col = col0 + c;
         if (m < a.M && col < a.N) {
             a.ws[((size_t)split * MR + m) * a.N + col] = red[m * SC + c] + red[(MR + m) * SC + c] +
                                                          red[(2 * MR + m) * SC + c] + red[(3 * MR + m) * SC + c];
         }
     }
-    __threadfence();  // release the partial at device scope
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counters + seg, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (unsigned)(a.nsplit - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();  // acquire every other split's partial
-    for (int o = tid; o < MR * SC; o += kThreads) {
+    __threadfence();
+    unsigned prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(a.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0);
+    if (prev != (unsigned)(a.nsplit - 1)) return;
+    __threadfence();
+    for (int o = lane; o < MR * SC; o += 64) {
         const int m = o / SC, c = o % SC, col = col0 + c;
         if (m < a.M && col < a.N) {
             const float *src = a.ws + (size_t)m * a.N + col;
@@ -279,15 +263,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
             *cp = v;
         }
     }
-    if (tid == 0) a.counters[seg] = 0u;  // ready for the next launch
+    if (lane == 0) a.counters[seg] = 0u;  // ready for the next launch
 }
 
 // ---------------------------------------------------------------- host side
 struct GemvPlan {
-    int mr, vb, e, sc, rowstep;
+    int mr, vb, e, cl, sc, rowstep;
     int nseg, nsplit, krows;
     bool vec;
-    size_t smem;
 };
 
 int pick_vb(int fmt, int mr) {
@@ -305,52 +288,75 @@ int elems_per_lane(int fmt, int vb) {
 
 bool is_aligned(const void *p, size_t n) { return ((uintptr_t)p % n) == 0; }
 
+// Bytes of B one workgroup should stream: enough to keep its CU's memory
+// pipeline full for one latency, small enough that the grid reaches many CUs.
+constexpr int64_t kBlockBytes = 64 << 10;
+constexpr int64_t kMinBlocks = 32;
+
 GemvPlan make_plan(const MatmulArgs &m) {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-    }
     GemvPlan p{};
     p.mr = m.M <= 1 ? 1 : m.M <= 2 ? 2 : m.M <= 4 ? 4 : 8;
     p.vb = pick_vb(m.fmt, p.mr);
     p.e = elems_per_lane(m.fmt, p.vb);
     p.vec = (m.N % p.e == 0) && is_aligned(m.B, (size_t)p.vb);
     if (m.fmt == TML_FMT_Q8_K) p.vec = p.vec && (m.block % p.e == 0);
-    const int cl = 128 / p.vb, rl = 64 / cl;
+    const int64_t block_bytes = env_int("TML_GEMV_BLOCK_KB", 0) > 0 ? (int64_t)env_int("TML_GEMV_BLOCK_KB", 0) << 10
+                                                                     : kBlockBytes;
+    // Column strip per workgroup: the widest strip (CL lanes of VB bytes)
+    // whose K rows fit the byte budget with enough strips to spread over
+    // the CUs; each workgroup then covers all of K and needs no reduction
+    // with other workgroups.
+    int cl = 1;
+    bool fits = false;
+    for (int c = 8; c >= 1; c >>= 1) {
+        const int64_t nseg = (m.N + (int64_t)c * p.e - 1) / ((int64_t)c * p.e);
+        if ((int64_t)c * p.vb * m.K <= block_bytes && nseg >= kMinBlocks) {
+            cl = c;
+            fits = true;
+            break;
+        }
+    }
+    const int forced_cl = env_int("TML_GEMV_CL", 0);
+    if (forced_cl == 1 || forced_cl == 2 || forced_cl == 4 || forced_cl == 8) cl = forced_cl;
+    p.cl = cl;
     p.sc = cl * p.e;
-    p.rowstep = 4 * rl;
+    p.rowstep = 4 * (64 / cl);
     p.nseg = (int)((m.N + p.sc - 1) / p.sc);
-    // Splits: enough workgroups to give every CU one (each streams its rows
-    // with two 8-row batches in flight per lane), never so few that the
-    // staged A slice outgrows its LDS budget, never less than one ROWSTEP of
-    // rows per split.  TML_GEMV_SPLIT forces a split count (experiments).
-    const int64_t max_split = m.K > p.rowstep ? m.K / p.rowstep : 1;
-    const int64_t min_split = (m.K * p.mr + kMaxStagedFloats - 1) / kMaxStagedFloats;
-    int64_t want = (cus + p.nseg - 1) / p.nseg;
+    // Narrow outputs (few strips): split K across workgroups as well.
+    int64_t nsplit = 1;
+    if (!fits) {
+        const int64_t per_strip = (int64_t)p.cl * p.vb * m.K;
+        nsplit = (per_strip + block_bytes - 1) / block_bytes;
+        const int64_t need = (kMinBlocks + p.nseg - 1) / p.nseg;
+        if (nsplit < need) nsplit = need;
+    }
     const int forced = env_int("TML_GEMV_SPLIT", 0);
-    if (forced > 0) want = forced;
-    int64_t nsplit = want < max_split ? want : max_split;
-    if (nsplit < min_split) nsplit = min_split;
+    if (forced > 0) nsplit = forced;
+    const int64_t max_split = m.K > p.rowstep ? m.K / p.rowstep : 1;
+    if (nsplit > max_split) nsplit = max_split;
     if (nsplit < 1) nsplit = 1;
     int64_t kr = (m.K + nsplit - 1) / nsplit;
     kr = ((kr + p.rowstep - 1) / p.rowstep) * p.rowstep;
-    if (kr * p.mr > kMaxStagedFloats) kr = (kMaxStagedFloats / p.mr / p.rowstep) * p.rowstep;
     if (kr < p.rowstep) kr = p.rowstep;
     p.krows = (int)kr;
-    p.nsplit = (int)((m.K + kr - 1) / kr);
-    if (m.K == 0) { p.krows = p.rowstep; p.nsplit = 1; }
-    const size_t xs = (size_t)p.krows * p.mr * sizeof(float);
-    const size_t red = (size_t)4 * p.mr * p.sc * sizeof(float);
-    p.smem = xs > red ? xs : red;
+    p.nsplit = m.K == 0 ? 1 : (int)((m.K + kr - 1) / kr);
     return p;
 }
 
-template <int FMT, int MR, int VB, bool VEC>
+template <int FMT, int MR, int VB, int CL, bool VEC>
 void launch_one(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
-    gemv_kernel<FMT, MR, VB, VEC><<<dim3((unsigned)(p.nseg * p.nsplit)), dim3(kThreads), p.smem, s>>>(ka);
+    constexpr int U = MR <= 2 ? 8 : 4;  // rows per lane per batch (register budget)
+    gemv_kernel<FMT, MR, VB, CL, U, VEC><<<dim3((unsigned)(p.nseg * p.nsplit)), dim3(kThreads), 0, s>>>(ka);
+}
+
+template <int FMT, int MR, int VB, bool VEC>
+void launch_cl(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
+    switch (p.cl) {
+        case 1: launch_one<FMT, MR, VB, 1, VEC>(ka, p, s); break;
+        case 2: launch_one<FMT, MR, VB, 2, VEC>(ka, p, s); break;
+        case 4: launch_one<FMT, MR, VB, 4, VEC>(ka, p, s); break;
+        default: launch_one<FMT, MR, VB, 8, VEC>(ka, p, s); break;
+    }
 }
 
 template <int FMT, int MR>
@@ -358,8 +364,8 @@ Status launch_mr(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
     constexpr int VB_VEC = FMT == TML_FMT_F32 ? 16
                          : (FMT == TML_FMT_Q4_0 ? (MR <= 2 ? 16 : (MR == 4 ? 8 : 4)) : (MR <= 4 ? 16 : 8));
     if (p.vb != VB_VEC) return Status::Err(TML_ERR_INVALID_ARG, "gemv plan/instantiation mismatch");
-    if (p.vec) launch_one<FMT, MR, VB_VEC, true>(ka, p, s);
-    else launch_one<FMT, MR, VB_VEC, false>(ka, p, s);
+    if (p.vec) launch_cl<FMT, MR, VB_VEC, true>(ka, p, s);
+    else launch_cl<FMT, MR, VB_VEC, false>(ka, p, s);
     TML_HIP_TRY(hipGetLastError());
     return Status::Ok();
 }
