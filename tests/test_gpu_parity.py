@@ -300,3 +300,47 @@ def test_registered_weight_path(orc):
         np.testing.assert_array_equal(c0, c1)
     finally:
         _abi.weight_release(q)
+
+
+# ------------------------------------------------------- forced kernel plans
+@pytest.fixture
+def forced_env():
+    saved = {k: os.environ.get(k) for k in ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE")}
+    yield os.environ
+    for k, v in saved.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = v
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("split", [1, 2, 3, 8])
+def test_sgemm_dma_tiles_and_splits(orc, forced_env, tile, split):
+    # Every tile config of the direct-copy kernel with K split 1-8 ways,
+    # on ragged shapes (M, N not multiples of the tile; K % 32 != 0).
+    forced_env["TML_GEMM_DMA_TILE"] = str(tile)
+    forced_env["TML_GEMM_SPLIT"] = str(split)
+    for (m, n, k) in [(300, 260, 516), (129, 68, 1028), (512, 1024, 1024)]:
+        a, b = rnd(81, m, k), rnd(82, k, n, 0.02)
+        bias = synth.normal(83, n, 0.0, 0.02)
+        got = ops.matmulBias(T(a), T(b), Tensor.from_numpy(bias)).numpy()
+        err = rel_err(got, orc.matmul_bias(a, b, bias))
+        assert err <= FP32_TOL, (m, n, k, err)
+
+
+def test_sgemm_split_deterministic(forced_env):
+    forced_env["TML_GEMM_SPLIT"] = "8"
+    a, b = rnd(91, 512, 4096), rnd(92, 4096, 1024, 0.02)
+    r0 = ops.matmul(T(a), T(b)).data.copy()
+    for _ in range(3):
+        np.testing.assert_array_equal(ops.matmul(T(a), T(b)).data, r0)
+
+
+def test_sgemm_register_staged_kernel(orc, forced_env):
+    # The register-staged kernel (used for quantized B) on fp32 as well.
+    forced_env["TML_GEMM_DMA"] = "0"
+    for tile in ("1", "2", "3", "4", "5", "6", "7"):
+        forced_env["TML_GEMM_TILE"] = tile
+        a, b = rnd(95, 200, 136), rnd(96, 136, 264, 0.02)
+        assert rel_err(ops.matmul(T(a), T(b)).numpy(), orc.matmul(a, b)) <= FP32_TOL, tile

@@ -1,0 +1,400 @@
+// gemm_dma.hip -- fp32 SGEMM on gfx950 matrix cores with direct global->LDS
+// loads (the ops.matmul / matmulBias path, src/core/ops.zig:235-471).
+//
+//   C[M,N] = alpha * A[M,K] . B[K,N] + beta * C + bias[N]
+//
+// Data path.  Each BK = 32 deep slice of the A and B tiles is copied from
+// HBM/L2 straight into LDS with global_load_lds_dwordx4 (no staging through
+// VGPRs, no ds_write instructions).  Three LDS stages: while the waves run the
+// MFMAs of slice t, the copies of slices t+1 and t+2 are in flight.  A wave's
+// copy instruction fills 1 KiB of LDS in lane order, so the tiles are stored
+// unpadded and bank conflicts are avoided with XOR swizzles instead:
+//   A stage [BM][BK]: 16-byte chunk q of row r sits in slot q ^ (r % 8), so the
+//     per-lane 16-byte fragment reads of 8 consecutive rows hit 8 distinct
+//     bank groups;
+//   B stage [BK][BN]: 16-byte chunk c of k-row k sits in slot c ^ 4 when
+//     (k / 4) is odd, so the lane groups reading rows k and k + 4 use opposite
+//     halves of the banks.
+// Synchronisation per slice: each wave waits for its own outstanding copies
+// of the next slice (s_waitcnt vmcnt with an exact count), then a raw
+// s_barrier makes every wave's copies visible.  __syncthreads() is not used in
+// the loop: its release fence would wait for all copies in flight
+// (vmcnt(0)) and serialise the pipeline.
+//
+// Compute: v_mfma_f32_16x16x4_f32, fp32 accumulation; lane l feeds A[l%16][kk]
+// and B[kk][l%16] with kk = l/16 and holds D[4*(l/16)+r][l%16] in register r;
+// within a 16-deep chunk, step s feeds the physical k = 4*kk + s.  Fragment
+// reads run one chunk ahead of the MFMAs, and the last chunk of a slice is
+// multiplied after the barrier so that it covers the first reads of the next.
+#include <type_traits>
+
+#include "tml_internal.hpp"
+
+namespace tml {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kNumXcd = 8;
+constexpr int kBK = kDmaBK;  // slice depth (two 16-deep MFMA chunks)
+
+struct DmaArgs {
+    int M, N, K;
+    const float *A;
+    const float *B;
+    const float *bias;
+    float *C;
+    float alpha, beta;
+    int tiles_m, tiles_n, group_m;
+    int nsplit, spl;      // K splits and BK-slices per split
+    float *ws;            // split partials: [split][M][N]
+    const float *zero;
+};
+
+#define TML_GPTR(p) ((__attribute__((address_space(1))) void *)(p))
+#define TML_LPTR(p) ((__attribute__((address_space(3))) void *)(p))
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() {
+    __builtin_amdgcn_s_waitcnt((0xF) | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));
+}
+// Workgroup barrier without a memory fence; the empty asm with a memory
+// clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void raw_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int BM, int BN, int WM, int WN, int NW, int NS>
+__global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
+    static_assert(NS == 3 || NS == 4, "3 or 4 LDS stages");
+    constexpr int BK = kBK;
+    constexpr int NC = BK / 16;
+    constexpr int WAVES_N = BN / WN;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    static_assert((BM / WM) * (BN / WN) == NW, "one wave per WM x WN sub-tile");
+    static_assert(NC == 2, "fragment double-buffering assumes two chunks per slice");
+    // 1 KiB copy blocks per stage and their shapes.
+    constexpr int SLOTS_A = BK / 4;             // 16-byte slots per A row (8)
+    constexpr int ROWS_A = 64 / SLOTS_A;        // A rows per copy block (8)
+    constexpr int BLKS_A = BM * BK / 256;       // copy blocks per A stage
+    constexpr int SLOTS_B = BN / 4;             // 16-byte slots per B k-row
+    constexpr int ROWS_B = 64 / SLOTS_B;        // B k-rows per copy block
+    constexpr int BLKS_B = BK * BN / 256;
+    static_assert(SLOTS_A == 8, "A swizzle assumes 8 slots per row");
+    static_assert(SLOTS_B >= 8 && 64 % SLOTS_B == 0, "B swizzle needs >= 8 slots per k-row");
+    static_assert(BLKS_A % NW == 0 && BLKS_B % NW == 0, "copy blocks must split evenly over the waves");
+    constexpr int LPW = BLKS_A / NW + BLKS_B / NW;  // copies per wave per slice
+
+    __shared__ __attribute__((aligned(1024))) float As0[BM * BK], As1[BM * BK], As2[BM * BK];
+    __shared__ __attribute__((aligned(1024))) float Bs0[BK * BN], Bs1[BK * BN], Bs2[BK * BN];
+    __shared__ __attribute__((aligned(1024))) float As3[NS > 3 ? BM * BK : 4], Bs3[NS > 3 ? BK * BN : 4];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm0 = (wave / WAVES_N) * WM;
+    const int wn0 = (wave % WAVES_N) * WN;
+
+    // XCD-aware remap of the workgroup id, then GROUP_M swizzle.
+    const int nblk = gridDim.x;
+    const int b = blockIdx.x;
+    const int per = nblk / kNumXcd, rem = nblk % kNumXcd;
+    const int xcd = b % kNumXcd, idx = b / kNumXcd;
+    const int lin = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    // The K splits of one tile are adjacent ids, so they run on one XCD.
+    const int split = lin % a.nsplit;
+    const int tlin = lin / a.nsplit;
+    const int group = a.group_m * a.tiles_n;
+    const int first_m = (tlin / group) * a.group_m;
+    const int gsize = min(a.tiles_m - first_m, a.group_m);
+    const int tile_m = first_m + (tlin % group) % gsize;
+    const int tile_n = (tlin % group) / gsize;
+    const int m0 = tile_m * BM;
+    const int n0 = tile_n * BN;
+
+    // ---- per-lane copy sources (fixed part), see the layout notes above
+    int a_row[BLKS_A / NW], a_col[BLKS_A / NW];
+#pragma unroll
+    for (int i = 0; i < BLKS_A / NW; ++i) {
+        const int blk = wave + i * NW;
+        const int row = blk * ROWS_A + lane / SLOTS_A;
+        const int q = (lane % SLOTS_A) ^ (row % 8);
+        a_row[i] = m0 + row;
+        a_col[i] = q * 4;
+    }
+    int b_row[BLKS_B / NW], b_col[BLKS_B / NW];
+#pragma unroll
+    for (int i = 0; i < BLKS_B / NW; ++i) {
+        const int blk = wave + i * NW;
+        const int krow = blk * ROWS_B + lane / SLOTS_B;
+        const int q = (lane % SLOTS_B) ^ (((krow >> 2) & 1) << 2);
+        b_row[i] = krow;
+        b_col[i] = n0 + q * 4;
+    }
+    auto issue = [&](float *as, float *bs, int k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < BLKS_A / NW; ++i) {
+            const int gk = k0 + a_col[i];
+            const bool in = a_row[i] < a.M && gk < a.K;
+            const float *src = in ? a.A + (size_t)a_row[i] * a.K + gk : a.zero;
+            __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(as + (wave + i * NW) * 256), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < BLKS_B / NW; ++i) {
+            const int gk = k0 + b_row[i];
+            const bool in = gk < a.K && b_col[i] < a.N;
+            const float *src = in ? a.B + (size_t)gk * a.N + b_col[i] : a.zero;
+            __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(bs + (wave + i * NW) * 256), 16, 0, 0);
+        }
+    };
+
+    // ---- fragments
+    struct Frag {
+        floatx4 a[TM];
+        float b[TN][4];
+    };
+    const int lrow = lane & 15;
+    const int g = lane >> 4;  // lane group: feeds kk = g
+    int a_off[TM];            // float offset of the lane's A row (chunk added per read)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a_off[i] = (wm0 + i * 16 + lrow) * BK;
+    int b_off[TN];            // swizzled float offset of the lane's B column within a k-row
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = wn0 + j * 16 + lrow;
+        b_off[j] = (((n >> 2) ^ ((g & 1) << 2)) << 2) + (n & 3);
+    }
+    const int aswz = lrow & 7;
+    auto read_frag = [&](Frag &f, const float *as, const float *bs, int chunk) __attribute__((always_inline)) {
+        const int q = chunk * 4 + g;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) f.a[i] = *(const floatx4 *)&as[a_off[i] + ((q ^ aswz) << 2)];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int k = chunk * 16 + g * 4 + s;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) f.b[j][s] = bs[k * BN + b_off[j]];
+        }
+    };
+
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](const Frag &f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i][s], f.b[j][s], acc[i][j], 0, 0, 0);
+    };
+
+    // Stage buffers are selected at compile time (stage S of a step is a
+    // template constant) so the compiler can tell which LDS array each copy
+    // writes and never waits for copies into other stages.
+    auto stage_a = [&](auto S) -> float * {
+        if constexpr (decltype(S)::value == 0) return As0;
+        else if constexpr (decltype(S)::value == 1) return As1;
+        else if constexpr (decltype(S)::value == 2) return As2;
+        else return As3;
+    };
+    auto stage_b = [&](auto S) -> float * {
+        if constexpr (decltype(S)::value == 0) return Bs0;
+        else if constexpr (decltype(S)::value == 1) return Bs1;
+        else if constexpr (decltype(S)::value == 2) return Bs2;
+        else return Bs3;
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+
+    // This workgroup's slices: [ks0, ks0 + nk) of the K dimension.
+    const int ks0 = split * a.spl;
+    const int nk = min((a.K + BK - 1) / BK - ks0, a.spl);
+    if (nk > 0) {
+        Frag f[2];
+        // Prologue: slices 0 .. NS-2 in flight, slice 0 landed.
+        issue(As0, Bs0, ks0 * BK);
+        issue(As1, Bs1, (ks0 + min(1, nk - 1)) * BK);
+        if constexpr (NS > 3) issue(As2, Bs2, (ks0 + min(2, nk - 1)) * BK);
+        wait_vmcnt<LPW * (NS - 2)>();  // own copies of slice 0 landed
+        raw_barrier();                  // everyone's copies of slice 0 landed
+        read_frag(f[0], As0, Bs0, 0);
+
+        // One slice: stage S holds slice kt; stage S-1 (mod NS, slice kt-1,
+        // fully read before the previous barrier) receives slice kt+NS-1.
+        // Slice indices past the end are clamped to the last slice (repeat
+        // copies into stages nobody reads again), and the MFMAs of steps past
+        // the end are skipped, so every step runs the same memory operations.
+        auto step = [&](int kt, auto S) __attribute__((always_inline)) {
+            constexpr int s = decltype(S)::value;
+            using SN = std::integral_constant<int, (s + 1) % NS>;
+            using SF = std::integral_constant<int, (s + NS - 1) % NS>;
+            const bool live = kt < nk;
+            issue(stage_a(SF{}), stage_b(SF{}), (ks0 + min(kt + NS - 1, nk - 1)) * BK);
+            read_frag(f[1], stage_a(S), stage_b(S), 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) mma(f[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<LPW * (NS - 2)>();  // own copies of slice kt+1 landed
+            wait_lgkmcnt0();               // own reads of slice kt done before anyone overwrites it
+            raw_barrier();
+            read_frag(f[0], stage_a(SN{}), stage_b(SN{}), 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) mma(f[1]);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        for (int kt = 0; kt < nk; kt += NS) {
+            step(kt, S0{});
+            step(kt + 1, S1{});
+            step(kt + 2, S2{});
+            if constexpr (NS > 3) step(kt + 3, S3{});
+        }
+        wait_vmcnt<0>();  // no copy may still be landing when the waves retire
+    }
+
+    const int rq = g * 4;
+    if (a.nsplit > 1) {
+        // Split-K: store the raw partial of this split into ws[split][M][N];
+        // splitk_reduce_kernel (launched next on the same stream) sums the
+        // splits in order and applies the epilogue.
+        float *part = a.ws + (size_t)split * a.M * a.N;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn0 + j * 16 + lrow;
+                if (col >= a.N) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wm0 + i * 16 + rq + r;
+                    if (row < a.M) part[(size_t)row * a.N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+
+    // Epilogue: C = alpha * acc + beta * C + bias, bounds-checked.
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn0 + j * 16 + lrow;
+            if (col >= a.N) continue;
+            const float bcol = a.bias ? a.bias[col] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm0 + i * 16 + rq + r;
+                if (row < a.M) {
+                    float *cp = a.C + (size_t)row * a.N + col;
+                    float v = a.alpha * acc[i][j][r];
+                    if (a.beta != 0.0f) v += a.beta * *cp;
+                    if (a.bias) v += bcol;
+                    *cp = v;
+                }
+            }
+        }
+}
+
+// C = alpha * sum_s ws[s] + beta * C + bias over the M*N outputs, the splits
+// summed in order (deterministic).  Four outputs per thread when aligned.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws, int nsplit, long long mn,
+                                                            int n, float *C, float alpha, float beta,
+                                                            const float *__restrict__ bias, bool vec) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    if (vec) {
+        for (long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x; q < mn / 4; q += stride) {
+            floatx4 acc = *(const floatx4 *)(ws + 4 * q);
+            for (int s = 1; s < nsplit; ++s) acc += *(const floatx4 *)(ws + (size_t)s * mn + 4 * q);
+            floatx4 v = alpha * acc;
+            float *cp = C + 4 * q;
+            if (beta != 0.0f) v += beta * *(const floatx4 *)cp;
+            if (bias) v += *(const floatx4 *)(bias + (4 * q) % n);
+            *(floatx4 *)cp = v;
+        }
+    } else {
+        for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < mn; e += stride) {
+            float acc = ws[e];
+            for (int s = 1; s < nsplit; ++s) acc += ws[(size_t)s * mn + e];
+            float v = alpha * acc;
+            if (beta != 0.0f) v += beta * C[e];
+            if (bias) v += bias[e % n];
+            C[e] = v;
+        }
+    }
+}
+
+struct DmaCfg {
+    int bm, bn;
+};
+constexpr DmaCfg kDmaCfgs[] = {{128, 128}, {128, 64}, {64, 64}, {256, 128}};
+
+}  // namespace
+
+int gemm_dma_num_cfgs() { return (int)(sizeof(kDmaCfgs) / sizeof(kDmaCfgs[0])); }
+
+void gemm_dma_tile(int cfg, int *bm, int *bn) {
+    *bm = kDmaCfgs[cfg].bm;
+    *bn = kDmaCfgs[cfg].bn;
+}
+
+bool gemm_dma_supported(const MatmulArgs &m) {
+    return m.fmt == TML_FMT_F32 && m.K % 4 == 0 && m.N % 4 == 0 && ((uintptr_t)m.A % 16) == 0 &&
+           ((uintptr_t)m.B % 16) == 0;
+}
+
+Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspace &ws, hipStream_t s) {
+    if (!gemm_dma_supported(m)) return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM needs f32, K%4 == N%4 == 0, aligned");
+    const int cfg = p.cfg;
+    if (cfg < 0 || cfg >= gemm_dma_num_cfgs()) return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
+    DmaArgs a;
+    a.M = (int)m.M; a.N = (int)m.N; a.K = (int)m.K;
+    a.A = m.A; a.B = (const float *)m.B; a.bias = m.bias; a.C = m.C;
+    a.alpha = m.alpha_eff; a.beta = m.beta;
+    a.zero = (const float *)m.zero;
+    const int bm = kDmaCfgs[cfg].bm, bn = kDmaCfgs[cfg].bn;
+    a.tiles_m = (int)((m.M + bm - 1) / bm);
+    a.tiles_n = (int)((m.N + bn - 1) / bn);
+    a.group_m = 4;
+    a.nsplit = p.nsplit;
+    a.spl = p.spl;
+    a.ws = ws.partials;
+    const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+    if (p.nsplit > 1 && (ws.partials == nullptr || ws.partial_floats < (size_t)p.nsplit * m.M * m.N))
+        return Status::Err(TML_ERR_INVALID_ARG, "GEMM split-K workspace too small");
+    if (p.spl < 1 || (int64_t)p.spl * p.nsplit < (m.K + kBK - 1) / kBK)
+        return Status::Err(TML_ERR_INVALID_ARG, "GEMM split plan does not cover K");
+    if (tiles * p.nsplit >= ((int64_t)1 << 31)) return Status::Err(TML_ERR_INVALID_SHAPE, "GEMM grid too large");
+    const dim3 grid((unsigned)(tiles * p.nsplit));
+    switch (cfg) {
+        case 0: gemm_f32_dma_kernel<128, 128, 64, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 1: gemm_f32_dma_kernel<128, 64, 32, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 2: gemm_f32_dma_kernel<64, 64, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 3: gemm_f32_dma_kernel<256, 128, 64, 64, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        default: return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
+    }
+    TML_HIP_TRY(hipGetLastError());
+    if (p.nsplit > 1) {
+        const int64_t n4 = (m.M * m.N + 3) / 4;
+        const int64_t blocks = (n4 + 255) / 256;
+        splitk_reduce_kernel<<<dim3((unsigned)(blocks < 65535 ? blocks : 65535)), 256, 0, s>>>(
+            ws.partials, p.nsplit, m.M * m.N, m.N, m.C, m.alpha_eff, m.beta, m.bias,
+            m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0));
+        TML_HIP_TRY(hipGetLastError());
+    }
+    return Status::Ok();
+}
+
+}  // namespace tml

@@ -32,8 +32,9 @@ namespace tml {
 namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uintx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uintx2 __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;
 constexpr int kNumXcd = 8;
 
 struct GemmKArgs {
@@ -47,6 +48,8 @@ struct GemmKArgs {
     float alpha;
     float beta;
     int tiles_m, tiles_n, group_m;
+    int xcd_remap;
+    const void *zero;
 };
 
 // ---------------------------------------------------------------- B formats
@@ -71,20 +74,22 @@ __device__ __forceinline__ float sext4(uint32_t word, int nib) {
     return (float)((int32_t)(word << (28 - 4 * nib)) >> 28);
 }
 
-// Vector-path chunk load at (k, n); caller guarantees n % EPC == 0.
+// Vector-path chunk load at (k, n); n % EPC == 0.  Branch-free: an out-of-
+// range chunk reads the zero block (its address is selected, not its value), so the
+// compiler keeps every load of a slice in flight together.
 template <int FMT>
 __device__ __forceinline__ void load_b_vec(const GemmKArgs &a, int k, int n, BRaw &r) {
     const bool in = (k < a.K) && (n < a.N);
-    const size_t e = (size_t)k * a.N + n;
+    const size_t e = (size_t)(in ? k : 0) * a.N + (in ? n : 0);
     if constexpr (FMT == TML_FMT_F32) {
-        uint4 v = in ? *(const uint4 *)((const float *)a.B + e) : make_uint4(0, 0, 0, 0);
-        r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+        const uintx4 v = *(const uintx4 *)(in ? (const void *)((const float *)a.B + e) : a.zero);
+        r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3];
     } else if constexpr (FMT == TML_FMT_Q8_0 || FMT == TML_FMT_Q8_K) {
-        uint2 v = in ? *(const uint2 *)((const int8_t *)a.B + e) : make_uint2(0, 0);
-        r.w[0] = v.x; r.w[1] = v.y;
-        if constexpr (FMT == TML_FMT_Q8_K) r.s = in ? a.scales[e / a.block] : 0.0f;
+        const uintx2 v = *(const uintx2 *)(in ? (const void *)((const int8_t *)a.B + e) : a.zero);
+        r.w[0] = v[0]; r.w[1] = v[1];
+        if constexpr (FMT == TML_FMT_Q8_K) r.s = a.scales[e / a.block];
     } else {  // Q4_0: 8 nibbles = 4 bytes starting at byte e/2 (e % 8 == 0)
-        r.w[0] = in ? *(const uint32_t *)((const uint8_t *)a.B + e / 2) : 0u;
+        r.w[0] = *(const uint32_t *)(in ? (const void *)((const uint8_t *)a.B + e / 2) : a.zero);
     }
 }
 
@@ -126,14 +131,16 @@ __device__ __forceinline__ void decode_b(const BRaw &r, float *out) {
 }
 
 // ---------------------------------------------------------------- kernel
-template <int FMT, int BM, int BN, int BK, int WM, int WN, bool VEC>
-__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmKArgs a) {
+template <int FMT, int BM, int BN, int BK, int WM, int WN, int NW, bool VEC>
+__global__ __launch_bounds__(NW * 64) void gemm_mfma_kernel(GemmKArgs a) {
+    constexpr int kThreads = NW * 64;
     constexpr int WAVES_N = BN / WN;
     constexpr int TM = WM / 16, TN = WN / 16;
+    constexpr int NC = BK / 16;  // 16-deep MFMA chunks per slice
     constexpr int EPC = BFmt<FMT>::EPC;
-    static_assert((BM / WM) * (BN / WN) == 4, "4 waves per workgroup");
-    static_assert(BK % 16 == 0 && WM % 16 == 0 && WN % 16 == 0, "MFMA granularity");
-    // A slice: float4 chunks; B slice: EPC-element chunks.
+    static_assert((BM / WM) * (BN / WN) == NW, "one wave per WM x WN sub-tile");
+    static_assert(WM % 16 == 0 && WN % 16 == 0, "MFMA granularity");
+    static_assert(NC % 2 == 0, "the pipeline below assumes an even number of chunks per slice");
     constexpr int A_CHUNKS = BM * BK / 4;
     constexpr int B_CHUNKS = BK * BN / EPC;
     constexpr int A_PER = (A_CHUNKS + kThreads - 1) / kThreads;
@@ -155,7 +162,8 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmKArgs a) {
     const int b = blockIdx.x;
     const int per = nblk / kNumXcd, rem = nblk % kNumXcd;
     const int xcd = b % kNumXcd, idx = b / kNumXcd;
-    const int lin = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int lin = !a.xcd_remap ? b
+                  : (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
     const int group = a.group_m * a.tiles_n;
     const int first_m = (lin / group) * a.group_m;
     const int gsize = min(a.tiles_m - first_m, a.group_m);
@@ -170,12 +178,13 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmKArgs a) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // Staging registers for the next slice.
-    float4 ra[A_PER];
-    BRaw rb[B_PER];
-    float rbe[VEC ? 1 : B_PER * EPC];  // generic path: already-decoded B
-
-    auto load_slice = [&](int k0) {
+    // ---- global -> registers -> LDS staging of one BK slice
+    struct Stage {
+        floatx4 a[A_PER];
+        BRaw b[VEC ? B_PER : 1];
+        float be[VEC ? 1 : B_PER * EPC];  // generic path: already decoded
+    };
+    auto load_slice = [&](Stage &st, int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < A_PER; ++i) {
             const int c = tid + i * kThreads;
@@ -183,14 +192,15 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmKArgs a) {
                 const int row = c / (BK / 4), kq = (c % (BK / 4)) * 4;
                 const int gm = m0 + row, gk = k0 + kq;
                 if constexpr (VEC) {
-                    ra[i] = (gm < a.M && gk < a.K) ? *(const float4 *)(a.A + (size_t)gm * a.K + gk)
-                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                    const bool in = gm < a.M && gk < a.K;
+                    st.a[i] = *(const floatx4 *)(in ? (const void *)(a.A + (size_t)gm * a.K + gk)
+                                                    : a.zero);
                 } else {
                     float t[4];
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
                         t[q] = (gm < a.M && gk + q < a.K) ? a.A[(size_t)gm * a.K + gk + q] : 0.0f;
-                    ra[i] = make_float4(t[0], t[1], t[2], t[3]);
+                    st.a[i] = floatx4{t[0], t[1], t[2], t[3]};
                 }
             }
         }
@@ -200,22 +210,21 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmKArgs a) {
             if (B_CHUNKS % kThreads == 0 || c < B_CHUNKS) {
                 const int kr = c / (BN / EPC), nc = (c % (BN / EPC)) * EPC;
                 if constexpr (VEC) {
-                    load_b_vec<FMT>(a, k0 + kr, n0 + nc, rb[i]);
+                    load_b_vec<FMT>(a, k0 + kr, n0 + nc, st.b[i]);
                 } else {
 #pragma unroll
-                    for (int q = 0; q < EPC; ++q) rbe[i * EPC + q] = load_b_elem<FMT>(a, k0 + kr, n0 + nc + q);
+                    for (int q = 0; q < EPC; ++q) st.be[i * EPC + q] = load_b_elem<FMT>(a, k0 + kr, n0 + nc + q);
                 }
             }
         }
     };
-
-    auto store_slice = [&](int buf) {
+    auto store_slice = [&](const Stage &st, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < A_PER; ++i) {
             const int c = tid + i * kThreads;
             if (A_CHUNKS % kThreads == 0 || c < A_CHUNKS) {
                 const int row = c / (BK / 4), kq = (c % (BK / 4)) * 4;
-                *(float4 *)&As[buf][row * LDA + kq] = ra[i];
+                *(floatx4 *)&As[buf][row * LDA + kq] = st.a[i];
             }
         }
 #pragma unroll
@@ -225,52 +234,91 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmKArgs a) {
                 const int kr = c / (BN / EPC), nc = (c % (BN / EPC)) * EPC;
                 float v[EPC];
                 if constexpr (VEC) {
-                    decode_b<FMT>(rb[i], v);
+                    decode_b<FMT>(st.b[i], v);
                 } else {
 #pragma unroll
-                    for (int q = 0; q < EPC; ++q) v[q] = rbe[i * EPC + q];
+                    for (int q = 0; q < EPC; ++q) v[q] = st.be[i * EPC + q];
                 }
 #pragma unroll
                 for (int q = 0; q < EPC; q += 4)
-                    *(float4 *)&Bs[buf][kr * LDB + nc + q] = make_float4(v[q], v[q + 1], v[q + 2], v[q + 3]);
+                    *(floatx4 *)&Bs[buf][kr * LDB + nc + q] = floatx4{v[q], v[q + 1], v[q + 2], v[q + 3]};
             }
         }
     };
 
-    const int nk = (a.K + BK - 1) / BK;
-    load_slice(0);
-    store_slice(0);
-    __syncthreads();
-
+    // ---- LDS -> register fragments of one 16-deep chunk, and its MFMAs
+    struct Frag {
+        floatx4 a[TM];
+        float b[TN][4];
+    };
     const int lrow = lane & 15;
     const int lk = (lane >> 4) * 4;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) load_slice((kt + 1) * BK);
-        const float *as = As[cur];
-        const float *bs = Bs[cur];
+    auto read_frag = [&](Frag &f, int buf, int chunk) __attribute__((always_inline)) {
+        const float *as = As[buf];
+        const float *bs = Bs[buf];
+        const int kc = chunk * 16;
 #pragma unroll
-        for (int kc = 0; kc < BK; kc += 16) {
-            float4 av[TM];
-            float bv[TN][4];
+        for (int i = 0; i < TM; ++i) f.a[i] = *(const floatx4 *)&as[(wm0 + i * 16 + lrow) * LDA + kc + lk];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) av[i] = *(const float4 *)&as[(wm0 + i * 16 + lrow) * LDA + kc + lk];
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+            for (int s = 0; s < 4; ++s) f.b[j][s] = bs[(kc + lk + s) * LDB + wn0 + j * 16 + lrow];
+    };
+    auto mma = [&](const Frag &f) __attribute__((always_inline)) {
 #pragma unroll
-                for (int s = 0; s < 4; ++s) bv[j][s] = bs[(kc + lk + s) * LDB + wn0 + j * 16 + lrow];
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+            for (int i = 0; i < TM; ++i) {
+                const float av = f.a[i][s];
 #pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const float as_ = s == 0 ? av[i].x : s == 1 ? av[i].y : s == 2 ? av[i].z : av[i].w;
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(as_, bv[j][s], acc[i][j], 0, 0, 0);
-                }
-        }
-        if (kt + 1 < nk) store_slice(cur ^ 1);
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
+            }
+    };
+
+    // ---- pipeline
+    // Global loads run two slices ahead of the MFMAs (two register stages),
+    // LDS holds two slices, and fragment reads run one chunk ahead; the last
+    // chunk's MFMAs of a slice are issued after the barrier so that they
+    // cover the first fragment reads of the next slice.
+    // Every step below is unconditional (a slice index past the end is
+    // clamped to the last slice and its loads/stores are harmless repeats),
+    // so the loop body is straight-line code with uniform branches only.
+    const int nk = (a.K + BK - 1) / BK;
+    if (nk > 0) {
+        Stage s0, s1;
+        Frag f[2];
+        load_slice(s0, 0);
+        store_slice(s0, 0);
+        load_slice(s1, min(1, nk - 1) * BK);
         __syncthreads();
+        read_frag(f[0], 0, 0);
+
+        // sched_barrier(0) fences keep the compiler from sinking the next
+        // chunk's LDS reads down to their first use: every read of chunk c+1
+        // is issued before the MFMAs of chunk c, so its latency is covered.
+        auto step = [&](int kt, Stage &sl, const Stage &ss, int cur) __attribute__((always_inline)) {
+            load_slice(sl, min(kt + 2, nk - 1) * BK);  // sl's slice kt is already in LDS
+#pragma unroll
+            for (int c = 0; c + 1 < NC; ++c) {
+                read_frag(f[(c + 1) & 1], cur, c + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                mma(f[c & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            store_slice(ss, cur ^ 1);  // slice kt + 1
+            __syncthreads();
+            read_frag(f[0], cur ^ 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(f[1]);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        int kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            step(kt, s0, s1, 0);
+            step(kt + 1, s1, s0, 1);
+        }
+        if (kt < nk) step(kt, s0, s1, 0);
     }
 
     // Epilogue: C = alpha * acc + beta * C + bias, bounds-checked.
@@ -308,23 +356,32 @@ constexpr TileCfg kCfgs[] = {
     {64, 128, 0.92f},
     {64, 64, 0.85f},
     {32, 64, 0.60f},
+    {256, 128, 1.00f},
+    {128, 128, 0.80f},
+    {128, 128, 0.0f},  // experiments only (eff 0: never picked)
+    {128, 64, 0.0f},
+    {64, 64, 0.0f},
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int FMT, bool VEC>
 Status launch_cfg(int cfg, const GemmKArgs &ka, hipStream_t s) {
-    dim3 block(kThreads);
     auto grid_of = [&](int bm, int bn) { return dim3((unsigned)(((ka.M + bm - 1) / bm) * ((ka.N + bn - 1) / bn))); };
     if constexpr (!VEC) {
         // The generic (unaligned) path is instantiated for one tile shape.
-        gemm_mfma_kernel<FMT, 64, 64, 32, 32, 32, false><<<grid_of(64, 64), block, 0, s>>>(ka);
+        gemm_mfma_kernel<FMT, 64, 64, 32, 32, 32, 4, false><<<grid_of(64, 64), 256, 0, s>>>(ka);
     } else {
         switch (cfg) {
-        case 0: gemm_mfma_kernel<FMT, 128, 128, 16, 64, 64, VEC><<<grid_of(128, 128), block, 0, s>>>(ka); break;
-        case 1: gemm_mfma_kernel<FMT, 128, 64, 16, 64, 32, VEC><<<grid_of(128, 64), block, 0, s>>>(ka); break;
-        case 2: gemm_mfma_kernel<FMT, 64, 128, 16, 32, 64, VEC><<<grid_of(64, 128), block, 0, s>>>(ka); break;
-        case 3: gemm_mfma_kernel<FMT, 64, 64, 32, 32, 32, VEC><<<grid_of(64, 64), block, 0, s>>>(ka); break;
-        case 4: gemm_mfma_kernel<FMT, 32, 64, 32, 16, 32, VEC><<<grid_of(32, 64), block, 0, s>>>(ka); break;
+        case 0: gemm_mfma_kernel<FMT, 128, 128, 32, 64, 32, 8, VEC><<<grid_of(128, 128), 512, 0, s>>>(ka); break;
+        case 1: gemm_mfma_kernel<FMT, 128, 64, 32, 32, 32, 8, VEC><<<grid_of(128, 64), 512, 0, s>>>(ka); break;
+        case 2: gemm_mfma_kernel<FMT, 64, 128, 32, 32, 32, 8, VEC><<<grid_of(64, 128), 512, 0, s>>>(ka); break;
+        case 3: gemm_mfma_kernel<FMT, 64, 64, 32, 32, 32, 4, VEC><<<grid_of(64, 64), 256, 0, s>>>(ka); break;
+        case 4: gemm_mfma_kernel<FMT, 32, 64, 32, 16, 32, 4, VEC><<<grid_of(32, 64), 256, 0, s>>>(ka); break;
+        case 5: gemm_mfma_kernel<FMT, 256, 128, 32, 64, 64, 8, VEC><<<grid_of(256, 128), 512, 0, s>>>(ka); break;
+        case 6: gemm_mfma_kernel<FMT, 128, 128, 32, 64, 64, 4, VEC><<<grid_of(128, 128), 256, 0, s>>>(ka); break;
+        case 7: gemm_mfma_kernel<FMT, 128, 128, 64, 64, 32, 8, VEC><<<grid_of(128, 128), 512, 0, s>>>(ka); break;
+        case 8: gemm_mfma_kernel<FMT, 128, 64, 64, 32, 32, 8, VEC><<<grid_of(128, 64), 512, 0, s>>>(ka); break;
+        case 9: gemm_mfma_kernel<FMT, 64, 64, 64, 32, 32, 4, VEC><<<grid_of(64, 64), 256, 0, s>>>(ka); break;
         default: return Status::Err(TML_ERR_INVALID_ARG, "bad GEMM tile config");
         }
     }
@@ -340,6 +397,7 @@ int pick_cfg(int64_t M, int64_t N, int cus) {
     for (int c = 0; c < kNumCfgs; ++c) {
         const int64_t tiles = ((M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((N + kCfgs[c].bn - 1) / kCfgs[c].bn);
         const int64_t rounds = (tiles + cus - 1) / cus;
+        if (kCfgs[c].eff <= 0.0f) continue;
         const double t = (double)rounds * kCfgs[c].bm * kCfgs[c].bn / kCfgs[c].eff;
         if (t < best_t) {
             best_t = t;
@@ -347,6 +405,61 @@ int pick_cfg(int64_t M, int64_t N, int cus) {
         }
     }
     return best;
+}
+
+int device_cus() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
+// Direct-copy fp32 kernel: pick (tile, K splits) with the smallest modelled
+// time = rounds of workgroups over the CUs (a CU holds per_cu workgroups of
+// a tile at once) x (slices per split + fixed cost) x tile area / efficiency.
+// The fixed cost covers pipeline fill, epilogue and, with splits, the
+// partial-tile exchange.
+void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
+    static const float eff[] = {1.00f, 0.92f, 0.80f, 1.05f};
+    static const int per_cu[] = {1, 2, 3, 1};
+    static const int splits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    const int cus = device_cus();
+    const int64_t nk = (K + kDmaBK - 1) / kDmaBK;
+    const int forced_tile = env_int("TML_GEMM_DMA_TILE", 0) - 1;
+    const int forced_split = env_int("TML_GEMM_SPLIT", 0);
+    double best_t = 1e300;
+    for (int c = 0; c < gemm_dma_num_cfgs(); ++c) {
+        if (forced_tile >= 0 && c != forced_tile) continue;
+        int bm = 0, bn = 0;
+        gemm_dma_tile(c, &bm, &bn);
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        for (int sp : splits) {
+            if (forced_split > 0 && sp != forced_split) continue;
+            if (sp > 1 && nk < 2 * sp) continue;
+            const int64_t spl = nk > 0 ? (nk + sp - 1) / sp : 1;
+            const int64_t real = nk > 0 ? (nk + spl - 1) / spl : 1;
+            const int64_t units = tiles * real;
+            const int64_t slots = (int64_t)cus * per_cu[c];
+            const int64_t rounds = (units + slots - 1) / slots;
+            // fill/epilogue ~2 slices; splits add a reduce launch (~2.5 us
+            // of launch gap plus streaming the partials), ~6 slices.
+            const double fixed = 2.0 + (real > 1 ? 6.0 : 0.0);
+            const double t = (double)rounds * ((double)spl + fixed) * bm * bn * per_cu[c] / eff[c];
+            if (t < best_t) {
+                best_t = t;
+                p->cfg = c;
+                p->nsplit = (int)real;
+                p->spl = (int)spl;
+                p->tiles = (int)tiles;
+            }
+        }
+    }
 }
 
 bool aligned(const void *p, size_t n) { return ((uintptr_t)p % n) == 0; }
@@ -357,6 +470,7 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
     ka.M = (int)m.M; ka.N = (int)m.N; ka.K = (int)m.K;
     ka.A = m.A; ka.B = m.B; ka.scales = m.scales; ka.block = m.block;
     ka.bias = m.bias; ka.C = m.C; ka.alpha = m.alpha_eff; ka.beta = m.beta;
+    ka.zero = m.zero;
     int cfg = env_int("TML_GEMM_TILE", 0) - 1;
     if (cfg < 0 || cfg >= kNumCfgs) cfg = pick_cfg(m.M, m.N, cus);
     constexpr int EPC = BFmt<FMT>::EPC;
@@ -367,24 +481,39 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
     const int bm = kCfgs[cfg].bm, bn = kCfgs[cfg].bn;
     ka.tiles_m = (int)((m.M + bm - 1) / bm);
     ka.tiles_n = (int)((m.N + bn - 1) / bn);
-    ka.group_m = 4;
+    ka.group_m = env_int("TML_GEMM_GROUPM", 4);
+    if (ka.group_m < 1) ka.group_m = 1;
+    ka.xcd_remap = env_int("TML_GEMM_XCD", 1);
     return vec ? launch_cfg<FMT, true>(cfg, ka, s) : launch_cfg<FMT, false>(3, ka, s);
 }
 
 }  // namespace
 
-Status launch_gemm_mfma(const MatmulArgs &m, hipStream_t s) {
-    // Index math in the kernel is 32-bit for dimensions and 64-bit for
+GemmPlan plan_gemm(const MatmulArgs &m) {
+    GemmPlan p;
+    if (m.fmt == TML_FMT_F32 && env_int("TML_GEMM_DMA", 1) != 0 && gemm_dma_supported(m) && m.K > 0) {
+        p.dma = true;
+        pick_dma(m.M, m.N, m.K, &p);
+    }
+    return p;
+}
+
+void gemm_workspace_need(const MatmulArgs &m, size_t *partial_floats, size_t *counters) {
+    const GemmPlan p = plan_gemm(m);
+    *partial_floats = 0;
+    *counters = 0;
+    if (p.dma && p.nsplit > 1) *partial_floats = (size_t)p.nsplit * m.M * m.N;
+}
+
+Status launch_gemm_mfma(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
+    // Index math in the kernels is 32-bit for dimensions and 64-bit for
     // element offsets; grids are 1-D.
     const int64_t lim = (int64_t)1 << 30;
     if (m.M >= lim || m.N >= lim || m.K >= lim)
         return Status::Err(TML_ERR_INVALID_SHAPE, "GEMM dimension exceeds 2^30");
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0;
-        TML_HIP_TRY(hipGetDevice(&dev));
-        TML_HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    }
+    const GemmPlan p = plan_gemm(m);
+    if (p.dma) return launch_gemm_f32_dma(m, p, ws, s);
+    const int cus = device_cus();
     switch (m.fmt) {
         case TML_FMT_F32: return launch_fmt<TML_FMT_F32>(m, s, cus);
         case TML_FMT_Q8_0: return launch_fmt<TML_FMT_Q8_0>(m, s, cus);

@@ -30,6 +30,8 @@ namespace tml {
 namespace {
 
 constexpr int kThreads = 256;
+typedef uint32_t uintx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uintx2 __attribute__((ext_vector_type(2)));
 
 struct GemvKArgs {
     int M, N, K;
@@ -43,6 +45,7 @@ struct GemvKArgs {
     int nseg, nsplit, krows;  // krows = rows per split
     float *ws;
     unsigned *counters;
+    const void *zero;
 };
 
 template <int FMT, int VB> struct GemvFmt;
@@ -62,26 +65,26 @@ __device__ __forceinline__ float sext4(uint32_t word, int nib) {
 }
 
 // Vector path: one VB-byte load of row k at column n.  Branch-free: a chunk
-// past the end of the row (last segment, N % SC != 0) re-reads column 0 and
-// is zeroed, so every lane issues the same straight-line loads and the
-// compiler can keep a whole batch of them in flight.  Host guarantees
-// N % E == 0 and VB-byte alignment.
+// past the end of the row (last strip, N % SC != 0) reads the zero block (the
+// address is selected, not the value), so every lane issues the same
+// straight-line loads and the compiler keeps a whole batch in flight.  Host
+// guarantees N % E == 0 and VB-byte alignment.
 template <int FMT, int VB>
 __device__ __forceinline__ void load_row(const GemvKArgs &a, int k, int n, Raw<VB> &r) {
     const bool in = n < a.N;
     const size_t e = (size_t)k * a.N + (in ? n : 0);
-    const void *p = FMT == TML_FMT_F32 ? (const void *)((const float *)a.B + e)
+    const void *p = !in ? a.zero
+                  : FMT == TML_FMT_F32 ? (const void *)((const float *)a.B + e)
                   : FMT == TML_FMT_Q4_0 ? (const void *)((const uint8_t *)a.B + e / 2)
                                         : (const void *)((const int8_t *)a.B + e);
     if constexpr (VB == 16) {
-        const uint4 v = *(const uint4 *)p;
-        r.w[0] = in ? v.x : 0u; r.w[1] = in ? v.y : 0u; r.w[2] = in ? v.z : 0u; r.w[3] = in ? v.w : 0u;
+        const uintx4 v = *(const uintx4 *)p;
+        r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3];
     } else if constexpr (VB == 8) {
-        const uint2 v = *(const uint2 *)p;
-        r.w[0] = in ? v.x : 0u; r.w[1] = in ? v.y : 0u;
+        const uintx2 v = *(const uintx2 *)p;
+        r.w[0] = v[0]; r.w[1] = v[1];
     } else {
-        const uint32_t v = *(const uint32_t *)p;
-        r.w[0] = in ? v : 0u;
+        r.w[0] = *(const uint32_t *)p;
     }
     if constexpr (FMT == TML_FMT_Q8_K) r.s = a.scales[e / a.block];
 }
@@ -166,8 +169,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 const bool ok = valid && m < a.M;
-                const float v = a.A[(size_t)(m < a.M ? m : 0) * a.K + k];
-                x[u][m] = ok ? v : 0.0f;
+                x[u][m] = *(ok ? a.A + (size_t)m * a.K + k : (const float *)a.zero);
             }
         }
     };
@@ -408,6 +410,7 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     ka.bias = m.bias; ka.C = m.C; ka.alpha = m.alpha_eff; ka.beta = m.beta;
     ka.nseg = p.nseg; ka.nsplit = p.nsplit; ka.krows = p.krows;
     ka.ws = ws.partials; ka.counters = ws.counters;
+    ka.zero = m.zero;
     switch (m.fmt) {
         case TML_FMT_F32: return launch_fmt<TML_FMT_F32>(ka, p, s);
         case TML_FMT_Q8_0: return launch_fmt<TML_FMT_Q8_0>(ka, p, s);

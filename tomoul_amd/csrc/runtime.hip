@@ -68,7 +68,8 @@ struct DeviceCtx {
     int device = -1;
     hipStream_t stream = nullptr;
     DevBuf a, b, c, bias, scales, qtmp;  // staging of the host-pointer API
-    DevBuf ws, counters;                 // split-K workspace (gemv)
+    DevBuf ws, counters;                 // split-K workspace (gemv, gemm)
+    DevBuf zero;                         // kZeroBlockBytes of zeros
     std::unordered_map<const void *, Registered> weights;
 };
 
@@ -94,6 +95,17 @@ Status current_ctx(DeviceCtx **out) {
         delete c;
         return hip_status(e, "hipStreamCreateWithFlags");
     }
+    Status zs = c->zero.ensure(kZeroBlockBytes);
+    if (zs.ok()) {
+        e = hipMemset(c->zero.p, 0, kZeroBlockBytes);
+        if (e != hipSuccess) zs = hip_status(e, "hipMemset");
+    }
+    if (!zs.ok()) {
+        (void)hipStreamDestroy(c->stream);
+        c->zero.release();
+        delete c;
+        return zs;
+    }
     g_ctx[dev] = c;
     *out = c;
     return Status::Ok();
@@ -103,7 +115,8 @@ Status current_ctx(DeviceCtx **out) {
 // zeroed (kernels leave them zero when they finish).
 Status ensure_workspace(DeviceCtx *c, const MatmulArgs &m, hipStream_t s, Workspace *ws) {
     size_t pf = 0, nc = 0;
-    gemv_workspace_need(m, &pf, &nc);
+    if (m.M <= kGemvMaxM) gemv_workspace_need(m, &pf, &nc);
+    else gemm_workspace_need(m, &pf, &nc);
     if (pf > 0) {
         TML_TRY(c->ws.ensure(pf * sizeof(float)));
         if (c->counters.bytes < nc * sizeof(unsigned)) {
@@ -150,12 +163,11 @@ Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const fl
     m.A = A; m.B = B; m.scales = scales; m.block = fmt == TML_FMT_Q8_K ? block : 1;
     m.bias = bias; m.C = C; m.beta = beta; m.fmt = fmt;
     m.alpha_eff = (fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0) ? alpha * scale : alpha;
-    if (M <= kGemvMaxM) {
-        Workspace ws;
-        TML_TRY(ensure_workspace(c, m, s, &ws));
-        return launch_gemv(m, ws, s);
-    }
-    return launch_gemm_mfma(m, s);
+    m.zero = c->zero.p;
+    Workspace ws;
+    TML_TRY(ensure_workspace(c, m, s, &ws));
+    if (M <= kGemvMaxM) return launch_gemv(m, ws, s);
+    return launch_gemm_mfma(m, ws, s);
 }
 
 // Resident copy of a registered host buffer of at least `bytes`, or null.
@@ -253,6 +265,7 @@ void tml_hip_shutdown(void) {
         for (auto &w : c->weights) (void)hipFree(w.second.dev);
         c->a.release(); c->b.release(); c->c.release(); c->bias.release();
         c->scales.release(); c->qtmp.release(); c->ws.release(); c->counters.release();
+        c->zero.release();
         if (c->stream) (void)hipStreamDestroy(c->stream);
         (void)hipSetDevice(prev);
         delete c;

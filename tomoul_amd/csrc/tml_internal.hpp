@@ -48,7 +48,14 @@ struct MatmulArgs {
     float alpha_eff;       // alpha * per-tensor scale
     float beta;
     int fmt;
+    const void *zero;      // >= 64 zero bytes of device memory (see below)
 };
+
+// Kernels load out-of-range chunks from this zeroed block instead of
+// branching around the load: the selected address keeps the load
+// unconditional, which lets the compiler keep whole batches of global loads
+// in flight (a branch around a load makes it wait for all earlier loads).
+constexpr size_t kZeroBlockBytes = 64;
 
 // Split-K workspace handed to kernels that reduce across workgroups.
 struct Workspace {
@@ -60,7 +67,25 @@ struct Workspace {
 
 // Kernel-family launchers (asynchronous).  Each validates that the problem
 // fits what its kernels assume before launching.
-Status launch_gemm_mfma(const MatmulArgs &a, hipStream_t s);
+// Tiled GEMM families for M > kGemvMaxM.  The plan (kernel, tile, K splits)
+// is a pure function of the problem, so workspace sizing and launch agree.
+struct GemmPlan {
+    bool dma = false;  // direct-copy fp32 kernel (gemm_dma.hip)
+    int cfg = 0;       // tile config of that kernel family
+    int nsplit = 1;    // K splits (dma kernel only)
+    int spl = 0;       // BK-slices per split
+    int tiles = 0;
+};
+GemmPlan plan_gemm(const MatmulArgs &a);
+void gemm_workspace_need(const MatmulArgs &a, size_t *partial_floats, size_t *counters);
+Status launch_gemm_mfma(const MatmulArgs &a, const Workspace &ws, hipStream_t s);
+// fp32 GEMM with direct global->LDS copies (gemm_dma.hip); supported when
+// K % 4 == N % 4 == 0 and A, B are 16-byte aligned.
+bool gemm_dma_supported(const MatmulArgs &a);
+int gemm_dma_num_cfgs();
+void gemm_dma_tile(int cfg, int *bm, int *bn);
+constexpr int kDmaBK = 32;
+Status launch_gemm_f32_dma(const MatmulArgs &a, const GemmPlan &p, const Workspace &ws, hipStream_t s);
 Status launch_gemv(const MatmulArgs &a, const Workspace &ws, hipStream_t s);
 // Workspace needed by launch_gemv for this problem.
 void gemv_workspace_need(const MatmulArgs &a, size_t *partial_floats, size_t *counters);
