@@ -57,6 +57,10 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true", help="only the headline workload")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    p.add_argument("--profile-step", action="store_true",
+                   help="only warm up and run the timed headline steps (for rocprofv3 runs)")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="run a plain 256 MiB device copy 5 times (scale for FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -130,8 +134,30 @@ def main():
         for (_, _, _, _, fn) in launches:
             fn(st)
 
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": 256 << 20, "copies": 5}), flush=True)
+        return
+
+    # The step is captured once as a HIP graph and replayed: four GEMM
+    # launches (plus a split-K reduce where the plan splits K) per replay.
     for _ in range(args.warmup):
         step()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        step(side.cuda_stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        step(side.cuda_stream)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
     torch.cuda.synchronize()
     # correctness guard against a float64 torch product on the GPU
     max_rel = 0.0
@@ -141,12 +167,13 @@ def main():
     log(f"headline max rel err vs f64: {max_rel:.3e}")
 
     torch.cuda.synchronize()
+    cur = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    ev0.record(stream)
+    ev0.record(cur)
     for _ in range(args.steps):
-        step()
-    ev1.record(stream)
+        graph.replay()
+    ev1.record(cur)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     ev_ms = ev0.elapsed_time(ev1)
@@ -154,6 +181,9 @@ def main():
     value = step_flops / (ms_per_step * 1e-3) / 1e12
     log(f"headline: {ms_per_step * 1e3:.1f} us/step wall, {ev_ms / args.steps * 1e3:.1f} us/step events, "
         f"{value:.2f} TFLOP/s")
+    if args.profile_step:
+        print(json.dumps({"profile_step": True, "ms_per_step": ms_per_step, "tflops": value}), flush=True)
+        return
 
     # per-launch durations of the GEMM kernel (events around each launch)
     per_shape = {}
@@ -164,10 +194,14 @@ def main():
         per_shape[name] = {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2), "tflops": round(fl / ms / 1e9, 2)}
         tot_fl += fl
         tot_ms += ms
-    achieved = tot_fl / tot_ms / 1e9
+    # achieved: the step's algorithmic flops over its HIP-event duration in
+    # the timed region (all GEMM launches of the step, gaps included).
+    achieved = step_flops / (ev_ms / args.steps) / 1e9
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
-                "kernel": "gemm_mfma_kernel (fp32, 16x16x4 f32 MFMA)", "per_shape": per_shape}
+                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": traffic_per_step(),
+                "algorithmic_bytes": int(sum(4 * (M * K + K * N + M * N) for (_, M, N, K) in XLMR_SHAPES)),
+                "kernel": "gemm_f32_dma_kernel (+ splitk_reduce_kernel), v_mfma_f32_16x16x4_f32",
+                "per_shape": per_shape, "per_shape_sum_tflops": round(tot_fl / tot_ms / 1e9, 2)}
     log(f"roofline: {json.dumps(roofline)}")
 
     result = {
@@ -199,6 +233,18 @@ def main():
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
 
     print(json.dumps(result), flush=True)
+
+
+def traffic_per_step():
+    """HBM bytes per headline step from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a plain copy kernel),
+    or None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemm_xlmr_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_step")
+    except (OSError, ValueError):
+        return None
 
 
 def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):

@@ -113,6 +113,16 @@ int tml_hip_sgemm_q8k(int64_t M, int64_t N, int64_t K, const float *A, const int
  * k*N + j). */
 int tml_hip_sgemm_q4(int64_t M, int64_t N, int64_t K, const float *A, const uint8_t *Bp, float scale, float *C);
 
+/* Generic host-pointer matmul with an optional fused bias:
+ *   C = A . dequant(B) + bias      (bias may be NULL)
+ * fmt/scale/scales/block as for tml_hip_gemm_dev below.  Replaces the
+ * quantized branch of matmulWithWeightBias (src/core/attention.zig:132-149,
+ * duplicated at src/core/transformer.zig:147-166), which runs the weight-only
+ * matmul and then a separate addBiasInPlace pass; here the bias is applied in
+ * the kernel epilogue. */
+int tml_hip_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                 const float *scales, int64_t block, const float *bias, float *C);
+
 /* Host-pointer form of tml_hip_quantize_dev below (synchronous): the GPU
  * replacement for the load-time quantizers quantizeQ8 / quantizeQ8K /
  * quantizeQ4 (src/core/quantization.zig:98-129, :406-446, :721-754) that

@@ -344,3 +344,29 @@ def test_sgemm_register_staged_kernel(orc, forced_env):
         forced_env["TML_GEMM_TILE"] = tile
         a, b = rnd(95, 200, 136), rnd(96, 136, 264, 0.02)
         assert rel_err(ops.matmul(T(a), T(b)).numpy(), orc.matmul(a, b)) <= FP32_TOL, tile
+
+
+# --------------------------------------------- weight-type dispatch (callers)
+@pytest.mark.parametrize("m", [1, 7, 64])
+def test_matmul_with_weight_bias_all_formats(orc, m):
+    # matmulWithWeightBias (src/core/attention.zig:132-149): reference =
+    # scalar weight-only matmul, then a separate bias add.
+    from tomoul_amd import dispatch
+    k, n = 96, 160
+    a = rnd(101, m, k)
+    w = rnd(102, k, n, 0.02)
+    bias = synth.normal(103, n, 0.0, 0.02)
+    tb = Tensor.from_numpy(bias)
+    got = dispatch.matmulWithWeightBias(T(a), T(w), tb).numpy()
+    assert rel_err(got, orc.matmul_bias(a, w, bias)) <= FP32_TOL
+    q, s = orc.quantize_q8(w)
+    got = dispatch.matmulWithWeightBias(T(a), qz.QuantizedTensorQ8(s, q, (k, n)), tb).numpy()
+    assert rel_err(got, orc.matmul_q8(a, q, s) + bias) <= Q_TOL
+    p, s4 = orc.quantize_q4(w)
+    got = dispatch.matmulWithWeightBias(T(a), qz.QuantizedTensorQ4(s4, p, (k, n)), tb).numpy()
+    assert rel_err(got, orc.matmul_q4(a, p, k, n, s4) + bias) <= Q_TOL
+    qk, sk = orc.quantize_q8k(w)
+    got = dispatch.matmulWithWeightBias(T(a), qz.QuantizedTensorQ8K(sk, qk, (k, n)), tb).numpy()
+    assert rel_err(got, orc.matmul_q8k(a, qk, sk) + bias) <= Q_TOL
+    got = dispatch.matmulWithWeight(T(a), qz.QuantizedTensorQ8(s, q, (k, n))).numpy()
+    assert rel_err(got, orc.matmul_q8(a, q, s)) <= Q_TOL

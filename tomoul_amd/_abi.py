@@ -41,6 +41,7 @@ SIGNATURES = {
     "tml_hip_sgemm_q8": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _f, _vp]),
     "tml_hip_sgemm_q8k": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "tml_hip_sgemm_q4": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _f, _vp]),
+    "tml_hip_gemm": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp]),
     "tml_hip_quantize": (ctypes.c_int, [ctypes.c_int, _i64, _vp, _vp, _vp]),
     "tml_hip_weight_register": (ctypes.c_int, [_vp, ctypes.c_size_t]),
     "tml_hip_weight_release": (ctypes.c_int, [_vp]),
@@ -135,6 +136,11 @@ def sgemm_q8k(m: int, n: int, k: int, a: np.ndarray, q: np.ndarray, scales: np.n
 
 def sgemm_q4(m: int, n: int, k: int, a: np.ndarray, packed: np.ndarray, scale: float, c: np.ndarray) -> None:
     check(lib().tml_hip_sgemm_q4(m, n, k, _ptr(a), _ptr(packed), scale, _ptr(c)))
+
+
+def gemm(fmt: int, m: int, n: int, k: int, a: np.ndarray, b: np.ndarray, c: np.ndarray, *, scale: float = 1.0,
+         scales: np.ndarray | None = None, block: int = 32, bias: np.ndarray | None = None) -> None:
+    check(lib().tml_hip_gemm(fmt, m, n, k, _ptr(a), _ptr(b), scale, _ptr(scales), block, _ptr(bias), _ptr(c)))
 
 
 def quantize(fmt: int, w: np.ndarray, q: np.ndarray, scales: np.ndarray) -> None:

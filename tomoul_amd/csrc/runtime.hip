@@ -317,6 +317,11 @@ int tml_hip_sgemm_q4(int64_t M, int64_t N, int64_t K, const float *A, const uint
     return report(host_gemm(TML_FMT_Q4_0, M, N, K, A, Bp, scale, nullptr, 0, nullptr, C, 1.0f, 0.0f));
 }
 
+int tml_hip_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                 const float *scales, int64_t block, const float *bias, float *C) {
+    return report(host_gemm(fmt, M, N, K, A, B, scale, scales, block, bias, C, 1.0f, 0.0f));
+}
+
 int tml_hip_quantize(int fmt, int64_t n, const float *w, void *q, float *scales) {
     if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K)
         return report(Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0 or Q8_K"));

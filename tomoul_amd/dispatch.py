@@ -1,0 +1,52 @@
+"""Weight-type dispatch of the reference's attention/transformer layers.
+
+matmulWithWeight(input, weight)         src/core/attention.zig:114-130
+matmulWithWeightBias(input, weight, b)  src/core/attention.zig:132-149
+(duplicated at src/core/transformer.zig:129-166).  The weight's type selects
+the kernel family; every branch runs on the GPU.  For quantized weights the
+reference runs the matmul and then addBiasInPlace; here the bias is fused
+into the kernel epilogue (one launch, no second pass over the output).
+"""
+from __future__ import annotations
+
+from . import _abi, ops, quantization as qz
+from .tensor import Tensor
+
+
+def _check(a: Tensor, w_shape, bias: Tensor | None = None):
+    if len(a.shape) != 2 or len(w_shape) != 2 or (bias is not None and len(bias.shape) != 1):
+        raise ops.OpsError.InvalidShape(f"matmul needs 2-D operands, got {a.shape} and {w_shape}")
+    if a.shape[1] != w_shape[0]:
+        raise ops.OpsError.ShapeMismatch(f"inner dimensions differ: {a.shape} x {w_shape}")
+    if bias is not None and bias.shape[0] != w_shape[1]:
+        raise ops.OpsError.ShapeMismatch(f"bias has {bias.shape[0]} entries, output has {w_shape[1]} columns")
+    return a.shape[0], w_shape[1], a.shape[1]
+
+
+def matmulWithWeight(a: Tensor, weight) -> Tensor:  # noqa: N802 (reference name)
+    if isinstance(weight, Tensor):
+        return ops.matmul(a, weight)
+    if isinstance(weight, qz.QuantizedTensorQ8):
+        return qz.matmulF32Q8Simd(a, weight)
+    if isinstance(weight, qz.QuantizedTensorQ4):
+        return qz.matmulF32Q4Simd(a, weight)
+    if isinstance(weight, qz.QuantizedTensorQ8K):
+        return qz.matmulF32Q8KSimd(a, weight)
+    raise TypeError(f"unsupported weight type {type(weight).__name__}")
+
+
+def matmulWithWeightBias(a: Tensor, weight, bias: Tensor) -> Tensor:  # noqa: N802
+    if isinstance(weight, Tensor):
+        return ops.matmulBias(a, weight, bias)
+    m, n, k = _check(a, weight.shape, bias)
+    out = Tensor.init((m, n))
+    if isinstance(weight, qz.QuantizedTensorQ8):
+        _abi.gemm(_abi.FMT_Q8_0, m, n, k, a.data, weight.data, out.data, scale=weight.scale, bias=bias.data)
+    elif isinstance(weight, qz.QuantizedTensorQ4):
+        _abi.gemm(_abi.FMT_Q4_0, m, n, k, a.data, weight.data, out.data, scale=weight.scale, bias=bias.data)
+    elif isinstance(weight, qz.QuantizedTensorQ8K):
+        _abi.gemm(_abi.FMT_Q8_K, m, n, k, a.data, weight.data, out.data, scales=weight.scales,
+                  block=weight.block_size, bias=bias.data)
+    else:
+        raise TypeError(f"unsupported weight type {type(weight).__name__}")
+    return out
