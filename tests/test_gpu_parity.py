@@ -370,3 +370,75 @@ def test_matmul_with_weight_bias_all_formats(orc, m):
     assert rel_err(got, orc.matmul_q8k(a, qk, sk) + bias) <= Q_TOL
     got = dispatch.matmulWithWeight(T(a), qz.QuantizedTensorQ8(s, q, (k, n))).numpy()
     assert rel_err(got, orc.matmul_q8(a, q, s)) <= Q_TOL
+
+
+# ---------------------------------------- GEMV plans (M <= 8), every variant
+@pytest.fixture
+def gemv_env():
+    keys = ("TML_GEMV_LPR", "TML_GEMV_NB")
+    saved = {k: os.environ.get(k) for k in keys}
+    yield os.environ
+    for k, v in saved.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = v
+
+
+@pytest.mark.parametrize("lpr", [4, 8, 16, 32, 64])
+@pytest.mark.parametrize("nb", [1, 3])
+def test_gemv_segments_and_splits(orc, gemv_env, lpr, nb):
+    # Every segment width (lanes per row) and batches-per-split setting of
+    # the GEMV, for every format and row count M = 1..8; K = 333 is ragged
+    # for every batch height, so the last split is partial and, for most
+    # settings, K is split over several workgroups (exchange path).
+    gemv_env["TML_GEMV_LPR"] = str(lpr)
+    gemv_env["TML_GEMV_NB"] = str(nb)
+    k, n = 333, 640
+    w = rnd(111, k, n, 0.02)
+    bias = synth.normal(112, n, 0.0, 0.02)
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    qk, sk = orc.quantize_q8k(w)
+    for m in (1, 2, 3, 5, 8):
+        a = rnd(113 + m, m, k)
+        cases = [
+            (_abi.FMT_F32, w, 1.0, None, orc.matmul(a, w), FP32_TOL),
+            (_abi.FMT_Q8_0, q, s, None, orc.matmul_q8(a, q, s), Q_TOL),
+            (_abi.FMT_Q4_0, p, s4, None, orc.matmul_q4(a, p, k, n, s4), Q_TOL),
+            (_abi.FMT_Q8_K, qk, 1.0, sk, orc.matmul_q8k(a, qk, sk, 32), Q_TOL),
+        ]
+        for fmt, b, scale, scales, ref, tol in cases:
+            got = np.zeros((m, n), np.float32)
+            _abi.gemm(fmt, m, n, k, a, np.ascontiguousarray(b), got, scale=scale, scales=scales, bias=bias)
+            err = rel_err(got, ref + bias)
+            assert err <= tol, (fmt, m, err)
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_gemv_generic_path(orc, m):
+    # Odd N (no vector loads possible) and a Q8_K block that does not divide
+    # N take the element-wise path.
+    k, n = 77, 45
+    a = rnd(121, m, k)
+    w = rnd(122, k, n, 0.02)
+    got = ops.matmul(T(a), T(w)).numpy()
+    assert rel_err(got, orc.matmul(a, w)) <= FP32_TOL
+    q, s = orc.quantize_q8(w)
+    got = qz.matmulF32Q8Simd(T(a), qz.QuantizedTensorQ8(s, q, (k, n))).numpy()
+    assert rel_err(got, orc.matmul_q8(a, q, s)) <= Q_TOL
+    p, s4 = orc.quantize_q4(w)
+    got = qz.matmulF32Q4Simd(T(a), qz.QuantizedTensorQ4(s4, p, (k, n))).numpy()
+    assert rel_err(got, orc.matmul_q4(a, p, k, n, s4)) <= Q_TOL
+    qk, sk = orc.quantize_q8k(w)
+    got = qz.matmulF32Q8KSimd(T(a), qz.QuantizedTensorQ8K(sk, qk, (k, n))).numpy()
+    assert rel_err(got, orc.matmul_q8k(a, qk, sk, 32)) <= Q_TOL
+
+
+def test_gemv_alpha_beta(orc):
+    m, k, n = 3, 200, 256
+    a, w = rnd(131, m, k), rnd(132, k, n, 0.02)
+    c0 = rnd(133, m, n)
+    got = c0.copy()
+    _abi.sgemm(m, n, k, a, w, got, 0.5, -2.0)
+    assert rel_err(got, 0.5 * orc.matmul(a, w) - 2.0 * c0) <= FP32_TOL

@@ -2,34 +2,39 @@
 //
 //   C[M,N] = alpha * A[M,K] . Bdeq[K,N] + beta * C + bias[N]
 //
-// At M <= 8 the product is bound by streaming B once from HBM; at the
-// decoder sizes (3-4 MB of weights) a launch is latency-bound, so the design
-// minimises dependent memory round trips:
+// At M <= 8 the product streams B once; at the decoder sizes (3-4 MB of
+// weights) one launch is bound by memory latency, not bandwidth: a plain
+// 4 MiB read kernel needs ~2 us on MI355X however it is shaped, and it gets
+// there only when every CU has its whole share of loads in flight at once.
+// So the kernel is built for parallelism and few dependent round trips:
 //   * B stays in its stored [K,N] layout (N contiguous; src/core/
-//     quantization.zig:193-197).  A workgroup owns a column strip of CL*VB
-//     bytes of every row and walks all K rows of it: each lane loads VB
-//     bytes (16, 8 or 4) of one row per instruction, CL lanes span the strip
-//     and the 64/CL lane groups of each wave take different rows.  Rows are
-//     fetched in batches of U per lane, two batches in flight, with
-//     branch-free clamped addresses so the compiler keeps the batch's loads
-//     outstanding together; the activations of each row are fetched in the
-//     same batch.
+//     quantization.zig:193-197).  Work is cut into column segments of LPR
+//     lanes x LW bytes and row batches; every lane issues its U loads of LW
+//     bytes (and the activations of those rows) back to back, branch-free,
+//     before it does any arithmetic.  The grid holds as many workgroups as
+//     there are (segment, K split) units, typically one to a few per CU.
 //   * Dequantization happens in registers (sign-extending bit-field
 //     extracts); Q8_0 / Q4_0 per-tensor scales are applied once in the
-//     epilogue, Q8_K block scales per row chunk.
-//   * Reduction over the rows of a strip: __shfl_xor across the lane groups
-//     of a wave, then the 4 waves through LDS.
-//   * Only when the output is too narrow to give enough strips is K split
-//     across workgroups; then wave 0 of each workgroup stores its partial,
-//     and the last workgroup of the strip to arrive (device-scope counter)
-//     sums the partials in split order and writes C, so results do not
-//     depend on scheduling.  That workgroup resets the counter.
+//     epilogue, Q8_K block scales per chunk.
+//   * The RW = 64 / LPR row lanes of a wave that share a column chunk are
+//     combined with a reduce-scatter butterfly (each step exchanges half of
+//     the remaining values), which costs about one shuffle per value whatever
+//     RW is; the 4 waves then add up through LDS.
+//   * K splits: each workgroup publishes its partial segment with
+//     agent-coherent stores, waits for them to complete, and bumps the
+//     segment's counter; the last workgroup to arrive reads the other
+//     partials with agent-coherent loads, sums all of them in split order
+//     (results do not depend on scheduling) and writes C, then resets the
+//     counter.  Only agent-scope atomic loads/stores touch the partials, so
+//     no cache-wide write-back or invalidate is needed.
 #include "tml_internal.hpp"
 
 namespace tml {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kNumXcd = 8;
 typedef uint32_t uintx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t uintx2 __attribute__((ext_vector_type(2)));
 
@@ -42,19 +47,22 @@ struct GemvKArgs {
     const float *bias;
     float *C;
     float alpha, beta;
-    int nseg, nsplit, krows;  // krows = rows per split
-    float *ws;
-    unsigned *counters;
+    int nseg;            // column segments
+    int nsplit;          // K splits (workgroups per segment)
+    int nb;              // row batches per workgroup
+    float *ws;           // [nsplit][MR][N] partials when nsplit > 1
+    unsigned *counters;  // one per segment, zero between launches
     const void *zero;
 };
 
-template <int FMT, int VB> struct GemvFmt;
-template <int VB> struct GemvFmt<TML_FMT_F32, VB> { static constexpr int E = VB / 4; };
-template <int VB> struct GemvFmt<TML_FMT_Q8_0, VB> { static constexpr int E = VB; };
-template <int VB> struct GemvFmt<TML_FMT_Q8_K, VB> { static constexpr int E = VB; };
-template <int VB> struct GemvFmt<TML_FMT_Q4_0, VB> { static constexpr int E = 2 * VB; };
+// Elements of B held in LW bytes.
+template <int FMT, int LW> struct Elems;
+template <int LW> struct Elems<TML_FMT_F32, LW> { static constexpr int value = LW / 4; };
+template <int LW> struct Elems<TML_FMT_Q8_0, LW> { static constexpr int value = LW; };
+template <int LW> struct Elems<TML_FMT_Q8_K, LW> { static constexpr int value = LW; };
+template <int LW> struct Elems<TML_FMT_Q4_0, LW> { static constexpr int value = 2 * LW; };
 
-template <int VB> struct Raw { uint32_t w[VB / 4]; float s; };
+template <int LW> struct Raw { uint32_t w[LW / 4]; float s; };
 
 // Sign-extending field extracts (compile to v_bfe_i32).
 __device__ __forceinline__ float sext8(uint32_t word, int byte) {
@@ -64,53 +72,43 @@ __device__ __forceinline__ float sext4(uint32_t word, int nib) {
     return (float)((int32_t)(word << (28 - 4 * nib)) >> 28);
 }
 
-// Vector path: one VB-byte load of row k at column n.  Branch-free: a chunk
-// past the end of the row (last strip, N % SC != 0) reads the zero block (the
-// address is selected, not the value), so every lane issues the same
-// straight-line loads and the compiler keeps a whole batch in flight.  Host
-// guarantees N % E == 0 and VB-byte alignment.
-template <int FMT, int VB>
-__device__ __forceinline__ void load_row(const GemvKArgs &a, int k, int n, Raw<VB> &r) {
-    const bool in = n < a.N;
-    const size_t e = (size_t)k * a.N + (in ? n : 0);
+// s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding).
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); }
+
+__device__ __forceinline__ void store_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Vector path: one LW-byte load of row k at column n.  Branch-free: an
+// invalid chunk (row past the split, column past N) reads the zero block
+// (the address is selected, not the value).  Host guarantees N % E == 0,
+// LW-byte alignment of B and, for Q8_K, N % block == 0 and block % E == 0,
+// so a chunk never straddles a row or a scale block.
+template <int FMT, int LW>
+__device__ __forceinline__ void load_chunk(const GemvKArgs &a, bool in, int k, int n, Raw<LW> &r) {
+    const size_t e = (size_t)k * a.N + n;
     const void *p = !in ? a.zero
                   : FMT == TML_FMT_F32 ? (const void *)((const float *)a.B + e)
                   : FMT == TML_FMT_Q4_0 ? (const void *)((const uint8_t *)a.B + e / 2)
                                         : (const void *)((const int8_t *)a.B + e);
-    if constexpr (VB == 16) {
+    if constexpr (LW == 16) {
         const uintx4 v = *(const uintx4 *)p;
         r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3];
-    } else if constexpr (VB == 8) {
+    } else if constexpr (LW == 8) {
         const uintx2 v = *(const uintx2 *)p;
         r.w[0] = v[0]; r.w[1] = v[1];
     } else {
         r.w[0] = *(const uint32_t *)p;
     }
-    if constexpr (FMT == TML_FMT_Q8_K) r.s = a.scales[e / a.block];
+    if constexpr (FMT == TML_FMT_Q8_K) r.s = *(in ? a.scales + e / a.block : (const float *)a.zero);
 }
 
-// Generic path: element-wise loads with bounds, any N and alignment; the
-// values come back dequantized (Q8_K scale applied, Q8_0 / Q4_0 as integers).
-template <int FMT, int E>
-__device__ __forceinline__ void load_elems(const GemvKArgs &a, int k, int n, float *w) {
-    const size_t e = (size_t)k * a.N + n;
-#pragma unroll
-    for (int i = 0; i < E; ++i) {
-        float v = 0.0f;
-        if (n + i < a.N) {
-            const size_t ei = e + i;
-            if constexpr (FMT == TML_FMT_F32) v = ((const float *)a.B)[ei];
-            else if constexpr (FMT == TML_FMT_Q8_0) v = (float)((const int8_t *)a.B)[ei];
-            else if constexpr (FMT == TML_FMT_Q8_K) v = (float)((const int8_t *)a.B)[ei] * a.scales[ei / a.block];
-            else v = sext4(((const uint8_t *)a.B)[ei / 2], (int)(ei & 1));
-        }
-        w[i] = v;
-    }
-}
-
-template <int FMT, int VB>
-__device__ __forceinline__ void decode_row(const Raw<VB> &r, float *w) {
-    constexpr int E = GemvFmt<FMT, VB>::E;
+template <int FMT, int LW>
+__device__ __forceinline__ void decode_chunk(const Raw<LW> &r, float *w) {
+    constexpr int E = Elems<FMT, LW>::value;
     if constexpr (FMT == TML_FMT_F32) {
 #pragma unroll
         for (int i = 0; i < E; ++i) w[i] = __uint_as_float(r.w[i]);
@@ -128,44 +126,77 @@ __device__ __forceinline__ void decode_row(const Raw<VB> &r, float *w) {
     }
 }
 
-template <int FMT, int MR, int VB, int CL, int U, bool VEC>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
-    constexpr int E = GemvFmt<FMT, VB>::E;
-    constexpr int RL = 64 / CL;        // row lanes per wave
-    constexpr int SC = CL * E;         // columns per segment
-    constexpr int ROWSTEP = 4 * RL;    // rows per step of the workgroup
+// Generic path: element-wise loads with bounds, any N, block and alignment;
+// the values come back dequantized (Q8_K scale applied, Q8_0 / Q4_0 as
+// integers).
+template <int FMT, int E>
+__device__ __forceinline__ void load_elems(const GemvKArgs &a, bool row_ok, int k, int n, float *w) {
+    const size_t e = (size_t)k * a.N + n;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        float v = 0.0f;
+        if (row_ok && n + i < a.N) {
+            const size_t ei = e + i;
+            if constexpr (FMT == TML_FMT_F32) v = ((const float *)a.B)[ei];
+            else if constexpr (FMT == TML_FMT_Q8_0) v = (float)((const int8_t *)a.B)[ei];
+            else if constexpr (FMT == TML_FMT_Q8_K) v = (float)((const int8_t *)a.B)[ei] * a.scales[ei / a.block];
+            else v = sext4(((const uint8_t *)a.B)[ei / 2], (int)(ei & 1));
+        }
+        w[i] = v;
+    }
+}
 
-    __shared__ __attribute__((aligned(16))) float red[4 * MR * SC];
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
+
+template <int FMT, int MR, int LW, int LPR, int U, bool VEC>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
+    constexpr int E = Elems<FMT, LW>::value;
+    constexpr int RW = 64 / LPR;          // row lanes per wave (rows per load instruction)
+    constexpr int SC = LPR * E;           // columns per segment
+    constexpr int RB = kWaves * RW * U;   // rows per batch of the workgroup
+    constexpr int V = MR * E;             // partial sums per lane
+    constexpr int LOG_RW = ilog2(RW);
+    constexpr int LOG_V = ilog2(V);
+    constexpr int NOUT = MR * SC;         // outputs of the segment
+    constexpr int OPT = (NOUT + kThreads - 1) / kThreads;
+    static_assert((1 << LOG_RW) == RW && (1 << LOG_V) == V, "power-of-two shapes");
+
+    __shared__ __attribute__((aligned(16))) float red[kWaves * NOUT];
+    __shared__ unsigned arrived;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int cl = lane % CL, rl = lane / CL;
-    const int R = wave * RL + rl;      // row lane within the workgroup
+    const int cl = lane % LPR, rl = lane / LPR;
 
-    const int seg = blockIdx.x % a.nseg;
-    const int split = blockIdx.x / a.nseg;
+    // Consecutive work ids run on one XCD (workgroups are dealt to the XCDs
+    // round-robin), so segments narrower than a cache line share its L2.
+    const int nblk = gridDim.x, bid = blockIdx.x;
+    const int per = nblk / kNumXcd, rem = nblk % kNumXcd;
+    const int xcd = bid % kNumXcd, idx = bid / kNumXcd;
+    const int work = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int seg = work % a.nseg;
+    const int split = work / a.nseg;
     const int n = seg * SC + cl * E;
-    const int k0 = split * a.krows;
-    const int nk = min(a.K, k0 + a.krows) - k0;             // >= 1 (host)
-    const int nb = (nk + U * ROWSTEP - 1) / (U * ROWSTEP);  // batches (uniform)
+    const bool col_in = n < a.N;
+    const int kbeg = split * a.nb * RB;
+    const int kend = min(a.K, kbeg + a.nb * RB);
+    const int nbat = kend > kbeg ? (kend - kbeg + RB - 1) / RB : 0;
+    const int lrow = (wave * RW + rl) * U;  // the lane's first row in a batch
 
-    float acc[MR][E];
+    float acc[V];
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[m][e] = 0.0f;
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 
-    // One batch = U rows per lane: B chunks plus the M activations of each
-    // row.  Rows past the split re-read row k0 and get zero activations.
-    Raw<VB> w0[U], w1[U];
+    // One batch = U consecutive rows per lane: B chunks plus the MR
+    // activations of each row.  Rows past the split read the zero block.
+    Raw<LW> w0[U], w1[U];
     float x0[U][MR], x1[U][MR];
-    auto load_batch = [&](Raw<VB> *w, float (*x)[MR], int b) {
+    auto load_batch = [&](Raw<LW> *w, float (*x)[MR], int bt) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int kk = R + (b * U + u) * ROWSTEP;
-            const bool valid = kk < nk;
-            const int k = k0 + (valid ? kk : 0);
-            if constexpr (VEC) load_row<FMT, VB>(a, k, n, w[u]);
+            const int k = kbeg + bt * RB + lrow + u;
+            const bool valid = k < kend;
+            if constexpr (VEC) load_chunk<FMT, LW>(a, valid && col_in, valid ? k : 0, col_in ? n : 0, w[u]);
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 const bool ok = valid && m < a.M;
@@ -173,109 +204,151 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
             }
         }
     };
-    auto compute_batch = [&](const Raw<VB> *w, const float (*x)[MR], int b) {
+    auto compute_batch = [&](const Raw<LW> *w, const float (*x)[MR], int bt) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float wv[E];
             if constexpr (VEC) {
-                decode_row<FMT, VB>(w[u], wv);
+                decode_chunk<FMT, LW>(w[u], wv);
             } else {
-                const int kk = R + (b * U + u) * ROWSTEP;
-                load_elems<FMT, E>(a, k0 + (kk < nk ? kk : 0), n, wv);
+                const int k = kbeg + bt * RB + lrow + u;
+                load_elems<FMT, E>(a, k < kend, k < kend ? k : 0, n, wv);
             }
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
-                for (int e = 0; e < E; ++e) acc[m][e] += x[u][m] * wv[e];
+                for (int e = 0; e < E; ++e) acc[m * E + e] += x[u][m] * wv[e];
         }
     };
 
     // Stream B with two batches in flight.
-    load_batch(w0, x0, 0);
-    for (int b = 0; b < nb; b += 2) {
-        if (b + 1 < nb) load_batch(w1, x1, b + 1);
-        compute_batch(w0, x0, b);
-        if (b + 2 < nb) load_batch(w0, x0, b + 2);
-        if (b + 1 < nb) compute_batch(w1, x1, b + 1);
+    if (nbat > 0) load_batch(w0, x0, 0);
+    for (int bt = 0; bt < nbat; bt += 2) {
+        if (bt + 1 < nbat) load_batch(w1, x1, bt + 1);
+        compute_batch(w0, x0, bt);
+        if (bt + 2 < nbat) load_batch(w0, x0, bt + 2);
+        if (bt + 1 < nbat) compute_batch(w1, x1, bt + 1);
     }
 
-    // Reduce over the RL row lanes of the wave, then over the 4 waves.
+    // Reduce-scatter over the RW row lanes (lane bits LPR .. 32): at each
+    // step the lane pair splits the remaining values in halves, each keeps
+    // one half and adds the partner's copy of it.  Once one value is left,
+    // the remaining steps are a plain butterfly.  a + b == b + a exactly, so
+    // both lanes of a pair produce identical sums.
+    int base = 0;  // index of the first value this lane holds
 #pragma unroll
-    for (int off = CL; off < 64; off <<= 1)
+    for (int s = 0; s < LOG_RW; ++s) {
+        const int o = LPR << s;
+        const bool hi = (lane & o) != 0;
+        if (s < LOG_V) {
+            const int half = V >> (s + 1);
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
+            for (int i = 0; i < half; ++i) {
+                const float send = hi ? acc[i] : acc[i + half];
+                const float keep = hi ? acc[i + half] : acc[i];
+                acc[i] = keep + __shfl_xor(send, o);
+            }
+            if (hi) base += half;
+        } else {
+            acc[0] += __shfl_xor(acc[0], o);
+        }
+    }
+    constexpr int HELD = LOG_RW < LOG_V ? (V >> LOG_RW) : 1;
+    const bool writer = LOG_RW <= LOG_V || (rl >> LOG_V) == 0;
+    if (writer) {
 #pragma unroll
-            for (int e = 0; e < E; ++e) acc[m][e] += __shfl_xor(acc[m][e], off);
-    if (rl == 0) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m)
-#pragma unroll
-            for (int e = 0; e < E; ++e) red[(wave * MR + m) * SC + cl * E + e] = acc[m][e];
+        for (int j = 0; j < HELD; ++j) {
+            const int i = base + j;
+            const int m = i / E, e = i % E;
+            red[wave * NOUT + m * SC + cl * E + e] = acc[j];
+        }
     }
     __syncthreads();
 
+    float pv[OPT];
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) {
+        const int o = tid + j * kThreads;
+        float p = 0.0f;
+        if (o < NOUT) {
+            p = red[o];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) p += red[w * NOUT + o];
+        }
+        pv[j] = p;
+    }
+
     const int col0 = seg * SC;
+    auto epilogue = [&](int o, float p) __attribute__((always_inline)) {
+        const int m = o / SC, col = col0 + o % SC;
+        float *cp = a.C + (size_t)m * a.N + col;
+        float v = a.alpha * p;
+        if (a.beta != 0.0f) v += a.beta * *cp;
+        if (a.bias) v += a.bias[col];
+        *cp = v;
+    };
+    auto useful = [&](int o) __attribute__((always_inline)) {
+        return o < NOUT && o / SC < a.M && col0 + o % SC < a.N;
+    };
+
     if (a.nsplit == 1) {
-        for (int o = tid; o < MR * SC; o += kThreads) {
-            const int m = o / SC, c = o % SC, col = col0 + c;
-            if (m < a.M && col < a.N) {
-                const float p = red[m * SC + c] + red[(MR + m) * SC + c] + red[(2 * MR + m) * SC + c] +
-                                red[(3 * MR + m) * SC + c];
-                float *cp = a.C + (size_t)m * a.N + col;
-                float v = a.alpha * p;
-                if (a.beta != 0.0f) v += a.beta * *cp;
-                if (a.bias) v += a.bias[col];
-                *cp = v;
-            }
+#pragma unroll
+        for (int j = 0; j < OPT; ++j) {
+            const int o = tid + j * kThreads;
+            if (useful(o)) epilogue(o, pv[j]);
         }
         return;
     }
 
-    // Split-K: wave 0 alone publishes this split's partial and, if this
-    // workgroup is the last of its segment to arrive, sums all partials in
-    // split order.  Its device-scope fence orders its own partial stores
-    // before its counter increment (release) and its partial loads after it
-    // (acquire), so one fence per workgroup suffices.
-    if (wave != 0) return;
-    for (int o = lane; o < MR * SC; o += 64) {
-        const int m = o / SC, c = o % SC, col = col0 + c;
-        if (m < a.M && col < a.N) {
-            a.ws[((size_t)split * MR + m) * a.N + col] = red[m * SC + c] + red[(MR + m) * SC + c] +
-                                                         red[(2 * MR + m) * SC + c] + red[(3 * MR + m) * SC + c];
-        }
+    // Split-K exchange (see the header comment).
+    const size_t plane = (size_t)MR * a.N;
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) {
+        const int o = tid + j * kThreads;
+        if (useful(o)) store_agent(a.ws + split * plane + (size_t)(o / SC) * a.N + col0 + o % SC, pv[j]);
     }
-    __threadfence();
-    unsigned prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(a.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0);
-    if (prev != (unsigned)(a.nsplit - 1)) return;
-    __threadfence();
-    for (int o = lane; o < MR * SC; o += 64) {
-        const int m = o / SC, c = o % SC, col = col0 + c;
-        if (m < a.M && col < a.N) {
-            const float *src = a.ws + (size_t)m * a.N + col;
-            const size_t stride = (size_t)MR * a.N;
-            float p = 0.0f;
-#pragma unroll 8
-            for (int s = 0; s < a.nsplit; ++s) p += src[s * stride];
-            float *cp = a.C + (size_t)m * a.N + col;
-            float v = a.alpha * p;
-            if (a.beta != 0.0f) v += a.beta * *cp;
-            if (a.bias) v += a.bias[col];
-            *cp = v;
+    wait_vm0();  // this thread's partial stores have completed
+    __syncthreads();
+    if (tid == 0)
+        arrived = __hip_atomic_fetch_add(a.counters + seg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != (unsigned)(a.nsplit - 1)) return;
+    // Issue the loads of up to kXB splits at once (each is a memory round
+    // trip), then add them in split order.
+    constexpr int kXB = 8;
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) {
+        const int o = tid + j * kThreads;
+        const bool use = useful(o);
+        const float *src = a.ws + (use ? (size_t)(o / SC) * a.N + col0 + o % SC : 0);
+        float p = 0.0f;
+        for (int s0 = 0; s0 < a.nsplit; s0 += kXB) {
+            float t[kXB];
+#pragma unroll
+            for (int i = 0; i < kXB; ++i) {
+                const int s = min(s0 + i, a.nsplit - 1);
+                t[i] = use ? load_agent(src + s * plane) : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < kXB; ++i)
+                if (s0 + i < a.nsplit) p += (s0 + i == split) ? pv[j] : t[i];
         }
+        if (use) epilogue(o, p);
     }
-    if (lane == 0) a.counters[seg] = 0u;  // ready for the next launch
+    if (tid == 0) __hip_atomic_store(a.counters + seg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- host side
 struct GemvPlan {
-    int mr, vb, e, cl, sc, rowstep;
-    int nseg, nsplit, krows;
+    int mr, lw, e, lpr, u, sc, rb;
+    int nseg, nsplit, nb;
     bool vec;
 };
 
-int pick_vb(int fmt, int mr) {
+constexpr int kU = 4;         // loads per lane per batch
+constexpr int kMaxSplit = 8;  // default cap on K splits per segment
+
+int pick_lw(int fmt, int mr) {
     switch (fmt) {
         case TML_FMT_F32: return 16;
         case TML_FMT_Q8_0:
@@ -284,90 +357,109 @@ int pick_vb(int fmt, int mr) {
     }
 }
 
-int elems_per_lane(int fmt, int vb) {
-    return fmt == TML_FMT_F32 ? vb / 4 : (fmt == TML_FMT_Q4_0 ? 2 * vb : vb);
+int elems_per_lane(int fmt, int lw) {
+    return fmt == TML_FMT_F32 ? lw / 4 : (fmt == TML_FMT_Q4_0 ? 2 * lw : lw);
 }
 
 bool is_aligned(const void *p, size_t n) { return ((uintptr_t)p % n) == 0; }
 
-// Bytes of B one workgroup should stream: enough to keep its CU's memory
-// pipeline full for one latency, small enough that the grid reaches many CUs.
-constexpr int64_t kBlockBytes = 64 << 10;
-constexpr int64_t kMinBlocks = 32;
+int gemv_cus() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
 
+// Segment width: the narrowest segment of at least one 128-byte line per
+// row that wastes little of the last segment; narrower segments mean fewer
+// K splits (less partial traffic) at the cost of more shuffle steps.
+// Batches per workgroup: one (maximum parallelism, every load issued at
+// once) until the grid would exceed a few workgroups per CU.
 GemvPlan make_plan(const MatmulArgs &m) {
     GemvPlan p{};
     p.mr = m.M <= 1 ? 1 : m.M <= 2 ? 2 : m.M <= 4 ? 4 : 8;
-    p.vb = pick_vb(m.fmt, p.mr);
-    p.e = elems_per_lane(m.fmt, p.vb);
-    p.vec = (m.N % p.e == 0) && is_aligned(m.B, (size_t)p.vb);
-    if (m.fmt == TML_FMT_Q8_K) p.vec = p.vec && (m.block % p.e == 0);
-    const int64_t block_bytes = env_int("TML_GEMV_BLOCK_KB", 0) > 0 ? (int64_t)env_int("TML_GEMV_BLOCK_KB", 0) << 10
-                                                                     : kBlockBytes;
-    // Column strip per workgroup: the widest strip (CL lanes of VB bytes)
-    // whose K rows fit the byte budget with enough strips to spread over
-    // the CUs; each workgroup then covers all of K and needs no reduction
-    // with other workgroups.
-    int cl = 1;
-    bool fits = false;
-    for (int c = 8; c >= 1; c >>= 1) {
-        const int64_t nseg = (m.N + (int64_t)c * p.e - 1) / ((int64_t)c * p.e);
-        if ((int64_t)c * p.vb * m.K <= block_bytes && nseg >= kMinBlocks) {
-            cl = c;
-            fits = true;
-            break;
-        }
+    p.lw = pick_lw(m.fmt, p.mr);
+    p.e = elems_per_lane(m.fmt, p.lw);
+    p.u = kU;
+    p.vec = (m.N % p.e == 0) && is_aligned(m.B, (size_t)p.lw);
+    if (m.fmt == TML_FMT_Q8_K) p.vec = p.vec && (m.block % p.e == 0) && (m.N % m.block == 0);
+    const int64_t bpe_num = m.fmt == TML_FMT_F32 ? 4 : 1, bpe_den = m.fmt == TML_FMT_Q4_0 ? 2 : 1;
+    const int64_t rowbytes = (m.N * bpe_num + bpe_den - 1) / bpe_den;
+    // Segment width per row: 64 bytes for quantized B, 128 bytes (one line)
+    // for f32 -- measured best on MI355X at the decoder shapes (narrower
+    // segments scatter the loads over too many lines, wider ones need more
+    // K splits); rows narrower than that get the narrowest segment that
+    // covers them.
+    const int seg_bytes = m.fmt == TML_FMT_F32 ? 128 : 64;
+    int lpr = seg_bytes / p.lw;
+    if (lpr < 4) lpr = 4;
+    if (rowbytes < seg_bytes) {
+        lpr = 4;
+        while (lpr < 64 && (int64_t)lpr * p.lw < rowbytes) lpr *= 2;
     }
-    const int forced_cl = env_int("TML_GEMV_CL", 0);
-    if (forced_cl == 1 || forced_cl == 2 || forced_cl == 4 || forced_cl == 8) cl = forced_cl;
-    p.cl = cl;
-    p.sc = cl * p.e;
-    p.rowstep = 4 * (64 / cl);
+    const int forced_lpr = env_int("TML_GEMV_LPR", 0);
+    if (forced_lpr == 4 || forced_lpr == 8 || forced_lpr == 16 || forced_lpr == 32 || forced_lpr == 64)
+        lpr = forced_lpr;
+    if (!p.vec) lpr = 16;  // the generic path is instantiated for one shape
+    p.lpr = lpr;
+    p.sc = lpr * p.e;
+    p.rb = kWaves * (64 / lpr) * p.u;
     p.nseg = (int)((m.N + p.sc - 1) / p.sc);
-    // Narrow outputs (few strips): split K across workgroups as well.
-    int64_t nsplit = 1;
-    if (!fits) {
-        const int64_t per_strip = (int64_t)p.cl * p.vb * m.K;
-        nsplit = (per_strip + block_bytes - 1) / block_bytes;
-        const int64_t need = (kMinBlocks + p.nseg - 1) / p.nseg;
-        if (nsplit < need) nsplit = need;
+    const int64_t tb = m.K > 0 ? (m.K + p.rb - 1) / p.rb : 1;  // batches along K
+    // K splits: enough workgroups for about two per CU, but at most
+    // kMaxSplit per segment -- every split adds an arrival on the segment's
+    // counter, and those atomics serialise.
+    const int cus = gemv_cus();
+    int64_t nb = 1;
+    const int forced_nb = env_int("TML_GEMV_NB", 0);
+    if (forced_nb > 0) {
+        nb = forced_nb;
+    } else {
+        const int64_t max_split = env_int("TML_GEMV_MAXSPLIT", kMaxSplit);
+        int64_t want = (2 * (int64_t)cus + p.nseg - 1) / p.nseg;
+        if (want > max_split) want = max_split;
+        if (want < 1) want = 1;
+        nb = (tb + want - 1) / want;
     }
-    const int forced = env_int("TML_GEMV_SPLIT", 0);
-    if (forced > 0) nsplit = forced;
-    const int64_t max_split = m.K > p.rowstep ? m.K / p.rowstep : 1;
-    if (nsplit > max_split) nsplit = max_split;
-    if (nsplit < 1) nsplit = 1;
-    int64_t kr = (m.K + nsplit - 1) / nsplit;
-    kr = ((kr + p.rowstep - 1) / p.rowstep) * p.rowstep;
-    if (kr < p.rowstep) kr = p.rowstep;
-    p.krows = (int)kr;
-    p.nsplit = m.K == 0 ? 1 : (int)((m.K + kr - 1) / kr);
+    if (nb > tb) nb = tb;
+    if (nb < 1) nb = 1;
+    p.nb = (int)nb;
+    p.nsplit = (int)((tb + nb - 1) / nb);
     return p;
 }
 
-template <int FMT, int MR, int VB, int CL, bool VEC>
+template <int FMT, int MR, int LW, int LPR, bool VEC>
 void launch_one(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
-    constexpr int U = MR <= 2 ? 8 : 4;  // rows per lane per batch (register budget)
-    gemv_kernel<FMT, MR, VB, CL, U, VEC><<<dim3((unsigned)(p.nseg * p.nsplit)), dim3(kThreads), 0, s>>>(ka);
+    gemv_kernel<FMT, MR, LW, LPR, kU, VEC><<<dim3((unsigned)(p.nseg * p.nsplit)), dim3(kThreads), 0, s>>>(ka);
 }
 
-template <int FMT, int MR, int VB, bool VEC>
-void launch_cl(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
-    switch (p.cl) {
-        case 1: launch_one<FMT, MR, VB, 1, VEC>(ka, p, s); break;
-        case 2: launch_one<FMT, MR, VB, 2, VEC>(ka, p, s); break;
-        case 4: launch_one<FMT, MR, VB, 4, VEC>(ka, p, s); break;
-        default: launch_one<FMT, MR, VB, 8, VEC>(ka, p, s); break;
+template <int FMT, int MR, int LW>
+void launch_lpr(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
+    if (!p.vec) {
+        launch_one<FMT, MR, LW, 16, false>(ka, p, s);
+        return;
+    }
+    switch (p.lpr) {
+        case 4: launch_one<FMT, MR, LW, 4, true>(ka, p, s); break;
+        case 8: launch_one<FMT, MR, LW, 8, true>(ka, p, s); break;
+        case 16: launch_one<FMT, MR, LW, 16, true>(ka, p, s); break;
+        case 32: launch_one<FMT, MR, LW, 32, true>(ka, p, s); break;
+        default: launch_one<FMT, MR, LW, 64, true>(ka, p, s); break;
     }
 }
 
 template <int FMT, int MR>
 Status launch_mr(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
-    constexpr int VB_VEC = FMT == TML_FMT_F32 ? 16
-                         : (FMT == TML_FMT_Q4_0 ? (MR <= 2 ? 16 : (MR == 4 ? 8 : 4)) : (MR <= 4 ? 16 : 8));
-    if (p.vb != VB_VEC) return Status::Err(TML_ERR_INVALID_ARG, "gemv plan/instantiation mismatch");
-    if (p.vec) launch_cl<FMT, MR, VB_VEC, true>(ka, p, s);
-    else launch_cl<FMT, MR, VB_VEC, false>(ka, p, s);
+    constexpr int LW = FMT == TML_FMT_F32 ? 16
+                     : (FMT == TML_FMT_Q4_0 ? (MR <= 2 ? 16 : (MR == 4 ? 8 : 4)) : (MR <= 4 ? 16 : 8));
+    if (p.lw != LW) return Status::Err(TML_ERR_INVALID_ARG, "gemv plan/instantiation mismatch");
+    launch_lpr<FMT, MR, LW>(ka, p, s);
     TML_HIP_TRY(hipGetLastError());
     return Status::Ok();
 }
@@ -408,7 +500,7 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     ka.M = (int)m.M; ka.N = (int)m.N; ka.K = (int)m.K;
     ka.A = m.A; ka.B = m.B; ka.scales = m.scales; ka.block = m.block;
     ka.bias = m.bias; ka.C = m.C; ka.alpha = m.alpha_eff; ka.beta = m.beta;
-    ka.nseg = p.nseg; ka.nsplit = p.nsplit; ka.krows = p.krows;
+    ka.nseg = p.nseg; ka.nsplit = p.nsplit; ka.nb = p.nb;
     ka.ws = ws.partials; ka.counters = ws.counters;
     ka.zero = m.zero;
     switch (m.fmt) {
