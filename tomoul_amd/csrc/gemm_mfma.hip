@@ -421,14 +421,20 @@ int device_cus() {
 }
 
 // Direct-copy fp32 kernel: pick (tile, K splits) with the smallest modelled
-// time = rounds of workgroups over the CUs (a CU holds per_cu workgroups of
-// a tile at once) x (slices per split + fixed cost) x tile area / efficiency.
-// The fixed cost covers pipeline fill, epilogue and, with splits, the
-// partial-tile exchange.
+// time.  A CU runs its share of the units (tile x split) one after another
+// (the 64x64 tile three at a time, which is what its per-slice time below
+// already includes), so
+//   t = ceil(units / CUs) * slices_per_split * t_slice[tile]
+//       + t_fill + (splits > 1 ? t_reduce : 0)
+// with t_slice measured on MI355X at full occupancy (us per BK = 32 slice of
+// one unit, 2.4 GHz): 128x128 2.05, 128x64 1.09, 64x64 0.58, 256x128 4.05;
+// t_fill (pipeline fill, epilogue, launch) ~3.5 us; t_reduce (the second
+// launch that sums the splits' partials) ~3.6 us plus the partials'
+// traffic, splits * M * N * 8 bytes at ~6 TB/s.
 void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
-    static const float eff[] = {1.00f, 0.92f, 0.80f, 1.05f};
-    static const int per_cu[] = {1, 2, 3, 1};
-    static const int splits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    static const double t_slice[] = {2.05, 1.09, 0.58, 4.05};
+    static const int splits[] = {1, 2, 3, 4, 6, 8};
+    constexpr double kFill = 3.5, kReduce = 3.6, kBytesPerUs = 6.0e6;
     const int cus = device_cus();
     const int64_t nk = (K + kDmaBK - 1) / kDmaBK;
     const int forced_tile = env_int("TML_GEMM_DMA_TILE", 0) - 1;
@@ -445,12 +451,9 @@ void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
             const int64_t spl = nk > 0 ? (nk + sp - 1) / sp : 1;
             const int64_t real = nk > 0 ? (nk + spl - 1) / spl : 1;
             const int64_t units = tiles * real;
-            const int64_t slots = (int64_t)cus * per_cu[c];
-            const int64_t rounds = (units + slots - 1) / slots;
-            // fill/epilogue ~2 slices; splits add a reduce launch (~2.5 us
-            // of launch gap plus streaming the partials), ~6 slices.
-            const double fixed = 2.0 + (real > 1 ? 6.0 : 0.0);
-            const double t = (double)rounds * ((double)spl + fixed) * bm * bn * per_cu[c] / eff[c];
+            const int64_t per_cu = (units + cus - 1) / cus;
+            const double red = real > 1 ? kReduce + (double)real * M * N * 8.0 / kBytesPerUs : 0.0;
+            const double t = (double)per_cu * (double)spl * t_slice[c] + kFill + red;
             if (t < best_t) {
                 best_t = t;
                 p->cfg = c;

@@ -391,12 +391,13 @@ GemvPlan make_plan(const MatmulArgs &m) {
     if (m.fmt == TML_FMT_Q8_K) p.vec = p.vec && (m.block % p.e == 0) && (m.N % m.block == 0);
     const int64_t bpe_num = m.fmt == TML_FMT_F32 ? 4 : 1, bpe_den = m.fmt == TML_FMT_Q4_0 ? 2 : 1;
     const int64_t rowbytes = (m.N * bpe_num + bpe_den - 1) / bpe_den;
-    // Segment width per row: 64 bytes for quantized B, 128 bytes (one line)
-    // for f32 -- measured best on MI355X at the decoder shapes (narrower
-    // segments scatter the loads over too many lines, wider ones need more
-    // K splits); rows narrower than that get the narrowest segment that
-    // covers them.
-    const int seg_bytes = m.fmt == TML_FMT_F32 ? 128 : 64;
+    // Segment width per row: 128 bytes (one line) for f32, 64 bytes for
+    // quantized B at M <= 2 and 32 bytes at M > 2 -- measured best on MI355X
+    // at the decoder shapes (narrower segments scatter the loads over more
+    // lines, wider ones need more K splits and, with many partial sums per
+    // lane, fewer but costlier reduction steps); rows narrower than that get
+    // the narrowest segment that covers them.
+    const int seg_bytes = m.fmt == TML_FMT_F32 ? 128 : (p.mr <= 2 ? 64 : 32);
     int lpr = seg_bytes / p.lw;
     if (lpr < 4) lpr = 4;
     if (rowbytes < seg_bytes) {

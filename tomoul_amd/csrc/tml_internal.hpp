@@ -57,6 +57,37 @@ struct MatmulArgs {
 // in flight (a branch around a load makes it wait for all earlier loads).
 constexpr size_t kZeroBlockBytes = 64;
 
+// Cross-workgroup exchange of split-K partials.  A device-scope fence
+// (__threadfence) on MI355X writes back / invalidates the XCD's whole L2 and
+// costs tens of microseconds per launch, so kernels that combine partials
+// never use one.  Instead the partials themselves are written and read with
+// agent-scope atomic stores / loads (coherent across the XCDs by
+// construction), each writer waits for its stores to complete (vmcnt(0))
+// before its workgroup bumps the tile's arrival counter, and the last
+// workgroup to arrive reads the other partials and finishes the tile.
+__device__ __forceinline__ void xchg_store(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float xchg_load(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding).
+__device__ __forceinline__ void xchg_wait_stores() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); }
+// Bumps *counter once for the workgroup (after every thread has waited for
+// its partial stores) and returns, to every thread, the number of
+// workgroups that arrived before this one.  `slot` is a __shared__ word.
+__device__ __forceinline__ unsigned xchg_arrive(unsigned *counter, unsigned *slot) {
+    xchg_wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *slot = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    return *slot;
+}
+__device__ __forceinline__ void xchg_reset(unsigned *counter) {
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Split-K workspace handed to kernels that reduce across workgroups.
 struct Workspace {
     float *partials = nullptr;      // nsplit * M * N floats
