@@ -161,6 +161,38 @@ int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
  * ceil(n/32) floats (Q8_K).  Device pointers, asynchronous on stream. */
 int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream);
 
+/* ------------------------------------------------------ prepared weights */
+
+/* Device-native copy of an immutable weight for decoder products.  The
+ * reference's weights are immutable after load and owned by
+ * AttentionWeights / TransformerBlockWeights until deinit
+ * (src/core/attention.zig:54-86, src/core/transformer.zig:31-68), so a
+ * backend may keep them in whatever layout its kernels read best.  The
+ * prepared copy stores B K-contiguous (row n = column n of B, zero padded
+ * to a multiple of 16 bytes; Q4_0 keeps two k per byte, even k in the low
+ * nibble), so a GEMV with M <= 2 reads each output's weights as one
+ * contiguous run and needs no cross-workgroup reduction (M <= 8 for f32,
+ * M <= 4 for Q8_0, M <= 2 for Q4_0).  No counterpart in
+ * the reference (its CPU loops read B in place).
+ *
+ * tml_hip_prepare_dev: fmt is TML_FMT_F32, TML_FMT_Q8_0 or TML_FMT_Q4_0;
+ *   B is the device [K,N] weight in the layouts above, scale the Q8_0 /
+ *   Q4_0 per-tensor scale.  The copy is built asynchronously on `stream`.
+ *   B must stay valid and unchanged while the handle is used: calls with
+ *   more rows than the prepared kernel covers run on B itself.
+ * tml_hip_gemm_prepared: C = alpha * A[M,K] . dequant(B) + beta * C + bias
+ *   (bias may be NULL), device pointers, asynchronous on `stream`.
+ * tml_hip_prepared_free: waits for the device, then frees the copy.
+ *
+ * Host-pointer calls with a registered weight (tml_hip_weight_register) at
+ * those row counts build and use such a copy automatically. */
+typedef struct tml_prepared_weight *tml_prepared_t;
+int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scale, void *stream,
+                        tml_prepared_t *out);
+int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const float *bias, float *C, float alpha,
+                          float beta, void *stream);
+int tml_hip_prepared_free(tml_prepared_t w);
+
 #ifdef __cplusplus
 }
 #endif

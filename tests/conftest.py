@@ -4,6 +4,15 @@ import sys
 import numpy as np
 import pytest
 
+# torch ships its own HIP runtime under the same SONAME (libamdhip64.so.7)
+# as /opt/rocm's; whichever is loaded first serves the whole process.  Tests
+# that hand torch device buffers to libtomoul_hip need torch's copy loaded
+# before the library, so import torch first when it is installed.
+try:
+    import torch  # noqa: F401
+except ImportError:  # pragma: no cover
+    pass
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)

@@ -442,3 +442,108 @@ def test_gemv_alpha_beta(orc):
     got = c0.copy()
     _abi.sgemm(m, n, k, a, w, got, 0.5, -2.0)
     assert rel_err(got, 0.5 * orc.matmul(a, w) - 2.0 * c0) <= FP32_TOL
+
+
+# ------------------------------------- prepared (K-contiguous) decoder weights
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def _prepared_cases(orc, w, k, n, a):
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    return [(_abi.FMT_F32, w, 1.0, orc.matmul(a, w), FP32_TOL),
+            (_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s), Q_TOL),
+            (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4), Q_TOL)]
+
+
+def _run_prepared(fmt, b, scale, k, n, m, a, bias=None, c0=None, alpha=1.0, beta=0.0):
+    import torch
+    B, A = _dev(b), _dev(a)
+    h = _abi.prepare_dev(fmt, k, n, B.data_ptr(), scale)
+    try:
+        C = _dev(c0) if c0 is not None else torch.zeros((m, n), dtype=torch.float32, device="cuda:0")
+        Bias = _dev(bias) if bias is not None else None
+        _abi.gemm_prepared(h, m, A.data_ptr(), C.data_ptr(), bias_ptr=Bias.data_ptr() if Bias is not None else None,
+                           alpha=alpha, beta=beta)
+        torch.cuda.synchronize()
+        return C.cpu().numpy()
+    finally:
+        _abi.prepared_free(h)
+
+
+@pytest.mark.parametrize("k,n", [(1024, 4096), (1280, 5120), (5120, 96), (333, 640), (77, 45), (1, 3),
+                                 (2100, 130), (9000, 40)])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 9])
+def test_prepared_vs_oracle(orc, k, n, m):
+    # The K-contiguous kernel covers M <= 8 (f32), <= 4 (Q8_0), <= 2 (Q4_0);
+    # other row counts run the [K,N] GEMV / GEMM on the weight the copy was
+    # made from (M = 9 always does).
+    w = rnd(141, k, n, 0.02)
+    a = rnd(142 + m, m, k)
+    bias = synth.normal(143, n, 0.0, 0.02)
+    for fmt, b, scale, ref, tol in _prepared_cases(orc, w, k, n, a):
+        got = _run_prepared(fmt, b, scale, k, n, m, a, bias=bias)
+        err = rel_err(got, ref + bias)
+        assert err <= tol, (fmt, err)
+
+
+@pytest.mark.parametrize("lk", [64, 256])
+@pytest.mark.parametrize("cw", [1, 2, 4])
+@pytest.mark.parametrize("jb", [1, 2, 4])
+def test_prepared_plan_variants(orc, lk, cw, jb):
+    keys = ("TML_GEMVT_LK", "TML_GEMVT_CW", "TML_GEMVT_JB")
+    saved = {key: os.environ.get(key) for key in keys}
+    os.environ.update({"TML_GEMVT_LK": str(lk), "TML_GEMVT_CW": str(cw), "TML_GEMVT_JB": str(jb)})
+    try:
+        k, n = 1500, 70
+        w = rnd(151, k, n, 0.02)
+        for m in (1, 2):
+            a = rnd(152 + m, m, k)
+            for fmt, b, scale, ref, tol in _prepared_cases(orc, w, k, n, a):
+                assert rel_err(_run_prepared(fmt, b, scale, k, n, m, a), ref) <= tol, (fmt, m)
+    finally:
+        for key, v in saved.items():
+            if v is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = v
+
+
+def test_prepared_alpha_beta_and_inf(orc):
+    k, n, m = 300, 200, 2
+    w, a, c0 = rnd(161, k, n, 0.02), rnd(162, m, k), rnd(163, m, n)
+    got = _run_prepared(_abi.FMT_F32, w, 1.0, k, n, m, a, c0=c0, alpha=0.5, beta=-2.0)
+    assert rel_err(got, 0.5 * orc.matmul(a, w) - 2.0 * c0) <= FP32_TOL
+    # An infinite activation must give what the reference gives (inf or
+    # nan per output), not a nan from a padded product.
+    a2 = a.copy()
+    a2[0, 5] = np.inf
+    got = _run_prepared(_abi.FMT_F32, w, 1.0, k, n, m, a2)
+    ref = orc.matmul(a2, w)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    np.testing.assert_array_equal(np.isinf(got), np.isinf(ref))
+
+
+def test_registered_weight_uses_prepared_copy(orc):
+    # Host-pointer decoder calls on a registered weight go through the
+    # prepared copy; results agree with the unregistered path to tolerance
+    # and with the oracle.
+    k, n = 640, 384
+    w = rnd(171, k, n, 0.02)
+    q, s = orc.quantize_q8(w)
+    for m in (1, 2):
+        a = rnd(172 + m, m, k)
+        c0 = np.zeros((m, n), np.float32)
+        _abi.sgemm_q8(m, n, k, a, q, s, c0)
+        _abi.weight_register(q)
+        try:
+            c1 = np.zeros((m, n), np.float32)
+            _abi.sgemm_q8(m, n, k, a, q, s, c1)
+            c2 = np.zeros((m, n), np.float32)
+            _abi.sgemm_q8(m, n, k, a, q, s, c2)
+        finally:
+            _abi.weight_release(q)
+        np.testing.assert_array_equal(c1, c2)
+        assert rel_err(c1, c0) <= Q_TOL and rel_err(c1, orc.matmul_q8(a, q, s)) <= Q_TOL

@@ -48,6 +48,9 @@ SIGNATURES = {
     "tml_hip_gemm_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp, _f, _f,
                                         _vp]),
     "tml_hip_quantize_dev": (ctypes.c_int, [ctypes.c_int, _i64, _vp, _vp, _vp, _vp]),
+    "tml_hip_prepare_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _f, _vp, ctypes.POINTER(_vp)]),
+    "tml_hip_gemm_prepared": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _f, _f, _vp]),
+    "tml_hip_prepared_free": (ctypes.c_int, [_vp]),
 }
 
 
@@ -165,3 +168,20 @@ def gemm_dev(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr: in
 
 def quantize_dev(fmt: int, n: int, w_ptr: int, q_ptr: int, scales_ptr: int, stream: int | None = None) -> None:
     check(lib().tml_hip_quantize_dev(fmt, n, w_ptr, q_ptr, scales_ptr, stream))
+
+
+# ---------------------------------------------------------- prepared weights
+def prepare_dev(fmt: int, k: int, n: int, b_ptr: int, scale: float = 1.0, stream: int | None = None) -> int:
+    """Device-native copy of the [K,N] device weight at b_ptr; returns a handle."""
+    h = ctypes.c_void_p()
+    check(lib().tml_hip_prepare_dev(fmt, k, n, b_ptr, scale, stream, ctypes.byref(h)))
+    return h.value
+
+
+def gemm_prepared(handle: int, m: int, a_ptr: int, c_ptr: int, *, bias_ptr: int | None = None, alpha: float = 1.0,
+                  beta: float = 0.0, stream: int | None = None) -> None:
+    check(lib().tml_hip_gemm_prepared(handle, m, a_ptr, bias_ptr, c_ptr, alpha, beta, stream))
+
+
+def prepared_free(handle: int) -> None:
+    check(lib().tml_hip_prepared_free(handle))

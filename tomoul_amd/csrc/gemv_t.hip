@@ -1,0 +1,388 @@
+// gemv_t.hip -- decoder GEMV on prepared, K-contiguous weights (M <= 8 for
+// f32, <= 4 for Q8_0, <= 2 for Q4_0).
+//
+//   C[M,N] = alpha * A[M,K] . Bdeq[K,N] + beta * C + bias[N]
+//
+// with B held as its device-native "prepared" copy Bt[N][ldt]: row n of Bt
+// is column n of B, K contiguous (int8 one byte per k; int4 two k per byte,
+// even k in the low nibble -- the reference's nibble order, applied along
+// K; f32 four bytes per k), zero padded to ldt bytes, a multiple of 16.
+// Weights are immutable after load in the reference (AttentionWeights owns
+// them until deinit, src/core/attention.zig:54-86), so the copy is made once.
+//
+// Why: at decoder sizes a launch is bound by memory latency (a plain 4 MiB
+// read needs ~2 us on MI355X).  In the stored [K,N] layout a GEMV has to
+// split K over workgroups to reach every CU, and combining the splits costs
+// two more dependent memory round trips.  With K contiguous, each output is
+// one contiguous run of bytes: a column group of LK lanes (one wave, or the
+// whole workgroup) walks the runs of its CW outputs in 16-byte chunks, every
+// load instruction covers LK * 16 contiguous bytes, and no workgroup ever
+// needs another's result.
+//
+// Per lane: the CW * JB weight chunks of a batch and the activations at the
+// same k are loaded back to back (activations straight from L1/L2 into
+// registers -- staging them in LDS costs a barrier, and the per-lane stride
+// of E floats makes LDS reads conflict), dequantized in registers and
+// accumulated into CW * MR dot products, which are reduced over the column
+// group with a reduce-scatter butterfly (plus LDS across waves when the
+// column group spans the workgroup).  Q8_0 / Q4_0 per-tensor scales are
+// folded into alpha.
+#include "tml_internal.hpp"
+
+namespace tml {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+typedef uint32_t uintx4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct GemvTArgs {
+    int M, N, K;
+    const float *A;
+    const uint8_t *Bt;
+    long long ldt;        // bytes per prepared row
+    const float *bias;
+    float *C;
+    float alpha, beta;
+    int nchunk;           // 16-byte chunks per prepared row
+    const void *zero;
+};
+
+template <int FMT> struct TElems;
+template <> struct TElems<TML_FMT_F32> { static constexpr int value = 4; };
+template <> struct TElems<TML_FMT_Q8_0> { static constexpr int value = 16; };
+template <> struct TElems<TML_FMT_Q4_0> { static constexpr int value = 32; };
+
+__device__ __forceinline__ float tsext8(uint32_t word, int byte) {
+    return (float)((int32_t)(word << (24 - 8 * byte)) >> 24);
+}
+__device__ __forceinline__ float tsext4(uint32_t word, int nib) {
+    return (float)((int32_t)(word << (28 - 4 * nib)) >> 28);
+}
+
+template <int FMT>
+__device__ __forceinline__ float telem(const uintx4 &w, int i) {
+    if constexpr (FMT == TML_FMT_F32) return __uint_as_float(w[i]);
+    else if constexpr (FMT == TML_FMT_Q8_0) return tsext8(w[i / 4], i % 4);
+    else return tsext4(w[i / 8], i % 8);
+}
+
+constexpr int tlog2(int v) { return v <= 1 ? 0 : 1 + tlog2(v / 2); }
+
+
+
+// LK lanes per column group (64: one wave, 256: the workgroup), CW outputs
+// per column group, JB chunks per lane per batch (two batches in flight).
+// XVEC: activations loaded as 16-byte vectors (K % 4 == 0, A 16-byte
+// aligned); otherwise element by element.
+template <int FMT, int MR, int LK, int CW, int JB, bool XVEC>
+__global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
+    constexpr int E = TElems<FMT>::value;
+    constexpr int GROUPS = kThreads / LK;       // column groups per workgroup
+    constexpr int V = CW * MR;                  // dot products per lane
+    constexpr int LOG_V = tlog2(V);
+    static_assert((1 << LOG_V) == V, "power-of-two dot products per lane");
+    __shared__ float red[kWaves * V];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int grp = tid / LK, lk = tid % LK;
+    const int n0 = (blockIdx.x * GROUPS + grp) * CW;
+
+    // One batch = JB chunks per lane: the 16-byte weight chunk of each of
+    // the CW outputs plus the E activations of every row m at those k, all
+    // loaded back to back before any arithmetic.  The activations come
+    // straight from global memory (L1/L2-resident: every workgroup reads the
+    // same x) and serve the CW outputs.  A chunk past the row reads the zero
+    // block for weights and activations alike (so a padded product is
+    // 0 * 0, never 0 * inf); inside the last chunk the weights are zero
+    // padded and activations past K are loaded as zeros.
+    const int nbat = (a.nchunk + LK * JB - 1) / (LK * JB);
+    uintx4 w0[CW][JB], w1[CW][JB];
+    floatx4 x0[JB][MR][E / 4], x1[JB][MR][E / 4];
+    auto load_batch = [&](uintx4 (*w)[JB], floatx4 (*x)[MR][E / 4], int bt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < CW; ++c)
+#pragma unroll
+            for (int j = 0; j < JB; ++j) {
+                const int ch = (bt * JB + j) * LK + lk;
+                const int n = n0 + c;
+                const bool in = ch < a.nchunk && n < a.N;
+                const uint8_t *p = in ? a.Bt + (size_t)n * a.ldt + (size_t)ch * 16 : (const uint8_t *)a.zero;
+                w[c][j] = *(const uintx4 *)p;
+            }
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+            const int ch = (bt * JB + j) * LK + lk;
+            const int k0 = ch * E;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const bool row_ok = ch < a.nchunk && m < a.M;
+                const float *xr = a.A + (size_t)m * a.K;
+#pragma unroll
+                for (int q = 0; q < E / 4; ++q) {
+                    const int k = k0 + 4 * q;
+                    if constexpr (XVEC) {
+                        const bool in = row_ok && k < a.K;  // K % 4 == 0: all four in or out
+                        x[j][m][q] = *(const floatx4 *)(in ? xr + k : (const float *)a.zero);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const bool in = row_ok && k + r < a.K;
+                            x[j][m][q][r] = *(in ? xr + k + r : (const float *)a.zero);
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+    auto compute_batch = [&](const uintx4 (*w)[JB], const floatx4 (*x)[MR][E / 4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < JB; ++j)
+#pragma unroll
+            for (int c = 0; c < CW; ++c) {
+                float wv[E];
+#pragma unroll
+                for (int e = 0; e < E; ++e) wv[e] = telem<FMT>(w[c][j], e);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float s0 = 0.0f, s1 = 0.0f;  // two chains halve the add latency
+#pragma unroll
+                    for (int e = 0; e < E; e += 2) {
+                        s0 += x[j][m][e / 4][e % 4] * wv[e];
+                        s1 += x[j][m][(e + 1) / 4][(e + 1) % 4] * wv[e + 1];
+                    }
+                    acc[c * MR + m] += s0 + s1;
+                }
+            }
+    };
+    load_batch(w0, x0, 0);
+    for (int bt = 0; bt < nbat; bt += 2) {
+        if (bt + 1 < nbat) load_batch(w1, x1, bt + 1);
+        compute_batch(w0, x0);
+        if (bt + 2 < nbat) load_batch(w0, x0, bt + 2);
+        if (bt + 1 < nbat) compute_batch(w1, x1);
+    }
+
+    // Reduce the V dot products over the 64 lanes of the wave: reduce-
+    // scatter while more than one value is left, then a butterfly.  After
+    // the loop lane l holds value `base` (plus V / 64 - 1 more when V > 64,
+    // which the shapes here never need).
+    int base = 0;
+#pragma unroll
+    for (int s = 0; s < 6; ++s) {
+        const int o = 1 << s;
+        const bool hi = (lane & o) != 0;
+        if (s < LOG_V) {
+            const int half = V >> (s + 1);
+#pragma unroll
+            for (int i = 0; i < half; ++i) {
+                const float send = hi ? acc[i] : acc[i + half];
+                const float keep = hi ? acc[i + half] : acc[i];
+                acc[i] = keep + __shfl_xor(send, o);
+            }
+            if (hi) base += half;
+        } else {
+            acc[0] += __shfl_xor(acc[0], o);
+        }
+    }
+    static_assert(V <= 64, "one value per lane after the wave reduction");
+    // Lanes whose bits above LOG_V are zero hold the V distinct sums.
+    const bool holder = (lane >> LOG_V) == 0;
+    float val = acc[0];
+    int idx = base;
+    if constexpr (LK > 64) {
+        if (holder) red[wave * V + idx] = val;
+        __syncthreads();
+        if (wave != 0 || !holder) return;
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) val += red[w * V + idx];
+    } else {
+        if (!holder) return;
+    }
+    const int c = idx / MR, m = idx % MR;
+    const int n = n0 + c;
+    if (m < a.M && n < a.N) {
+        float *cp = a.C + (size_t)m * a.N + n;
+        float v = a.alpha * val;
+        if (a.beta != 0.0f) v += a.beta * *cp;
+        if (a.bias) v += a.bias[n];
+        *cp = v;
+    }
+}
+
+// ---- prepare: Bt[n][j] from B[K,N] (one thread per output 32-bit word)
+template <int FMT>
+__global__ __launch_bounds__(256) void prepare_t_kernel(const void *B, int K, int N, long long ldt, uint32_t *Bt) {
+    const long long words_per_row = ldt / 4;
+    const long long total = (long long)N * words_per_row;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int n = (int)(i / words_per_row);
+        const long long wj = i % words_per_row;
+        uint32_t word = 0;
+        if constexpr (FMT == TML_FMT_F32) {
+            const long long k = wj;
+            if (k < K) word = ((const uint32_t *)B)[k * N + n];
+        } else if constexpr (FMT == TML_FMT_Q8_0) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const long long k = wj * 4 + b;
+                if (k < K) word |= (uint32_t)((const uint8_t *)B)[k * N + n] << (8 * b);
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const long long k = wj * 8 + h;
+                if (k < K) {
+                    const long long e = k * N + n;
+                    const uint32_t byte = ((const uint8_t *)B)[e / 2];
+                    word |= ((e & 1) ? (byte >> 4) : (byte & 0xF)) << (4 * h);
+                }
+            }
+        }
+        Bt[i] = word;
+    }
+}
+
+struct TPlan {
+    int lk, cw, jb;
+};
+
+// Column-group shape: one wave along K when a row has at most two waves'
+// worth of chunks, else the whole workgroup; outputs per group chosen so
+// the grid has at least ~one workgroup per CU.
+TPlan plan_t(int fmt, int64_t N, int64_t nchunk, int cus) {
+    TPlan p;
+    p.lk = nchunk <= 128 ? 64 : 256;
+    const int groups = kThreads / p.lk;
+    p.cw = 4;
+    while (p.cw > 1 && (N + (int64_t)groups * p.cw - 1) / ((int64_t)groups * p.cw) < cus) p.cw /= 2;
+    const int64_t per_lane = (nchunk + p.lk - 1) / p.lk;
+    p.jb = per_lane >= 4 ? 4 : (per_lane >= 2 ? 2 : 1);  // capped per format at launch
+    const int forced_lk = env_int("TML_GEMVT_LK", 0), forced_cw = env_int("TML_GEMVT_CW", 0),
+              forced_jb = env_int("TML_GEMVT_JB", 0);
+    if (forced_lk == 64 || forced_lk == 256) p.lk = forced_lk;
+    if (forced_cw == 1 || forced_cw == 2 || forced_cw == 4) p.cw = forced_cw;
+    if (forced_jb == 1 || forced_jb == 2 || forced_jb == 4) p.jb = forced_jb;
+    return p;
+}
+
+template <int FMT, int MR, int LK, int CW, int JB>
+void launch_t4(const GemvTArgs &ka, unsigned grid, bool xvec, hipStream_t s) {
+    if (xvec) gemv_t_kernel<FMT, MR, LK, CW, JB, true><<<dim3(grid), dim3(kThreads), 0, s>>>(ka);
+    else gemv_t_kernel<FMT, MR, LK, CW, JB, false><<<dim3(grid), dim3(kThreads), 0, s>>>(ka);
+}
+// Batches are capped so that the two in-flight batches of activations stay
+// within ~128 registers: JB * MR * E <= 64.
+template <int FMT, int MR>
+constexpr int jb_max() {
+    return TElems<FMT>::value * MR <= 16 ? 4 : (TElems<FMT>::value * MR <= 32 ? 2 : 1);
+}
+template <int FMT, int MR, int LK, int CW>
+void launch_t3(const GemvTArgs &ka, const TPlan &p, unsigned grid, bool xvec, hipStream_t s) {
+    constexpr int JM = jb_max<FMT, MR>();
+    const int jb = p.jb < JM ? p.jb : JM;
+    if (jb >= 4) launch_t4<FMT, MR, LK, CW, (JM >= 4 ? 4 : JM)>(ka, grid, xvec, s);
+    else if (jb >= 2) launch_t4<FMT, MR, LK, CW, (JM >= 2 ? 2 : 1)>(ka, grid, xvec, s);
+    else launch_t4<FMT, MR, LK, CW, 1>(ka, grid, xvec, s);
+}
+template <int FMT, int MR, int LK>
+void launch_t2(const GemvTArgs &ka, const TPlan &p, unsigned grid, bool xvec, hipStream_t s) {
+    switch (p.cw) {
+        case 1: launch_t3<FMT, MR, LK, 1>(ka, p, grid, xvec, s); break;
+        case 2: launch_t3<FMT, MR, LK, 2>(ka, p, grid, xvec, s); break;
+        default: launch_t3<FMT, MR, LK, 4>(ka, p, grid, xvec, s); break;
+    }
+}
+template <int FMT, int MR>
+void launch_t1(const GemvTArgs &ka, const TPlan &p, unsigned grid, bool xvec, hipStream_t s) {
+    if (p.lk == 64) launch_t2<FMT, MR, 64>(ka, p, grid, xvec, s);
+    else launch_t2<FMT, MR, 256>(ka, p, grid, xvec, s);
+}
+template <int FMT>
+void launch_t0(const GemvTArgs &ka, const TPlan &p, unsigned grid, bool xvec, hipStream_t s) {
+    constexpr int E = TElems<FMT>::value;
+    if (ka.M <= 1) launch_t1<FMT, 1>(ka, p, grid, xvec, s);
+    else if (ka.M <= 2) launch_t1<FMT, 2>(ka, p, grid, xvec, s);
+    else if constexpr (E * 4 <= 64) {
+        if (ka.M <= 4) launch_t1<FMT, 4>(ka, p, grid, xvec, s);
+        else if constexpr (E * 8 <= 64) launch_t1<FMT, 8>(ka, p, grid, xvec, s);
+    }
+}
+
+int t_elems(int fmt) { return fmt == TML_FMT_F32 ? 4 : (fmt == TML_FMT_Q8_0 ? 16 : 32); }
+
+}  // namespace
+
+int64_t prepared_row_bytes(int fmt, int64_t K) {
+    const int64_t bytes = fmt == TML_FMT_F32 ? 4 * K : (fmt == TML_FMT_Q4_0 ? (K + 1) / 2 : K);
+    const int64_t r = (bytes + 15) / 16 * 16;
+    return r > 0 ? r : 16;
+}
+
+bool prepared_gemv_supported(int fmt, int64_t M, int64_t K) {
+    if (fmt != TML_FMT_F32 && fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0) return false;
+    if (M < 1 || M > kPreparedGemvMaxM || K >= ((int64_t)1 << 30)) return false;
+    // rows are padded to a power of two; their activations for one chunk
+    // must fit the register budget: MR * E <= 64 (f32 any M <= 8, Q8_0
+    // M <= 4, Q4_0 M <= 2)
+    const int64_t mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    return mr * t_elems(fmt) <= 64;
+}
+
+Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, int64_t ldt, hipStream_t s) {
+    if (ldt % 16 != 0 || ldt < prepared_row_bytes(fmt, K))
+        return Status::Err(TML_ERR_INVALID_ARG, "prepared row stride too small");
+    const long long words = (long long)N * (ldt / 4);
+    const long long blocks = (words + 255) / 256;
+    const dim3 grid((unsigned)(blocks < 65535 ? (blocks > 0 ? blocks : 1) : 65535));
+    switch (fmt) {
+        case TML_FMT_F32: prepare_t_kernel<TML_FMT_F32><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
+        case TML_FMT_Q8_0: prepare_t_kernel<TML_FMT_Q8_0><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
+        case TML_FMT_Q4_0: prepare_t_kernel<TML_FMT_Q4_0><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
+        default: return Status::Err(TML_ERR_INVALID_FORMAT, "prepared layout: format must be F32, Q8_0 or Q4_0");
+    }
+    TML_HIP_TRY(hipGetLastError());
+    return Status::Ok();
+}
+
+Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
+                     const float *bias, float *C, float alpha_eff, float beta, const void *zero, hipStream_t s) {
+    if (!prepared_gemv_supported(fmt, M, K)) return Status::Err(TML_ERR_INVALID_ARG, "prepared GEMV: unsupported");
+    if (N >= ((int64_t)1 << 30) || K >= ((int64_t)1 << 30))
+        return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV dimension exceeds 2^30");
+    if (ldt < prepared_row_bytes(fmt, K) || ldt % 16 != 0 || ((uintptr_t)Bt % 16) != 0)
+        return Status::Err(TML_ERR_INVALID_ARG, "prepared weight layout");
+    GemvTArgs ka;
+    ka.M = (int)M; ka.N = (int)N; ka.K = (int)K;
+    ka.A = A; ka.Bt = (const uint8_t *)Bt; ka.ldt = ldt;
+    ka.bias = bias; ka.C = C; ka.alpha = alpha_eff; ka.beta = beta;
+    ka.nchunk = (int)((prepared_row_bytes(fmt, K) + 15) / 16);
+    ka.zero = zero;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+    }
+    const TPlan p = plan_t(fmt, N, ka.nchunk, cus);
+    const int groups = kThreads / p.lk;
+    const int64_t outs_per_wg = (int64_t)groups * p.cw;
+    const int64_t grid = (N + outs_per_wg - 1) / outs_per_wg;
+    if (grid >= ((int64_t)1 << 31)) return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV grid too large");
+    const bool xvec = (K % 4 == 0) && ((uintptr_t)A % 16 == 0);
+    switch (fmt) {
+        case TML_FMT_F32: launch_t0<TML_FMT_F32>(ka, p, (unsigned)grid, xvec, s); break;
+        case TML_FMT_Q8_0: launch_t0<TML_FMT_Q8_0>(ka, p, (unsigned)grid, xvec, s); break;
+        default: launch_t0<TML_FMT_Q4_0>(ka, p, (unsigned)grid, xvec, s); break;
+    }
+    TML_HIP_TRY(hipGetLastError());
+    return Status::Ok();
+}
+
+}  // namespace tml

@@ -59,9 +59,23 @@ struct DevBuf {
     }
 };
 
+// Device-native copy of a weight for decoder GEMVs (gemv_t.hip).  `B` is
+// the [K,N] weight the copy was made from; it is used for row counts the
+// prepared kernel does not cover.
+struct Prepared {
+    int device = -1;
+    int fmt = 0;
+    int64_t K = 0, N = 0;
+    float scale = 1.0f;
+    const void *B = nullptr;
+    void *Bt = nullptr;
+    int64_t ldt = 0;
+};
+
 struct Registered {
     void *dev = nullptr;
     size_t bytes = 0;
+    Prepared *prep = nullptr;  // made on the first decoder call that uses this weight
 };
 
 struct DeviceCtx {
@@ -170,6 +184,54 @@ Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const fl
     return launch_gemm_mfma(m, ws, s);
 }
 
+bool preparable_fmt(int fmt) { return fmt == TML_FMT_F32 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0; }
+
+// Builds the prepared copy of the [K,N] device weight B (asynchronous on s).
+Status make_prepared(DeviceCtx *c, int fmt, int64_t K, int64_t N, const void *B, float scale, hipStream_t s,
+                     Prepared **out) {
+    if (!preparable_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, Q8_0 or Q4_0");
+    if (K < 0 || N < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
+    if (K >= ((int64_t)1 << 30) || N >= ((int64_t)1 << 30))
+        return Status::Err(TML_ERR_INVALID_SHAPE, "prepare: dimension exceeds 2^30");
+    if (B == nullptr && K > 0 && N > 0) return Status::Err(TML_ERR_INVALID_ARG, "null weight pointer");
+    Prepared *p = new Prepared();
+    p->device = c->device;
+    p->fmt = fmt;
+    p->K = K;
+    p->N = N;
+    p->scale = scale;
+    p->B = B;
+    p->ldt = prepared_row_bytes(fmt, K);
+    const size_t bytes = (size_t)(N > 0 ? N : 1) * (size_t)p->ldt;
+    hipError_t e = hipMalloc(&p->Bt, bytes);
+    if (e != hipSuccess) {
+        delete p;
+        return hip_status(e, "hipMalloc(prepared weight)");
+    }
+    Status st = N > 0 ? launch_prepare_t(fmt, K, N, B, p->Bt, p->ldt, s) : Status::Ok();
+    if (!st.ok()) {
+        (void)hipFree(p->Bt);
+        delete p;
+        return st;
+    }
+    *out = p;
+    return Status::Ok();
+}
+
+// C = alpha * A . dequant(B) + beta * C + bias with a prepared weight: the
+// K-contiguous decoder kernel when it covers M and K, else the [K,N] path.
+Status gemm_prepared(DeviceCtx *c, const Prepared *p, int64_t M, const float *A, const float *bias, float *C,
+                     float alpha, float beta, hipStream_t s) {
+    if (M < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
+    if (M == 0 || p->N == 0) return Status::Ok();
+    if (C == nullptr || (p->K > 0 && A == nullptr)) return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
+    if (prepared_gemv_supported(p->fmt, M, p->K)) {
+        const float alpha_eff = (p->fmt == TML_FMT_Q8_0 || p->fmt == TML_FMT_Q4_0) ? alpha * p->scale : alpha;
+        return launch_gemv_t(p->fmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, C, alpha_eff, beta, c->zero.p, s);
+    }
+    return gemm_dev(c, p->fmt, M, p->N, p->K, A, p->B, p->scale, nullptr, 0, bias, C, alpha, beta, s);
+}
+
 // Resident copy of a registered host buffer of at least `bytes`, or null.
 const void *resident(DeviceCtx *c, const void *host, size_t bytes) {
     auto it = c->weights.find(host);
@@ -215,8 +277,31 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
     const size_t cbytes = (size_t)M * N * sizeof(float);
     TML_TRY(c->c.ensure(cbytes));
     if (beta != 0.0f) TML_HIP_TRY(hipMemcpyAsync(c->c.p, C, cbytes, hipMemcpyHostToDevice, c->stream));
-    TML_TRY(gemm_dev(c, fmt, M, N, K, (const float *)dA, dB, scale, (const float *)dS, block,
-                     (const float *)dBias, (float *)c->c.p, alpha, beta, c->stream));
+    // A registered weight used at a decoder row count gets (once) and then
+    // uses its prepared, K-contiguous copy.
+    Registered *reg = nullptr;
+    if (preparable_fmt(fmt) && prepared_gemv_supported(fmt, M, K)) {
+        auto it = c->weights.find(B);
+        if (it != c->weights.end() && it->second.bytes >= weight_bytes(fmt, K, N)) reg = &it->second;
+    }
+    if (reg) {
+        Prepared *p = reg->prep;
+        if (p && (p->fmt != fmt || p->K != K || p->N != N || p->scale != scale)) {
+            TML_HIP_TRY(hipStreamSynchronize(c->stream));
+            TML_HIP_TRY(hipFree(p->Bt));
+            delete p;
+            p = reg->prep = nullptr;
+        }
+        if (!p) {
+            TML_TRY(make_prepared(c, fmt, K, N, reg->dev, scale, c->stream, &p));
+            reg->prep = p;
+        }
+        TML_TRY(gemm_prepared(c, p, M, (const float *)dA, (const float *)dBias, (float *)c->c.p, alpha, beta,
+                              c->stream));
+    } else {
+        TML_TRY(gemm_dev(c, fmt, M, N, K, (const float *)dA, dB, scale, (const float *)dS, block,
+                         (const float *)dBias, (float *)c->c.p, alpha, beta, c->stream));
+    }
     TML_HIP_TRY(hipMemcpyAsync(C, c->c.p, cbytes, hipMemcpyDeviceToHost, c->stream));
     TML_HIP_TRY(hipStreamSynchronize(c->stream));
     return Status::Ok();
@@ -262,7 +347,11 @@ void tml_hip_shutdown(void) {
         (void)hipGetDevice(&prev);
         (void)hipSetDevice(c->device);
         (void)hipDeviceSynchronize();
-        for (auto &w : c->weights) (void)hipFree(w.second.dev);
+        for (auto &w : c->weights) {
+            if (w.second.prep) (void)hipFree(w.second.prep->Bt);
+            delete w.second.prep;
+            (void)hipFree(w.second.dev);
+        }
         c->a.release(); c->b.release(); c->c.release(); c->bias.release();
         c->scales.release(); c->qtmp.release(); c->ws.release(); c->counters.release();
         c->zero.release();
@@ -356,11 +445,19 @@ int tml_hip_weight_register(const void *host, size_t bytes) {
     if (!s.ok()) return report(s);
     auto run = [&]() -> Status {
         auto it = c->weights.find(host);
-        if (it != c->weights.end() && it->second.bytes != bytes) {
+        if (it != c->weights.end()) {
+            // a refreshed weight invalidates its prepared copy
             TML_HIP_TRY(hipStreamSynchronize(c->stream));
-            TML_HIP_TRY(hipFree(it->second.dev));
-            c->weights.erase(it);
-            it = c->weights.end();
+            if (it->second.prep) {
+                TML_HIP_TRY(hipFree(it->second.prep->Bt));
+                delete it->second.prep;
+                it->second.prep = nullptr;
+            }
+            if (it->second.bytes != bytes) {
+                TML_HIP_TRY(hipFree(it->second.dev));
+                c->weights.erase(it);
+                it = c->weights.end();
+            }
         }
         if (it == c->weights.end()) {
             Registered r;
@@ -383,6 +480,10 @@ int tml_hip_weight_release(const void *host) {
     if (it == c->weights.end()) return report(Status::Err(TML_ERR_INVALID_ARG, "weight not registered"));
     auto run = [&]() -> Status {
         TML_HIP_TRY(hipStreamSynchronize(c->stream));
+        if (it->second.prep) {
+            TML_HIP_TRY(hipFree(it->second.prep->Bt));
+            delete it->second.prep;
+        }
         TML_HIP_TRY(hipFree(it->second.dev));
         c->weights.erase(it);
         return Status::Ok();
@@ -397,6 +498,43 @@ int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     Status s = current_ctx(&c);
     if (!s.ok()) return report(s);
     return report(gemm_dev(c, fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, (hipStream_t)stream));
+}
+
+int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scale, void *stream,
+                        tml_prepared_t *out) {
+    if (out == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null handle pointer"));
+    *out = nullptr;
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    Prepared *p = nullptr;
+    s = make_prepared(c, fmt, K, N, B, scale, (hipStream_t)stream, &p);
+    if (s.ok()) *out = (tml_prepared_t)p;
+    return report(s);
+}
+
+int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const float *bias, float *C, float alpha,
+                          float beta, void *stream) {
+    if (w == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null prepared weight"));
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    const Prepared *p = (const Prepared *)w;
+    if (p->device != c->device) return report(Status::Err(TML_ERR_INVALID_ARG, "prepared weight of another device"));
+    return report(gemm_prepared(c, p, M, A, bias, C, alpha, beta, (hipStream_t)stream));
+}
+
+int tml_hip_prepared_free(tml_prepared_t w) {
+    if (w == nullptr) return report(Status::Ok());
+    Prepared *p = (Prepared *)w;
+    auto run = [&]() -> Status {
+        TML_HIP_TRY(hipDeviceSynchronize());
+        TML_HIP_TRY(hipFree(p->Bt));
+        return Status::Ok();
+    };
+    Status s = run();
+    delete p;
+    return report(s);
 }
 
 int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream) {

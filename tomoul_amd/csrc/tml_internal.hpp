@@ -127,6 +127,16 @@ size_t quantize_tmp_floats(int fmt, int64_t n);
 // Largest M routed to the GEMV family (skinny decoder shapes).
 constexpr int64_t kGemvMaxM = 8;
 
+// Prepared (device-native, K-contiguous) weights for decoder GEMVs
+// (gemv_t.hip): row n holds column n of B, zero padded to a multiple of 16
+// bytes; int4 keeps two k per byte, even k in the low nibble.
+constexpr int64_t kPreparedGemvMaxM = 8;  // f32; Q8_0 <= 4, Q4_0 <= 2 (prepared_gemv_supported)
+int64_t prepared_row_bytes(int fmt, int64_t K);
+bool prepared_gemv_supported(int fmt, int64_t M, int64_t K);
+Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, int64_t ldt, hipStream_t s);
+Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
+                     const float *bias, float *C, float alpha_eff, float beta, const void *zero, hipStream_t s);
+
 // Tuning overrides for experiments (0 = heuristic).  Read from the
 // TML_GEMM_TILE / TML_GEMV_SPLIT environment variables once.
 int env_int(const char *name, int dflt);
