@@ -489,7 +489,7 @@ def test_prepared_vs_oracle(orc, k, n, m):
         assert err <= tol, (fmt, err)
 
 
-@pytest.mark.parametrize("lk", [64, 256])
+@pytest.mark.parametrize("lk", [16, 64, 256])
 @pytest.mark.parametrize("cw", [1, 2, 4])
 @pytest.mark.parametrize("jb", [1, 2, 4])
 def test_prepared_plan_variants(orc, lk, cw, jb):
@@ -499,7 +499,7 @@ def test_prepared_plan_variants(orc, lk, cw, jb):
     try:
         k, n = 1500, 70
         w = rnd(151, k, n, 0.02)
-        for m in (1, 2):
+        for m in (1, 2, 3, 7):
             a = rnd(152 + m, m, k)
             for fmt, b, scale, ref, tol in _prepared_cases(orc, w, k, n, a):
                 assert rel_err(_run_prepared(fmt, b, scale, k, n, m, a), ref) <= tol, (fmt, m)

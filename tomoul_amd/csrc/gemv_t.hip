@@ -70,9 +70,16 @@ __device__ __forceinline__ float telem(const uintx4 &w, int i) {
 
 constexpr int tlog2(int v) { return v <= 1 ? 0 : 1 + tlog2(v / 2); }
 
+// v of the lane selected by the DPP control CTRL within the 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
 
 
-// LK lanes per column group (64: one wave, 256: the workgroup), CW outputs
+
+// LK lanes per column group (16: a DPP row, 64: a wave, 256: the
+// workgroup), CW outputs
 // per column group, JB chunks per lane per batch (two batches in flight).
 // XVEC: activations loaded as 16-byte vectors (K % 4 == 0, A 16-byte
 // aligned); otherwise element by element.
@@ -83,6 +90,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
     constexpr int V = CW * MR;                  // dot products per lane
     constexpr int LOG_V = tlog2(V);
     static_assert((1 << LOG_V) == V, "power-of-two dot products per lane");
+    static_assert(V <= (LK < 64 ? LK : 64), "one published dot product per lane of the group");
     __shared__ float red[kWaves * V];
 
     const int tid = threadIdx.x;
@@ -169,41 +177,39 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
         if (bt + 1 < nbat) compute_batch(w1, x1);
     }
 
-    // Reduce the V dot products over the 64 lanes of the wave: reduce-
-    // scatter while more than one value is left, then a butterfly.  After
-    // the loop lane l holds value `base` (plus V / 64 - 1 more when V > 64,
-    // which the shapes here never need).
-    int base = 0;
+    // All-reduce the V dot products over the LK lanes of the column group:
+    // DPP within the 16-lane row (quad swaps, half mirror, mirror -- one VALU
+    // op each), then xor 16 (ds_swizzle) and xor 32 across the rows of the
+    // wave, then LDS across the waves when the group spans the workgroup.
+    // Each step adds two disjoint partial sums and both partners compute the
+    // same a + b, so every lane ends with bitwise identical totals.
 #pragma unroll
-    for (int s = 0; s < 6; ++s) {
-        const int o = 1 << s;
-        const bool hi = (lane & o) != 0;
-        if (s < LOG_V) {
-            const int half = V >> (s + 1);
-#pragma unroll
-            for (int i = 0; i < half; ++i) {
-                const float send = hi ? acc[i] : acc[i + half];
-                const float keep = hi ? acc[i + half] : acc[i];
-                acc[i] = keep + __shfl_xor(send, o);
-            }
-            if (hi) base += half;
-        } else {
-            acc[0] += __shfl_xor(acc[0], o);
+    for (int i = 0; i < V; ++i) {
+        float v = acc[i];
+        v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+        v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+        v += dpp_mov<0x141>(v);  // row_half_mirror
+        v += dpp_mov<0x140>(v);  // row_mirror
+        if constexpr (LK >= 64) {
+            v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+            v += __shfl_xor(v, 32);
         }
+        acc[i] = v;
     }
-    static_assert(V <= 64, "one value per lane after the wave reduction");
-    // Lanes whose bits above LOG_V are zero hold the V distinct sums.
-    const bool holder = (lane >> LOG_V) == 0;
+    // Lane lk < V of the group publishes dot product lk.
     float val = acc[0];
-    int idx = base;
-    if constexpr (LK > 64) {
-        if (holder) red[wave * V + idx] = val;
-        __syncthreads();
-        if (wave != 0 || !holder) return;
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) val += red[w * V + idx];
+    for (int i = 1; i < V; ++i)
+        if (lk % 64 == i) val = acc[i];
+    const int idx = lk % 64;
+    if constexpr (LK > 64) {
+        if (lane < V) red[wave * V + lane] = val;
+        __syncthreads();
+        if (wave != 0 || lane >= V) return;
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) val += red[w * V + lane];
     } else {
-        if (!holder) return;
+        if (idx >= V) return;
     }
     const int c = idx / MR, m = idx % MR;
     const int n = n0 + c;
@@ -254,22 +260,38 @@ struct TPlan {
     int lk, cw, jb;
 };
 
-// Column-group shape: one wave along K when a row has at most two waves'
-// worth of chunks, else the whole workgroup; outputs per group chosen so
-// the grid has at least ~one workgroup per CU.
-TPlan plan_t(int fmt, int64_t N, int64_t nchunk, int cus) {
+// Column-group shape, from sweeps on MI355X:
+//  * LK: at decoder sizes (latency-bound) every chunk gets its own lane --
+//    one wave per group up to two waves' worth of chunks, else the whole
+//    workgroup, fewer rows per wave for M > 2; once the weight streams tens
+//    of MB (bandwidth-bound, e.g. a vocabulary projection), short rows
+//    (<= 48 chunks) go to 16-lane groups, which waste no lanes and reduce
+//    with DPP alone.
+//  * CW: the most outputs per group (<= 4) that still gives one workgroup
+//    per CU, with CW * MR <= 16 dot products per lane.
+//  * JB = 1: one chunk per lane per batch; the batch loop keeps two in
+//    flight (larger batches cost registers and occupancy).
+TPlan plan_t(int fmt, int64_t M, int64_t N, int64_t nchunk, int cus) {
     TPlan p;
-    p.lk = nchunk <= 128 ? 64 : 256;
+    const int mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    const double weight_bytes = (double)N * (double)nchunk * 16.0;
+    if (weight_bytes > 32.0e6 && nchunk <= 48) p.lk = 16;
+    else if (nchunk <= 128 || mr > 2) p.lk = 64;
+    else p.lk = 256;
     const int groups = kThreads / p.lk;
     p.cw = 4;
     while (p.cw > 1 && (N + (int64_t)groups * p.cw - 1) / ((int64_t)groups * p.cw) < cus) p.cw /= 2;
-    const int64_t per_lane = (nchunk + p.lk - 1) / p.lk;
-    p.jb = per_lane >= 4 ? 4 : (per_lane >= 2 ? 2 : 1);  // capped per format at launch
+    while (p.cw > 1 && p.cw * mr > 16) p.cw /= 2;
+    p.jb = 1;
+    (void)fmt;
     const int forced_lk = env_int("TML_GEMVT_LK", 0), forced_cw = env_int("TML_GEMVT_CW", 0),
               forced_jb = env_int("TML_GEMVT_JB", 0);
-    if (forced_lk == 64 || forced_lk == 256) p.lk = forced_lk;
+    if (forced_lk == 16 || forced_lk == 64 || forced_lk == 256) p.lk = forced_lk;
     if (forced_cw == 1 || forced_cw == 2 || forced_cw == 4) p.cw = forced_cw;
     if (forced_jb == 1 || forced_jb == 2 || forced_jb == 4) p.jb = forced_jb;
+    // a 16-lane group publishes at most 16 dot products: CW * MR <= 16
+    if (p.lk == 16)
+        while (p.cw > 1 && p.cw * mr > 16) p.cw /= 2;
     return p;
 }
 
@@ -294,15 +316,21 @@ void launch_t3(const GemvTArgs &ka, const TPlan &p, unsigned grid, bool xvec, hi
 }
 template <int FMT, int MR, int LK>
 void launch_t2(const GemvTArgs &ka, const TPlan &p, unsigned grid, bool xvec, hipStream_t s) {
+    // plan_t keeps CW * MR <= 16 for 16-lane groups
     switch (p.cw) {
         case 1: launch_t3<FMT, MR, LK, 1>(ka, p, grid, xvec, s); break;
-        case 2: launch_t3<FMT, MR, LK, 2>(ka, p, grid, xvec, s); break;
-        default: launch_t3<FMT, MR, LK, 4>(ka, p, grid, xvec, s); break;
+        case 2:
+            if constexpr (LK != 16 || 2 * MR <= 16) launch_t3<FMT, MR, LK, 2>(ka, p, grid, xvec, s);
+            break;
+        default:
+            if constexpr (LK != 16 || 4 * MR <= 16) launch_t3<FMT, MR, LK, 4>(ka, p, grid, xvec, s);
+            break;
     }
 }
 template <int FMT, int MR>
 void launch_t1(const GemvTArgs &ka, const TPlan &p, unsigned grid, bool xvec, hipStream_t s) {
-    if (p.lk == 64) launch_t2<FMT, MR, 64>(ka, p, grid, xvec, s);
+    if (p.lk == 16) launch_t2<FMT, MR, 16>(ka, p, grid, xvec, s);
+    else if (p.lk == 64) launch_t2<FMT, MR, 64>(ka, p, grid, xvec, s);
     else launch_t2<FMT, MR, 256>(ka, p, grid, xvec, s);
 }
 template <int FMT>
@@ -370,7 +398,7 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
     }
-    const TPlan p = plan_t(fmt, N, ka.nchunk, cus);
+    const TPlan p = plan_t(fmt, M, N, ka.nchunk, cus);
     const int groups = kThreads / p.lk;
     const int64_t outs_per_wg = (int64_t)groups * p.cw;
     const int64_t grid = (N + outs_per_wg - 1) / outs_per_wg;
