@@ -61,6 +61,8 @@ def parse():
                    help="only warm up and run the timed headline steps (for rocprofv3 runs)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run a plain 256 MiB device copy 5 times (scale for FETCH_SIZE / WRITE_SIZE)")
+    p.add_argument("--profile-gemv", action="store_true",
+                   help="only run the decoder GEMVs (configs 3/4, M = 1) 50 times per path, eagerly, for rocprofv3")
     return p.parse_args()
 
 
@@ -133,6 +135,10 @@ def main():
     def step(st=sptr):
         for (_, _, _, _, fn) in launches:
             fn(st)
+
+    if args.profile_gemv:
+        profile_gemv(torch, dev, sptr, _abi, synth)
+        return
 
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -228,6 +234,7 @@ def main():
         result["gemv"] = bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np)
         result["qgemm"] = bench_qgemm(torch, dev, sptr, timer, _abi, synth, np)
         result["config1"] = bench_config1(torch, dev, sptr, timer, _abi, synth, np)
+        result["config5"] = bench_config5(torch, dev, sptr, _abi)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
@@ -344,6 +351,104 @@ def bench_config1(torch, dev, sptr, timer, _abi, synth, np):
     tf = 2.0 * 1500 * 1536 * 384 / ms / 1e9
     log(f"config1: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
     return {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+
+
+def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
+    """Decoder GEMVs at M = 1 for kernel traces / counters: Q8_0 1024x4096,
+    Q4_0 1280x5120 and 5120x1280, each on its prepared copy and in the [K,N]
+    layout, `launches` times over 16 distinct weight copies (eager launches,
+    one kernel per call)."""
+    for fmt, K, N in ((_abi.FMT_Q8_0, 1024, 4096), (_abi.FMT_Q4_0, 1280, 5120), (_abi.FMT_Q4_0, 5120, 1280)):
+        w = torch.from_numpy(synth.normal_matrix(2002, K, N, 0.02)).to(dev)
+        nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+        q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        sc = torch.empty(1, dtype=torch.float32, device=dev)
+        _abi.quantize_dev(fmt, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
+        torch.cuda.synchronize()
+        scale = float(sc.item())
+        copies = q.repeat(16).view(16, nbytes)
+        hs = [_abi.prepare_dev(fmt, K, N, copies[i].data_ptr(), scale, sptr) for i in range(16)]
+        x = torch.from_numpy(synth.normal_matrix(1001, 1, K)).to(dev)
+        y = torch.empty((1, N), dtype=torch.float32, device=dev)
+        for i in range(launches):
+            _abi.gemm_prepared(hs[i % 16], 1, x.data_ptr(), y.data_ptr(), stream=sptr)
+        for i in range(launches):
+            _abi.gemm_dev(fmt, 1, N, K, x.data_ptr(), copies[i % 16].data_ptr(), y.data_ptr(), scale=scale,
+                          stream=sptr)
+        torch.cuda.synchronize()
+        for h_ in hs:
+            _abi.prepared_free(h_)
+        log(f"profile-gemv: fmt {fmt} {K}x{N}: {launches} prepared + {launches} [K,N] launches")
+    print(json.dumps({"profile_gemv": True}), flush=True)
+
+
+def bench_config5(torch, dev, sptr, _abi, layers: int = 32):
+    """Config 5: the Whisper large-v3-turbo encoder linears at 1500 frames --
+    X[1500x1280] . W[1280x3840] (fused QKV), X . W[1280x5120] (FFN up),
+    H[1500x5120] . W[5120x1280] (FFN down) -- for each of `layers` layers with
+    their own weights, back to back, in fp32 and as Q8_0 / Q4_0 weights
+    (quantized on the device by the reference quantizer).  Weights are drawn
+    on the GPU (seeded N(0, 0.02)); X, H ~ N(0, 1).  The fp32 sweep streams
+    2.3 GB of weights, more than the 256 MB Infinity Cache."""
+    shapes = [(1500, 3840, 1280), (1500, 5120, 1280), (1500, 1280, 5120)]
+    flops = layers * sum(2.0 * M * N * K for (M, N, K) in shapes)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1001)
+    x = torch.randn(1500, 1280, generator=g, device=dev)
+    h = torch.randn(1500, 5120, generator=g, device=dev)
+    outs = [torch.empty(M, N, device=dev) for (M, N, K) in shapes]
+    res = {}
+    for fmt, name in ((_abi.FMT_F32, "fp32"), (_abi.FMT_Q8_0, "q8_0"), (_abi.FMT_Q4_0, "q4_0")):
+        weights = []  # per layer: [(ptr, scale)] and the tensors that own them
+        keep = []
+        for layer in range(layers):
+            g.manual_seed(2002 + layer)
+            row = []
+            for (M, N, K) in shapes:
+                w = torch.randn(K, N, generator=g, device=dev) * 0.02
+                if fmt == _abi.FMT_F32:
+                    keep.append(w)
+                    row.append((w.data_ptr(), 1.0))
+                    continue
+                nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+                q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+                sc = torch.empty(1, dtype=torch.float32, device=dev)
+                _abi.quantize_dev(fmt, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
+                keep.append((q, sc))
+                row.append((q.data_ptr(), sc))
+                del w
+            weights.append(row)
+        torch.cuda.synchronize()
+        weights = [[(p, s if isinstance(s, float) else float(s.item())) for (p, s) in row] for row in weights]
+
+        def sweep():
+            for row in weights:
+                for i, (M, N, K) in enumerate(shapes):
+                    a = x if K == 1280 else h
+                    p, sc = row[i]
+                    _abi.gemm_dev(fmt, M, N, K, a.data_ptr(), p, outs[i].data_ptr(), scale=sc, stream=sptr)
+
+        sweep()  # warm-up (workspaces, clocks)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 3
+        e0.record()
+        for _ in range(reps):
+            sweep()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        tf = flops / (ms * 1e-3) / 1e12
+        wbytes = sum((K * N * 4 if fmt == _abi.FMT_F32 else (K * N if fmt == _abi.FMT_Q8_0 else K * N // 2))
+                     for (M, N, K) in shapes) * layers
+        res[name] = {"ms_per_sweep": round(ms, 3), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4),
+                     "weight_bytes": wbytes}
+        log(f"config5 {name}: {layers} layers, {ms:.2f} ms/sweep, {tf:.1f} TFLOP/s")
+        del keep, weights
+        torch.cuda.empty_cache()
+    res["flops_per_sweep"] = flops
+    res["layers"] = layers
+    return res
 
 
 def cpu_baseline(budget_s: float):
