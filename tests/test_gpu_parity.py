@@ -314,7 +314,7 @@ def forced_env():
             os.environ[k] = v
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("split", [1, 2, 3, 8])
 def test_sgemm_dma_tiles_and_splits(orc, forced_env, tile, split):
     # Every tile config of the direct-copy kernel with K split 1-8 ways,

@@ -24,7 +24,8 @@
 // Compute: v_mfma_f32_16x16x4_f32, fp32 accumulation; lane l feeds A[l%16][kk]
 // and B[kk][l%16] with kk = l/16 and holds D[4*(l/16)+r][l%16] in register r;
 // within a 16-deep chunk, step s feeds the physical k = 4*kk + s.  Fragment
-// reads run one chunk ahead of the MFMAs, and the last chunk of a slice is
+// reads run one chunk ahead of the MFMAs and are issued between the two
+// halves of the current chunk's MFMAs; the last chunk of a slice is
 // multiplied after the barrier so that it covers the first reads of the next.
 #include <type_traits>
 
@@ -36,7 +37,6 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kNumXcd = 8;
-constexpr int kBK = kDmaBK;  // slice depth (two 16-deep MFMA chunks)
 
 struct DmaArgs {
     int M, N, K;
@@ -72,23 +72,23 @@ __device__ __forceinline__ void raw_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int WM, int WN, int NW, int NS>
+template <int BM, int BN, int BK, int WM, int WN, int NW, int NS>
 __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
     static_assert(NS == 3 || NS == 4, "3 or 4 LDS stages");
-    constexpr int BK = kBK;
+    static_assert(BK == 32 || BK == 64, "slice depth");
     constexpr int NC = BK / 16;
     constexpr int WAVES_N = BN / WN;
     constexpr int TM = WM / 16, TN = WN / 16;
     static_assert((BM / WM) * (BN / WN) == NW, "one wave per WM x WN sub-tile");
-    static_assert(NC == 2, "fragment double-buffering assumes two chunks per slice");
+    static_assert(NC % 2 == 0, "fragment double-buffering alternates two buffers over the chunks");
     // 1 KiB copy blocks per stage and their shapes.
-    constexpr int SLOTS_A = BK / 4;             // 16-byte slots per A row (8)
-    constexpr int ROWS_A = 64 / SLOTS_A;        // A rows per copy block (8)
+    constexpr int SLOTS_A = BK / 4;             // 16-byte slots per A row (8 or 16)
+    constexpr int ROWS_A = 64 / SLOTS_A;        // A rows per copy block (8 or 4)
     constexpr int BLKS_A = BM * BK / 256;       // copy blocks per A stage
     constexpr int SLOTS_B = BN / 4;             // 16-byte slots per B k-row
     constexpr int ROWS_B = 64 / SLOTS_B;        // B k-rows per copy block
     constexpr int BLKS_B = BK * BN / 256;
-    static_assert(SLOTS_A == 8, "A swizzle assumes 8 slots per row");
+    static_assert(SLOTS_A == 8 || SLOTS_A == 16, "A swizzle permutes the low 3 bits of the slot");
     static_assert(SLOTS_B >= 8 && 64 % SLOTS_B == 0, "B swizzle needs >= 8 slots per k-row");
     static_assert(BLKS_A % NW == 0 && BLKS_B % NW == 0, "copy blocks must split evenly over the waves");
     constexpr int LPW = BLKS_A / NW + BLKS_B / NW;  // copies per wave per slice
@@ -190,9 +190,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    auto mma = [&](const Frag &f) __attribute__((always_inline)) {
+    // Half h of a chunk's MFMAs: k-steps s = 2h, 2h + 1.
+    auto mma_half = [&](const Frag &f, int h) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 2 * h; s < 2 * h + 2; ++s)
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -244,17 +245,28 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
             using SF = std::integral_constant<int, (s + NS - 1) % NS>;
             const bool live = kt < nk;
             issue(stage_a(SF{}), stage_b(SF{}), (ks0 + min(kt + NS - 1, nk - 1)) * BK);
-            read_frag(f[1], stage_a(S), stage_b(S), 1);
-            __builtin_amdgcn_sched_barrier(0);
-            if (live) mma(f[0]);
-            __builtin_amdgcn_sched_barrier(0);
-            wait_vmcnt<LPW * (NS - 2)>();  // own copies of slice kt+1 landed
-            wait_lgkmcnt0();               // own reads of slice kt done before anyone overwrites it
-            raw_barrier();
-            read_frag(f[0], stage_a(SN{}), stage_b(SN{}), 0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (live) mma(f[1]);
-            __builtin_amdgcn_sched_barrier(0);
+            // Chunk c's fragments sit in f[c % 2].  The reads of the next
+            // chunk go between the two halves of chunk c's MFMAs: while copies
+            // to LDS are in flight the compiler can only wait for LDS reads
+            // with lgkmcnt(0), so the next wait must find nothing recent.
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                Frag &cur = f[c % 2];
+                Frag &nxt = f[(c + 1) % 2];
+                if (c + 1 == NC) {
+                    wait_vmcnt<LPW * (NS - 2)>();  // own copies of slice kt+1 landed
+                    wait_lgkmcnt0();               // own reads of slice kt done before anyone overwrites it
+                    raw_barrier();
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (live) mma_half(cur, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (c + 1 < NC) read_frag(nxt, stage_a(S), stage_b(S), c + 1);
+                else read_frag(nxt, stage_a(SN{}), stage_b(SN{}), 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (live) mma_half(cur, 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         };
         for (int kt = 0; kt < nk; kt += NS) {
             step(kt, S0{});
@@ -337,17 +349,21 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 }
 
 struct DmaCfg {
-    int bm, bn;
+    int bm, bn, bk;
 };
-constexpr DmaCfg kDmaCfgs[] = {{128, 128}, {128, 64}, {64, 64}, {256, 128}};
+// Tile configs (index = TML_GEMM_DMA_TILE - 1); see launch_gemm_f32_dma for
+// the wave tiling and LDS stages of each.
+constexpr DmaCfg kDmaCfgs[] = {{128, 128, 32}, {128, 64, 32}, {64, 64, 32}, {256, 128, 32},
+                               {128, 64, 64},  {64, 64, 64},  {32, 64, 32}, {32, 64, 64}};
 
 }  // namespace
 
 int gemm_dma_num_cfgs() { return (int)(sizeof(kDmaCfgs) / sizeof(kDmaCfgs[0])); }
 
-void gemm_dma_tile(int cfg, int *bm, int *bn) {
+void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk) {
     *bm = kDmaCfgs[cfg].bm;
     *bn = kDmaCfgs[cfg].bn;
+    *bk = kDmaCfgs[cfg].bk;
 }
 
 bool gemm_dma_supported(const MatmulArgs &m) {
@@ -374,15 +390,21 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
     if (p.nsplit > 1 && (ws.partials == nullptr || ws.partial_floats < (size_t)p.nsplit * m.M * m.N))
         return Status::Err(TML_ERR_INVALID_ARG, "GEMM split-K workspace too small");
-    if (p.spl < 1 || (int64_t)p.spl * p.nsplit < (m.K + kBK - 1) / kBK)
+    const int bk = kDmaCfgs[cfg].bk;
+    if (p.spl < 1 || (int64_t)p.spl * p.nsplit < (m.K + bk - 1) / bk)
         return Status::Err(TML_ERR_INVALID_ARG, "GEMM split plan does not cover K");
     if (tiles * p.nsplit >= ((int64_t)1 << 31)) return Status::Err(TML_ERR_INVALID_SHAPE, "GEMM grid too large");
     const dim3 grid((unsigned)(tiles * p.nsplit));
     switch (cfg) {
-        case 0: gemm_f32_dma_kernel<128, 128, 64, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
-        case 1: gemm_f32_dma_kernel<128, 64, 32, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
-        case 2: gemm_f32_dma_kernel<64, 64, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
-        case 3: gemm_f32_dma_kernel<256, 128, 64, 64, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        // <BM, BN, BK, WM, WN, waves, LDS stages>
+        case 0: gemm_f32_dma_kernel<128, 128, 32, 64, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 1: gemm_f32_dma_kernel<128, 64, 32, 32, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 2: gemm_f32_dma_kernel<64, 64, 32, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 3: gemm_f32_dma_kernel<256, 128, 32, 64, 64, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 4: gemm_f32_dma_kernel<128, 64, 64, 32, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 5: gemm_f32_dma_kernel<64, 64, 64, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 6: gemm_f32_dma_kernel<32, 64, 32, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 7: gemm_f32_dma_kernel<32, 64, 64, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
         default: return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
     }
     TML_HIP_TRY(hipGetLastError());

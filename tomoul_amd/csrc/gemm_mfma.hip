@@ -421,29 +421,31 @@ int device_cus() {
 }
 
 // Direct-copy fp32 kernel: pick (tile, K splits) with the smallest modelled
-// time.  A CU runs its share of the units (tile x split) one after another
-// (the 64x64 tile three at a time, which is what its per-slice time below
-// already includes), so
-//   t = ceil(units / CUs) * slices_per_split * t_slice[tile]
+// time.  A CU runs its share of the units (tile x split); with one unit per
+// CU a slice costs t_one, with several resident at once their slices overlap
+// and each costs t_many.  So
+//   t = ceil(units / CUs) * slices_per_split * (BK / 32) * t_slice(tile, one / many)
 //       + t_fill + (splits > 1 ? t_reduce : 0)
-// with t_slice measured on MI355X at full occupancy (us per BK = 32 slice of
-// one unit, 2.4 GHz): 128x128 2.05, 128x64 1.09, 64x64 0.58, 256x128 4.05;
-// t_fill (pipeline fill, epilogue, launch) ~3.5 us; t_reduce (the second
-// launch that sums the splits' partials) ~3.6 us plus the partials'
-// traffic, splits * M * N * 8 bytes at ~6 TB/s.
+// with per 32-deep slice costs measured on MI355X (us, one / several per CU):
+// 128x128 2.05, 128x64 1.09, 64x64 0.61 / 0.56, 256x128 4.05,
+// 128x64 (BK 64) 1.21, 64x64 (BK 64) 0.62, 32x64 0.40 / 0.33,
+// 32x64 (BK 64) 0.38 / 0.35; t_fill (pipeline fill, epilogue, launch)
+// ~3.5 us; t_reduce (the second launch that sums the splits' partials)
+// ~3.6 us plus the partials' traffic, splits * M * N * 8 bytes at ~6 TB/s.
 void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
-    static const double t_slice[] = {2.05, 1.09, 0.58, 4.05};
+    static const double t_one[] = {2.05, 1.09, 0.61, 4.05, 1.21, 0.62, 0.40, 0.38};
+    static const double t_many[] = {2.05, 1.09, 0.56, 4.05, 1.21, 0.62, 0.33, 0.35};
     static const int splits[] = {1, 2, 3, 4, 6, 8};
     constexpr double kFill = 3.5, kReduce = 3.6, kBytesPerUs = 6.0e6;
     const int cus = device_cus();
-    const int64_t nk = (K + kDmaBK - 1) / kDmaBK;
     const int forced_tile = env_int("TML_GEMM_DMA_TILE", 0) - 1;
     const int forced_split = env_int("TML_GEMM_SPLIT", 0);
     double best_t = 1e300;
     for (int c = 0; c < gemm_dma_num_cfgs(); ++c) {
         if (forced_tile >= 0 && c != forced_tile) continue;
-        int bm = 0, bn = 0;
-        gemm_dma_tile(c, &bm, &bn);
+        int bm = 0, bn = 0, bk = 32;
+        gemm_dma_tile(c, &bm, &bn, &bk);
+        const int64_t nk = (K + bk - 1) / bk;
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         for (int sp : splits) {
             if (forced_split > 0 && sp != forced_split) continue;
@@ -453,7 +455,8 @@ void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
             const int64_t units = tiles * real;
             const int64_t per_cu = (units + cus - 1) / cus;
             const double red = real > 1 ? kReduce + (double)real * M * N * 8.0 / kBytesPerUs : 0.0;
-            const double t = (double)per_cu * (double)spl * t_slice[c] + kFill + red;
+            const double ts = per_cu > 1 ? t_many[c] : t_one[c];
+            const double t = (double)per_cu * (double)spl * (bk / 32.0) * ts + kFill + red;
             if (t < best_t) {
                 best_t = t;
                 p->cfg = c;
@@ -462,6 +465,17 @@ void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
                 p->tiles = (int)tiles;
             }
         }
+    }
+    if (best_t == 1e300) {
+        // a forced split too deep for this K: run the forced (or first) tile unsplit
+        const int c = forced_tile >= 0 && forced_tile < gemm_dma_num_cfgs() ? forced_tile : 0;
+        int bm = 0, bn = 0, bk = 32;
+        gemm_dma_tile(c, &bm, &bn, &bk);
+        const int64_t nk = (K + bk - 1) / bk;
+        p->cfg = c;
+        p->nsplit = 1;
+        p->spl = (int)(nk > 0 ? nk : 1);
+        p->tiles = (int)(((M + bm - 1) / bm) * ((N + bn - 1) / bn));
     }
 }
 

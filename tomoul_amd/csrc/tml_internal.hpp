@@ -114,8 +114,7 @@ Status launch_gemm_mfma(const MatmulArgs &a, const Workspace &ws, hipStream_t s)
 // K % 4 == N % 4 == 0 and A, B are 16-byte aligned.
 bool gemm_dma_supported(const MatmulArgs &a);
 int gemm_dma_num_cfgs();
-void gemm_dma_tile(int cfg, int *bm, int *bn);
-constexpr int kDmaBK = 32;
+void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk);
 Status launch_gemm_f32_dma(const MatmulArgs &a, const GemmPlan &p, const Workspace &ws, hipStream_t s);
 Status launch_gemv(const MatmulArgs &a, const Workspace &ws, hipStream_t s);
 // Workspace needed by launch_gemv for this problem.
