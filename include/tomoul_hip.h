@@ -59,6 +59,14 @@ extern "C" {
 #define TML_FMT_Q4_0 2
 #define TML_FMT_Q8_K 3
 
+/* Activation applied after the bias, in the kernel epilogue. */
+#define TML_ACT_NONE 0
+#define TML_ACT_GELU_ERF 1  /* ops.geluExact: x/2 (1 + erf(x/sqrt 2)), erf by Abramowitz-Stegun
+                               7.1.26 as in src/core/ops.zig:2000-2057 */
+#define TML_ACT_GELU_TANH 2 /* ops.gelu: x/2 (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))), tanh by the
+                               reference's Pade approximant on its 8-wide vector part and exact
+                               tanh on the flat tail of (M*N) % 8 elements, src/core/ops.zig:1947-1998 */
+
 /* ---------------------------------------------------------------- setup */
 
 /* Selects the current HIP device and creates the library's stream.  Called
@@ -123,6 +131,15 @@ int tml_hip_sgemm_q4(int64_t M, int64_t N, int64_t K, const float *A, const uint
 int tml_hip_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
                  const float *scales, int64_t block, const float *bias, float *C);
 
+/* tml_hip_gemm with an activation fused after the bias:
+ *   C = act(A . dequant(B) + bias)
+ * Replaces the Whisper FFN's fc1 (src/models/whisper/encoder.zig:244-247 and
+ * decoder.zig:336-338: matmul, addBiasInPlace, geluExact) and the transformer
+ * FFN's first linear (src/core/transformer.zig:218-221: matmulWithWeightBias,
+ * then ops.gelu) with one launch. */
+int tml_hip_gemm_act(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                     const float *scales, int64_t block, const float *bias, int act, float *C);
+
 /* Host-pointer form of tml_hip_quantize_dev below (synchronous): the GPU
  * replacement for the load-time quantizers quantizeQ8 / quantizeQ8K /
  * quantizeQ4 (src/core/quantization.zig:98-129, :406-446, :721-754) that
@@ -153,6 +170,12 @@ int tml_hip_weight_release(const void *host);
 int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
                      const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
                      void *stream);
+
+/* tml_hip_gemm_dev with an activation applied after alpha, beta and bias:
+ *   C = act(alpha * (A . dequant(B)) + beta * C + bias). */
+int tml_hip_gemm_act_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                         const float *scales, int64_t block, const float *bias, int act, float *C, float alpha,
+                         float beta, void *stream);
 
 /* On-device quantizers, bit-identical to the reference's Zig quantizers
  * (quantizeQ8 quantization.zig:98-129, quantizeQ8K :406-446, quantizeQ4
@@ -192,6 +215,9 @@ int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scal
 int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const float *bias, float *C, float alpha,
                           float beta, void *stream);
 int tml_hip_prepared_free(tml_prepared_t w);
+/* tml_hip_gemm_prepared with a fused activation (TML_ACT_*) after the bias. */
+int tml_hip_gemm_prepared_act(tml_prepared_t w, int64_t M, const float *A, const float *bias, int act, float *C,
+                              float alpha, float beta, void *stream);
 
 #ifdef __cplusplus
 }

@@ -32,6 +32,16 @@
  *                                   bitwise equality with orc_matmul_f32 on the
  *                                   dequantized weights (the reference's own
  *                                   definition of the scalar path).
+ *   orc_erf_as                      |erf_as - erf| <= the published A&S
+ *                                   7.1.26 bound (1.5e-7) plus rounding over a
+ *                                   dense grid, odd symmetry, erf(0) = 0.
+ *   orc_gelu_exact                  == x/2 (1 + erf(x/sqrt 2)) within the erf
+ *                                   bound, GELU(0) = 0, GELU(x) - GELU(-x) = x.
+ *   orc_gelu_tanh                   reference KAT (ops.zig:2456-2480, 5
+ *                                   elements = all scalar tail), tail ==
+ *                                   exact tanh-GELU, vector part: odd,
+ *                                   derivative 1 at 0, saturates exactly at
+ *                                   inner = 3 (the Pade form's (x-3)^3 root).
  *   orc_fill_normal                 SplitMix64 published output for seed 0,
  *                                   moment checks.  (Input generator, not a
  *                                   reference function.)
@@ -374,6 +384,54 @@ void orc_matmul_q4_mt(i64 M, i64 N, i64 K, const float *A, const uint8_t *packed
                       int nthreads) {
 #pragma omp parallel for num_threads(nthreads) schedule(static)
     for (i64 i = 0; i < M; i++) orc_matmul_q4(1, N, K, A + i * K, packed, s, C + i * N);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Activations of the fused epilogue                                         */
+/* ------------------------------------------------------------------------ */
+
+/* erf by Abramowitz & Stegun 7.1.26 (ops.zig:2000-2022). */
+float orc_erf_as(float x) {
+    const float a1 = 0.254829592f, a2 = -0.284496736f, a3 = 1.421413741f;
+    const float a4 = -1.453152027f, a5 = 1.061405429f, p = 0.3275911f;
+    float sign = x < 0.0f ? -1.0f : 1.0f;
+    float ax = fabsf(x);
+    float t = 1.0f / (1.0f + p * ax);
+    float t2 = t * t, t3 = t2 * t, t4 = t3 * t, t5 = t4 * t;
+    float poly = a1 * t + a2 * t2 + a3 * t3 + a4 * t4 + a5 * t5;
+    return sign * (1.0f - poly * expf(-ax * ax));
+}
+
+/* geluExact (ops.zig:2029-2057), in place: x * 0.5 * (1 + erf(x / sqrt 2)).
+ * The 8-wide and scalar loops compute the same expression. */
+void orc_gelu_exact(i64 n, float *v) {
+    const float inv_sqrt_2 = 0.7071067811865476f;
+    for (i64 i = 0; i < n; i++) {
+        float x = v[i];
+        v[i] = x * 0.5f * (1.0f + orc_erf_as(x * inv_sqrt_2));
+    }
+}
+
+/* gelu, tanh form (ops.zig:1947-1998), in place.  Elements below
+ * n - n % 8 (the 8-wide AVX2 loop) use the clamped rational form
+ * x(27 + x^2) / (27 + 9x^2) for tanh; the scalar tail uses tanh itself. */
+void orc_gelu_tanh(i64 n, float *v) {
+    const float s2pi = 0.7978845608f, coeff = 0.044715f;
+    i64 tail0 = n - n % 8;
+    for (i64 i = 0; i < n; i++) {
+        float x = v[i];
+        float x3 = x * x * x;
+        float inner = s2pi * (x + coeff * x3);
+        float th;
+        if (i < tail0) {
+            float i2 = inner * inner;
+            th = inner * (27.0f + i2) / (27.0f + 9.0f * i2);
+            th = th > 1.0f ? 1.0f : (th < -1.0f ? -1.0f : th);
+        } else {
+            th = tanhf(inner);
+        }
+        v[i] = 0.5f * x * (1.0f + th);
+    }
 }
 
 int orc_max_threads(void) {

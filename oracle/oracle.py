@@ -63,6 +63,9 @@ def lib() -> ctypes.CDLL:
         "orc_matmul_q8_mt": (None, [_i64, _i64, _i64, _f32p, _i8p, ctypes.c_float, _f32p, ctypes.c_int]),
         "orc_matmul_q4_mt": (None, [_i64, _i64, _i64, _f32p, _u8p, ctypes.c_float, _f32p, ctypes.c_int]),
         "orc_max_threads": (ctypes.c_int, []),
+        "orc_erf_as": (ctypes.c_float, [ctypes.c_float]),
+        "orc_gelu_exact": (None, [_i64, _f32p]),
+        "orc_gelu_tanh": (None, [_i64, _f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -259,3 +262,35 @@ def matmul_q4_mt(a, packed, k: int, n: int, scale: float, nthreads: int) -> np.n
 
 def max_threads() -> int:
     return int(lib().orc_max_threads())
+
+
+# ---------------------------------------------------------------- activations
+ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2
+
+
+def erf_as(x: float) -> float:
+    """A&S 7.1.26 erf of src/core/ops.zig:2000-2022."""
+    return float(lib().orc_erf_as(x))
+
+
+def gelu_exact(v) -> np.ndarray:
+    """ops.geluExact (src/core/ops.zig:2029-2057) on a copy of v."""
+    out = _f32(v).copy()
+    lib().orc_gelu_exact(out.size, out.reshape(-1))
+    return out
+
+
+def gelu_tanh(v) -> np.ndarray:
+    """ops.gelu (src/core/ops.zig:1947-1998) on a copy of v: the flat index
+    decides between the 8-wide rational tanh and the scalar tail's tanh."""
+    out = _f32(v).copy()
+    lib().orc_gelu_tanh(out.size, out.reshape(-1))
+    return out
+
+
+def apply_act(v, act: int) -> np.ndarray:
+    if act == ACT_GELU_ERF:
+        return gelu_exact(v)
+    if act == ACT_GELU_TANH:
+        return gelu_tanh(v)
+    return _f32(v).copy()

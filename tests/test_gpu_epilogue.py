@@ -1,0 +1,173 @@
+"""GPU parity of the fused activation epilogue (GELU erf / GELU tanh).
+
+The reference runs the up-projection, then a separate pass over the whole
+output: ops.gelu (tanh form, src/core/transformer.zig:213-221) or
+ops.geluExact (erf form, src/models/whisper/encoder.zig:244-247).  The
+oracle applies its restatement of that pass (oracle/oracle.c: orc_gelu_tanh,
+orc_gelu_exact) to its matmul; the GPU applies it in the kernel epilogue.
+Tolerances as for the matmul itself: max|G-R|/max|R| <= 1e-4 (fp32),
+<= 1e-3 (quantized).  Shapes are chosen so that M*N % 8 != 0 where the tanh
+form's vector/scalar split matters, and so that every kernel family runs:
+the [K,N] GEMV (M <= 8), the prepared K-contiguous GEMV, the direct-copy
+fp32 GEMM with and without its split-K reduce, and the register-staged GEMM
+(quantized weights, or N % 4 != 0).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import elementwise_ok, rel_err
+from tomoul_amd import _abi, dispatch, quantization as qz, synth
+from tomoul_amd.tensor import Tensor
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+Q_TOL = 1e-3
+ACTS = [_abi.ACT_GELU_ERF, _abi.ACT_GELU_TANH]
+
+
+def T(a):
+    return Tensor.from_numpy(np.asarray(a, dtype=np.float32))
+
+
+def rnd(seed, m, n, std=1.0):
+    return synth.normal_matrix(seed, m, n, std)
+
+
+SHAPES = [(1, 165, 96), (3, 162, 96), (7, 162, 200), (8, 4097, 64), (64, 160, 96), (300, 262, 136),
+          (129, 68, 1028), (1500, 1536, 384)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_fused_gelu_all_formats(orc, m, n, k):
+    a = rnd(601, m, k)
+    w = rnd(602, k, n, 0.05)
+    bias = synth.normal(603, n, 0.0, 0.5)
+    tb = Tensor.from_numpy(bias)
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    qk, sk = orc.quantize_q8k(w)
+    cases = [
+        (T(w), orc.matmul_bias(a, w, bias), FP32_TOL),
+        (qz.QuantizedTensorQ8(s, q, (k, n)), orc.matmul_q8(a, q, s) + bias, Q_TOL),
+        (qz.QuantizedTensorQ4(s4, p, (k, n)), orc.matmul_q4(a, p, k, n, s4) + bias, Q_TOL),
+        (qz.QuantizedTensorQ8K(sk, qk, (k, n)), orc.matmul_q8k(a, qk, sk) + bias, Q_TOL),
+    ]
+    for weight, pre, tol in cases:
+        for fn, act in ((dispatch.matmulWithWeightBiasGeluExact, orc.ACT_GELU_ERF),
+                        (dispatch.matmulWithWeightBiasGelu, orc.ACT_GELU_TANH)):
+            got = fn(T(a), weight, tb).numpy()
+            ref = orc.apply_act(pre, act)
+            err = rel_err(got, ref)
+            assert err <= tol, (type(weight).__name__, act, err)
+
+
+def test_tanh_split_follows_flat_index(orc):
+    # Same pre-activation value in the vector part and in the scalar tail of
+    # ops.gelu: M*N = 3*7 = 21, so flat indices 16..20 use tanh itself and
+    # 0..15 the rational form.  With A = ones and B chosen so every output
+    # is exactly 2.0, the two forms give 1.9762 vs 1.9545 (see the oracle
+    # pinning tests); the GPU must reproduce both.
+    m, n, k = 3, 7, 4
+    a = np.ones((m, k), np.float32)
+    w = np.full((k, n), 0.5, np.float32)
+    got = np.zeros((m, n), np.float32)
+    _abi.gemm_act(_abi.FMT_F32, m, n, k, a, w, got, act=_abi.ACT_GELU_TANH)
+    ref = orc.gelu_tanh(np.full((m, n), 2.0, np.float32))
+    flat, rflat = got.reshape(-1), ref.reshape(-1)
+    assert abs(rflat[0] - rflat[20]) > 0.01
+    np.testing.assert_allclose(flat, rflat, rtol=2e-6, atol=0)
+
+
+@pytest.fixture
+def forced_env():
+    keys = ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE")
+    saved = {key: os.environ.get(key) for key in keys}
+    yield os.environ
+    for key, v in saved.items():
+        if v is None:
+            os.environ.pop(key, None)
+        else:
+            os.environ[key] = v
+
+
+@pytest.mark.parametrize("split", [1, 3])
+@pytest.mark.parametrize("act", ACTS)
+def test_fused_gelu_split_reduce(orc, forced_env, split, act):
+    # With K split, the direct-copy GEMM writes raw partials and the reduce
+    # kernel applies bias and activation (its 4-wide path); split 1 takes
+    # the GEMM's own epilogue.
+    forced_env["TML_GEMM_SPLIT"] = str(split)
+    for tile in ("1", "4", "7"):
+        forced_env["TML_GEMM_DMA_TILE"] = tile
+        for (m, n, k) in [(129, 68, 1028), (300, 260, 516)]:
+            a, w = rnd(611, m, k), rnd(612, k, n, 0.03)
+            bias = synth.normal(613, n, 0.0, 0.5)
+            got = np.zeros((m, n), np.float32)
+            _abi.gemm_act(_abi.FMT_F32, m, n, k, a, w, got, act=act, bias=bias)
+            ref = orc.apply_act(orc.matmul_bias(a, w, bias), act)
+            err = rel_err(got, ref)
+            assert err <= FP32_TOL and elementwise_ok(got, ref, 2e-4), (tile, m, n, k, err)
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("m", [1, 2, 3, 9])
+def test_fused_gelu_prepared(orc, act, m):
+    # Prepared weights: the K-contiguous kernel for M within its range, the
+    # [K,N] fallback beyond it (Q4_0 from M = 3, Q8_0 from M = 5, all at 9).
+    import torch
+    k, n = 1280, 1283
+    w = rnd(621, k, n, 0.03)
+    a = rnd(622 + m, m, k)
+    bias = synth.normal(623, n, 0.0, 0.5)
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    for fmt, b, scale, pre, tol in [(_abi.FMT_F32, w, 1.0, orc.matmul(a, w), FP32_TOL),
+                                    (_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s), Q_TOL),
+                                    (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4), Q_TOL)]:
+        B, A, Bias = _dev(b), _dev(a), _dev(bias)
+        C = torch.zeros((m, n), dtype=torch.float32, device="cuda:0")
+        h = _abi.prepare_dev(fmt, k, n, B.data_ptr(), scale)
+        try:
+            _abi.gemm_prepared_act(h, m, A.data_ptr(), C.data_ptr(), act=act, bias_ptr=Bias.data_ptr())
+            torch.cuda.synchronize()
+        finally:
+            _abi.prepared_free(h)
+        ref = orc.apply_act(pre + bias, act)
+        assert rel_err(C.cpu().numpy(), ref) <= tol, (fmt, m)
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 200, 300), (64, 256, 128), (70, 90, 33)])
+def test_fused_gelu_alpha_beta_dev(orc, m, n, k):
+    # The activation applies to alpha * A.B + beta * C + bias as a whole.
+    import torch
+    a, w, c0 = rnd(631, m, k), rnd(632, k, n, 0.05), rnd(633, m, n)
+    bias = synth.normal(634, n, 0.0, 0.5)
+    pre = 0.5 * orc.matmul(a, w) - 2.0 * c0 + bias
+    for act in ACTS:
+        A, B, C, Bias = _dev(a), _dev(w), _dev(c0), _dev(bias)
+        _abi.gemm_act_dev(_abi.FMT_F32, m, n, k, A.data_ptr(), B.data_ptr(), C.data_ptr(), act=act,
+                          bias_ptr=Bias.data_ptr(), alpha=0.5, beta=-2.0)
+        torch.cuda.synchronize()
+        assert rel_err(C.cpu().numpy(), orc.apply_act(pre, act)) <= FP32_TOL, act
+
+
+def test_act_none_matches_plain_entry_point():
+    # act = TML_ACT_NONE is the plain GEMM bit for bit; an unknown
+    # activation is rejected before any device work.
+    m, n, k = 5, 96, 64
+    a, w = rnd(641, m, k), rnd(642, k, n)
+    c0, c1 = np.zeros((m, n), np.float32), np.zeros((m, n), np.float32)
+    _abi.gemm(_abi.FMT_F32, m, n, k, a, w, c0)
+    _abi.gemm_act(_abi.FMT_F32, m, n, k, a, w, c1, act=_abi.ACT_NONE)
+    np.testing.assert_array_equal(c0, c1)
+    with pytest.raises(_abi.TmlError) as e:
+        _abi.gemm_act(_abi.FMT_F32, m, n, k, a, w, c1, act=7)
+    assert e.value.code == _abi.TML_ERR_INVALID_ARG

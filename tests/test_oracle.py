@@ -303,3 +303,80 @@ def test_roundtrip_realistic_distribution(orc):
     assert _rel_rmse(t, orc.dequantize_q8k(qk, sk)) < 0.01
     p, s4 = orc.quantize_q4(t)
     assert _rel_rmse(t, orc.dequantize_q4(p, t.size, s4)) < 0.15
+
+
+# ---------------------------------------------------------------- activations
+def test_erf_as_within_published_bound(orc):
+    # Abramowitz & Stegun 7.1.26 is published with |error| <= 1.5e-7; in f32
+    # the five-term sum (terms up to 1.4 with alternating signs) and the
+    # final 1 - poly * exp(-x^2) add a few ulps of 1 (worst near x = 0.02).
+    # A wrong coefficient or a dropped term breaks this by orders of
+    # magnitude.
+    import math
+    xs = np.linspace(-6.0, 6.0, 24001).astype(np.float32)
+    worst = max(abs(orc.erf_as(float(x)) - math.erf(float(x))) for x in xs)
+    assert worst <= 1.5e-7 + 3.5e-7, worst
+    assert orc.erf_as(0.0) == 0.0
+    for x in (0.1, 0.5, 1.3, 2.7, 5.0):
+        assert orc.erf_as(-x) == -orc.erf_as(x)
+    assert orc.erf_as(10.0) == 1.0 and orc.erf_as(-10.0) == -1.0
+
+
+def test_gelu_exact_closed_form(orc):
+    # x/2 (1 + erf(x/sqrt 2)) with the erf error above; GELU(x) - GELU(-x) = x.
+    import math
+    x = synth.normal(501, 4099, 0.0, 2.0)
+    got = orc.gelu_exact(x).astype(np.float64)
+    ref = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in x.astype(np.float64)])
+    assert np.all(np.abs(got - ref) <= 0.5 * np.abs(x) * 4e-7 + 1e-7)
+    neg = orc.gelu_exact(-x).astype(np.float64)
+    assert np.all(np.abs((got - neg) - x) <= 1e-6 * np.abs(x) + 1e-7)
+    assert orc.gelu_exact(np.zeros(9, np.float32)).tolist() == [0.0] * 9
+
+
+def test_gelu_tanh_reference_kat(orc):
+    # src/core/ops.zig:2456-2480 (five elements: the scalar tail only).
+    got = orc.gelu_tanh(np.array([-2.0, -1.0, 0.0, 1.0, 2.0], np.float32))
+    for g, want, tol in zip(got, [-0.0454, -0.1588, 0.0, 0.8412, 1.9545], [0.01, 0.01, 0.001, 0.01, 0.01]):
+        assert abs(g - want) <= tol
+
+
+def test_gelu_tanh_tail_is_exact_tanh(orc):
+    # Elements from n - n % 8 on use tanh itself (ops.zig:1972-1978).
+    import math
+    x = synth.normal(502, 8 * 5 + 7, 0.0, 2.0)
+    got = orc.gelu_tanh(x).astype(np.float64)
+    c = math.sqrt(2.0 / math.pi)
+    ref = np.array([0.5 * v * (1.0 + math.tanh(c * (v + 0.044715 * v ** 3))) for v in x.astype(np.float64)])
+    tail = slice(40, 47)
+    assert np.all(np.abs(got[tail] - ref[tail]) <= 1e-6 * (np.abs(ref[tail]) + 1e-3))
+    # The vector part is the rational form: within its ~2e-2 of the exact
+    # curve but visibly different from it somewhere on this sample.
+    body = slice(0, 40)
+    d = np.abs(got[body] - ref[body])
+    assert np.all(d <= 0.03 * np.abs(x[body]).astype(np.float64) + 1e-6) and d.max() > 1e-4
+
+
+def test_gelu_tanh_vector_form_properties(orc):
+    # The 8-wide loop's tanh is x(27 + x^2) / (27 + 9 x^2), clamped to
+    # [-1, 1] (ops.zig:1980-1997): odd (so GELU(x) - GELU(-x) = x), slope 1
+    # at 0, and it reaches 1 exactly where x(27 + x^2) = 27 + 9 x^2, i.e.
+    # (x - 3)^3 = 0: for inner = sqrt(2/pi)(x + 0.044715 x^3) >= 3 the
+    # output is exactly x, below it strictly less.
+    x = np.array([0.5, 1.0, 2.0, 2.3, 2.6, 3.0, 4.0, 6.0], np.float32)
+    g = orc.gelu_tanh(x)
+    gn = orc.gelu_tanh(-x)
+    assert np.all(np.abs((g.astype(np.float64) - gn) - x) <= 1e-6 * x)
+    inner = 0.7978845608 * (x.astype(np.float64) + 0.044715 * x.astype(np.float64) ** 3)
+    sat = inner >= 3.0 + 1e-5
+    below = inner <= 3.0 - 1e-3
+    assert sat.any() and below.any()
+    assert np.all(g[sat] == x[sat]) and np.all(g[below] < x[below])
+    eps = np.float32(1e-3)
+    small = orc.gelu_tanh(np.full(8, eps, np.float32))[0]
+    slope = (float(small) - float(eps) / 2) / (float(eps) ** 2 / 2)  # = sqrt(2/pi) * tanh'(0)
+    assert abs(slope - 0.7978845608) < 5e-3
+    # The rational form differs from the KAT's exact-tanh values at x = 2
+    # by more than the KAT tolerance: the split is observable.
+    g8 = orc.gelu_tanh(np.array([2.0] * 8 + [2.0], np.float32))
+    assert abs(g8[0] - 1.9545) > 0.01 and abs(g8[8] - 1.9545) <= 0.01

@@ -25,6 +25,7 @@ TML_ERR_NO_DEVICE = -6
 TML_ERR_HIP = -7
 
 FMT_F32, FMT_Q8_0, FMT_Q4_0, FMT_Q8_K = 0, 1, 2, 3
+ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2
 
 # Every symbol the header declares, with its ctypes signature.
 _i64 = ctypes.c_int64
@@ -51,6 +52,11 @@ SIGNATURES = {
     "tml_hip_prepare_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _f, _vp, ctypes.POINTER(_vp)]),
     "tml_hip_gemm_prepared": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _f, _f, _vp]),
     "tml_hip_prepared_free": (ctypes.c_int, [_vp]),
+    "tml_hip_gemm_act": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, ctypes.c_int,
+                                        _vp]),
+    "tml_hip_gemm_act_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp,
+                                            ctypes.c_int, _vp, _f, _f, _vp]),
+    "tml_hip_gemm_prepared_act": (ctypes.c_int, [_vp, _i64, _vp, _vp, ctypes.c_int, _vp, _f, _f, _vp]),
 }
 
 
@@ -146,6 +152,13 @@ def gemm(fmt: int, m: int, n: int, k: int, a: np.ndarray, b: np.ndarray, c: np.n
     check(lib().tml_hip_gemm(fmt, m, n, k, _ptr(a), _ptr(b), scale, _ptr(scales), block, _ptr(bias), _ptr(c)))
 
 
+def gemm_act(fmt: int, m: int, n: int, k: int, a: np.ndarray, b: np.ndarray, c: np.ndarray, *, act: int,
+             scale: float = 1.0, scales: np.ndarray | None = None, block: int = 32,
+             bias: np.ndarray | None = None) -> None:
+    check(lib().tml_hip_gemm_act(fmt, m, n, k, _ptr(a), _ptr(b), scale, _ptr(scales), block, _ptr(bias), act,
+                                 _ptr(c)))
+
+
 def quantize(fmt: int, w: np.ndarray, q: np.ndarray, scales: np.ndarray) -> None:
     check(lib().tml_hip_quantize(fmt, w.size, _ptr(w), _ptr(q), _ptr(scales)))
 
@@ -166,6 +179,13 @@ def gemm_dev(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr: in
                                  beta, stream))
 
 
+def gemm_act_dev(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr: int, *, act: int,
+                 scale: float = 1.0, scales_ptr: int | None = None, block: int = 32, bias_ptr: int | None = None,
+                 alpha: float = 1.0, beta: float = 0.0, stream: int | None = None) -> None:
+    check(lib().tml_hip_gemm_act_dev(fmt, m, n, k, a_ptr, b_ptr, scale, scales_ptr, block, bias_ptr, act, c_ptr,
+                                     alpha, beta, stream))
+
+
 def quantize_dev(fmt: int, n: int, w_ptr: int, q_ptr: int, scales_ptr: int, stream: int | None = None) -> None:
     check(lib().tml_hip_quantize_dev(fmt, n, w_ptr, q_ptr, scales_ptr, stream))
 
@@ -181,6 +201,11 @@ def prepare_dev(fmt: int, k: int, n: int, b_ptr: int, scale: float = 1.0, stream
 def gemm_prepared(handle: int, m: int, a_ptr: int, c_ptr: int, *, bias_ptr: int | None = None, alpha: float = 1.0,
                   beta: float = 0.0, stream: int | None = None) -> None:
     check(lib().tml_hip_gemm_prepared(handle, m, a_ptr, bias_ptr, c_ptr, alpha, beta, stream))
+
+
+def gemm_prepared_act(handle: int, m: int, a_ptr: int, c_ptr: int, *, act: int, bias_ptr: int | None = None,
+                      alpha: float = 1.0, beta: float = 0.0, stream: int | None = None) -> None:
+    check(lib().tml_hip_gemm_prepared_act(handle, m, a_ptr, bias_ptr, act, c_ptr, alpha, beta, stream))
 
 
 def prepared_free(handle: int) -> None:

@@ -49,6 +49,8 @@ struct DmaArgs {
     int nsplit, spl;      // K splits and BK-slices per split
     float *ws;            // split partials: [split][M][N]
     const float *zero;
+    int act;              // TML_ACT_* after the bias
+    long long tail0;      // tml_act_tail0(M * N)
 };
 
 #define TML_GPTR(p) ((__attribute__((address_space(1))) void *)(p))
@@ -314,17 +316,19 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
                     float v = a.alpha * acc[i][j][r];
                     if (a.beta != 0.0f) v += a.beta * *cp;
                     if (a.bias) v += bcol;
-                    *cp = v;
+                    *cp = tml_apply_act(v, a.act, (long long)row * a.N + col, a.tail0);
                 }
             }
         }
 }
 
-// C = alpha * sum_s ws[s] + beta * C + bias over the M*N outputs, the splits
-// summed in order (deterministic).  Four outputs per thread when aligned.
+// C = act(alpha * sum_s ws[s] + beta * C + bias) over the M*N outputs, the
+// splits summed in order (deterministic).  Four outputs per thread when
+// aligned.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws, int nsplit, long long mn,
                                                             int n, float *C, float alpha, float beta,
-                                                            const float *__restrict__ bias, bool vec) {
+                                                            const float *__restrict__ bias, bool vec, int act,
+                                                            long long tail0) {
     const long long stride = (long long)gridDim.x * blockDim.x;
     if (vec) {
         for (long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x; q < mn / 4; q += stride) {
@@ -334,6 +338,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
             float *cp = C + 4 * q;
             if (beta != 0.0f) v += beta * *(const floatx4 *)cp;
             if (bias) v += *(const floatx4 *)(bias + (4 * q) % n);
+            if (act != TML_ACT_NONE)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = tml_apply_act(v[r], act, 4 * q + r, tail0);
             *(floatx4 *)cp = v;
         }
     } else {
@@ -343,7 +350,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
             float v = alpha * acc;
             if (beta != 0.0f) v += beta * C[e];
             if (bias) v += bias[e % n];
-            C[e] = v;
+            C[e] = tml_apply_act(v, act, e, tail0);
         }
     }
 }
@@ -387,6 +394,8 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
     a.nsplit = p.nsplit;
     a.spl = p.spl;
     a.ws = ws.partials;
+    a.act = m.act;
+    a.tail0 = tml_act_tail0((long long)m.M * m.N);
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
     if (p.nsplit > 1 && (ws.partials == nullptr || ws.partial_floats < (size_t)p.nsplit * m.M * m.N))
         return Status::Err(TML_ERR_INVALID_ARG, "GEMM split-K workspace too small");
@@ -413,7 +422,8 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
         const int64_t blocks = (n4 + 255) / 256;
         splitk_reduce_kernel<<<dim3((unsigned)(blocks < 65535 ? blocks : 65535)), 256, 0, s>>>(
             ws.partials, p.nsplit, m.M * m.N, m.N, m.C, m.alpha_eff, m.beta, m.bias,
-            m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0));
+            m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0),
+            m.act, tml_act_tail0((long long)m.M * m.N));
         TML_HIP_TRY(hipGetLastError());
     }
     return Status::Ok();

@@ -53,6 +53,8 @@ struct GemvKArgs {
     float *ws;           // [nsplit][MR][N] partials when nsplit > 1
     unsigned *counters;  // one per segment, zero between launches
     const void *zero;
+    int act;             // TML_ACT_* after the bias
+    long long tail0;     // tml_act_tail0(M * N)
 };
 
 // Elements of B held in LW bytes.
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
         float v = a.alpha * p;
         if (a.beta != 0.0f) v += a.beta * *cp;
         if (a.bias) v += a.bias[col];
-        *cp = v;
+        *cp = tml_apply_act(v, a.act, (long long)m * a.N + col, a.tail0);
     };
     auto useful = [&](int o) __attribute__((always_inline)) {
         return o < NOUT && o / SC < a.M && col0 + o % SC < a.N;
@@ -504,6 +506,7 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     ka.nseg = p.nseg; ka.nsplit = p.nsplit; ka.nb = p.nb;
     ka.ws = ws.partials; ka.counters = ws.counters;
     ka.zero = m.zero;
+    ka.act = m.act; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
     switch (m.fmt) {
         case TML_FMT_F32: return launch_fmt<TML_FMT_F32>(ka, p, s);
         case TML_FMT_Q8_0: return launch_fmt<TML_FMT_Q8_0>(ka, p, s);

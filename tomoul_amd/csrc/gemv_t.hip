@@ -47,6 +47,8 @@ struct GemvTArgs {
     float alpha, beta;
     int nchunk;           // 16-byte chunks per prepared row
     const void *zero;
+    int act;              // TML_ACT_* after the bias
+    long long tail0;      // tml_act_tail0(M * N)
 };
 
 template <int FMT> struct TElems;
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
         float v = a.alpha * val;
         if (a.beta != 0.0f) v += a.beta * *cp;
         if (a.bias) v += a.bias[n];
-        *cp = v;
+        *cp = tml_apply_act(v, a.act, (long long)m * a.N + n, a.tail0);
     }
 }
 
@@ -381,7 +383,8 @@ Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, 
 }
 
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
-                     const float *bias, float *C, float alpha_eff, float beta, const void *zero, hipStream_t s) {
+                     const float *bias, float *C, float alpha_eff, float beta, const void *zero, int act,
+                     hipStream_t s) {
     if (!prepared_gemv_supported(fmt, M, K)) return Status::Err(TML_ERR_INVALID_ARG, "prepared GEMV: unsupported");
     if (N >= ((int64_t)1 << 30) || K >= ((int64_t)1 << 30))
         return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV dimension exceeds 2^30");
@@ -393,6 +396,8 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     ka.bias = bias; ka.C = C; ka.alpha = alpha_eff; ka.beta = beta;
     ka.nchunk = (int)((prepared_row_bytes(fmt, K) + 15) / 16);
     ka.zero = zero;
+    ka.act = act;
+    ka.tail0 = tml_act_tail0((long long)M * N);
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) {
         int n = 0;

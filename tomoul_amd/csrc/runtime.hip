@@ -162,10 +162,13 @@ size_t weight_bytes(int fmt, int64_t K, int64_t N) {
     }
 }
 
+bool valid_act(int act) { return act == TML_ACT_NONE || act == TML_ACT_GELU_ERF || act == TML_ACT_GELU_TANH; }
+
 Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B,
                 float scale, const float *scales, int64_t block, const float *bias, float *C, float alpha,
-                float beta, hipStream_t s) {
+                float beta, hipStream_t s, int act = TML_ACT_NONE) {
     if (!valid_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
+    if (!valid_act(act)) return Status::Err(TML_ERR_INVALID_ARG, "unknown activation");
     if (M < 0 || N < 0 || K < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
     if (M == 0 || N == 0) return Status::Ok();
     if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr)))
@@ -178,6 +181,7 @@ Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const fl
     m.bias = bias; m.C = C; m.beta = beta; m.fmt = fmt;
     m.alpha_eff = (fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0) ? alpha * scale : alpha;
     m.zero = c->zero.p;
+    m.act = act;
     Workspace ws;
     TML_TRY(ensure_workspace(c, m, s, &ws));
     if (M <= kGemvMaxM) return launch_gemv(m, ws, s);
@@ -221,15 +225,18 @@ Status make_prepared(DeviceCtx *c, int fmt, int64_t K, int64_t N, const void *B,
 // C = alpha * A . dequant(B) + beta * C + bias with a prepared weight: the
 // K-contiguous decoder kernel when it covers M and K, else the [K,N] path.
 Status gemm_prepared(DeviceCtx *c, const Prepared *p, int64_t M, const float *A, const float *bias, float *C,
-                     float alpha, float beta, hipStream_t s) {
+                     float alpha, float beta, hipStream_t s, int act = TML_ACT_NONE) {
     if (M < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
+    if (!valid_act(act)) return Status::Err(TML_ERR_INVALID_ARG, "unknown activation");
     if (M == 0 || p->N == 0) return Status::Ok();
     if (C == nullptr || (p->K > 0 && A == nullptr)) return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
     if (prepared_gemv_supported(p->fmt, M, p->K)) {
         const float alpha_eff = (p->fmt == TML_FMT_Q8_0 || p->fmt == TML_FMT_Q4_0) ? alpha * p->scale : alpha;
-        return launch_gemv_t(p->fmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, C, alpha_eff, beta, c->zero.p, s);
+        return launch_gemv_t(p->fmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, C, alpha_eff, beta, c->zero.p, act, s);
     }
-    return gemm_dev(c, p->fmt, M, p->N, p->K, A, p->B, p->scale, nullptr, 0, bias, C, alpha, beta, s);
+    if (p->B == nullptr)
+        return Status::Err(TML_ERR_INVALID_SHAPE, "row count beyond the prepared kernel and no [K,N] weight to fall back to");
+    return gemm_dev(c, p->fmt, M, p->N, p->K, A, p->B, p->scale, nullptr, 0, bias, C, alpha, beta, s, act);
 }
 
 // Resident copy of a registered host buffer of at least `bytes`, or null.
@@ -256,8 +263,10 @@ Status upload(DeviceCtx *c, DevBuf &buf, const void *host, size_t bytes, const v
 
 // Host-pointer call: stage operands, run, copy C back, wait.
 Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
-                 const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta) {
+                 const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
+                 int act = TML_ACT_NONE) {
     if (!valid_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
+    if (!valid_act(act)) return Status::Err(TML_ERR_INVALID_ARG, "unknown activation");
     if (M < 0 || N < 0 || K < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
     if (M == 0 || N == 0) return Status::Ok();
     if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr)))
@@ -297,10 +306,10 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
             reg->prep = p;
         }
         TML_TRY(gemm_prepared(c, p, M, (const float *)dA, (const float *)dBias, (float *)c->c.p, alpha, beta,
-                              c->stream));
+                              c->stream, act));
     } else {
         TML_TRY(gemm_dev(c, fmt, M, N, K, (const float *)dA, dB, scale, (const float *)dS, block,
-                         (const float *)dBias, (float *)c->c.p, alpha, beta, c->stream));
+                         (const float *)dBias, (float *)c->c.p, alpha, beta, c->stream, act));
     }
     TML_HIP_TRY(hipMemcpyAsync(C, c->c.p, cbytes, hipMemcpyDeviceToHost, c->stream));
     TML_HIP_TRY(hipStreamSynchronize(c->stream));
@@ -411,6 +420,11 @@ int tml_hip_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
     return report(host_gemm(fmt, M, N, K, A, B, scale, scales, block, bias, C, 1.0f, 0.0f));
 }
 
+int tml_hip_gemm_act(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                     const float *scales, int64_t block, const float *bias, int act, float *C) {
+    return report(host_gemm(fmt, M, N, K, A, B, scale, scales, block, bias, C, 1.0f, 0.0f, act));
+}
+
 int tml_hip_quantize(int fmt, int64_t n, const float *w, void *q, float *scales) {
     if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K)
         return report(Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0 or Q8_K"));
@@ -500,6 +514,16 @@ int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     return report(gemm_dev(c, fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, (hipStream_t)stream));
 }
 
+int tml_hip_gemm_act_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                         const float *scales, int64_t block, const float *bias, int act, float *C, float alpha,
+                         float beta, void *stream) {
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    return report(gemm_dev(c, fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, (hipStream_t)stream,
+                           act));
+}
+
 int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scale, void *stream,
                         tml_prepared_t *out) {
     if (out == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null handle pointer"));
@@ -522,6 +546,17 @@ int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const flo
     const Prepared *p = (const Prepared *)w;
     if (p->device != c->device) return report(Status::Err(TML_ERR_INVALID_ARG, "prepared weight of another device"));
     return report(gemm_prepared(c, p, M, A, bias, C, alpha, beta, (hipStream_t)stream));
+}
+
+int tml_hip_gemm_prepared_act(tml_prepared_t w, int64_t M, const float *A, const float *bias, int act, float *C,
+                              float alpha, float beta, void *stream) {
+    if (w == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null prepared weight"));
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    const Prepared *p = (const Prepared *)w;
+    if (p->device != c->device) return report(Status::Err(TML_ERR_INVALID_ARG, "prepared weight of another device"));
+    return report(gemm_prepared(c, p, M, A, bias, C, alpha, beta, (hipStream_t)stream, act));
 }
 
 int tml_hip_prepared_free(tml_prepared_t w) {

@@ -49,7 +49,45 @@ struct MatmulArgs {
     float beta;
     int fmt;
     const void *zero;      // >= 64 zero bytes of device memory (see below)
+    int act = TML_ACT_NONE;  // activation after the bias (TML_ACT_*)
 };
+
+// Activations of the epilogue, restating the reference's CPU code.
+// erf: Abramowitz & Stegun 7.1.26 exactly as src/core/ops.zig:2000-2022
+// (the published five-term approximation, |error| <= 1.5e-7).
+__device__ __forceinline__ float tml_erf_as(float x) {
+    const float a1 = 0.254829592f, a2 = -0.284496736f, a3 = 1.421413741f, a4 = -1.453152027f,
+                a5 = 1.061405429f, p = 0.3275911f;
+    const float sign = x < 0.0f ? -1.0f : 1.0f;
+    const float ax = fabsf(x);
+    const float t = 1.0f / (1.0f + p * ax);
+    const float t2 = t * t, t3 = t2 * t, t4 = t3 * t, t5 = t4 * t;
+    const float y = 1.0f - (a1 * t + a2 * t2 + a3 * t3 + a4 * t4 + a5 * t5) * expf(-ax * ax);
+    return sign * y;
+}
+// v -> act(v) for the element at flat index `flat` of C; tail0 = M*N minus
+// (M*N) % 8 is where the reference's 8-wide loops hand over to their
+// scalar tail (ops.gelu uses exact tanh there, a Pade approximant before).
+__device__ __forceinline__ float tml_apply_act(float v, int act, long long flat, long long tail0) {
+    if (act == TML_ACT_GELU_ERF) {
+        const float inv_sqrt_2 = 0.7071067811865476f;
+        return v * 0.5f * (1.0f + tml_erf_as(v * inv_sqrt_2));  // ops.zig:2029-2057
+    }
+    if (act == TML_ACT_GELU_TANH) {
+        const float sqrt_2_over_pi = 0.7978845608f, coeff = 0.044715f;  // ops.zig:1947-1998
+        const float inner = sqrt_2_over_pi * (v + coeff * (v * v * v));
+        float th;
+        if (flat < tail0) {
+            const float x2 = inner * inner;
+            th = fminf(1.0f, fmaxf(-1.0f, inner * (27.0f + x2) / (27.0f + 9.0f * x2)));
+        } else {
+            th = tanhf(inner);
+        }
+        return 0.5f * v * (1.0f + th);
+    }
+    return v;
+}
+__host__ __device__ __forceinline__ long long tml_act_tail0(long long mn) { return mn - mn % 8; }
 
 // Kernels load out-of-range chunks from this zeroed block instead of
 // branching around the load: the selected address keeps the load
@@ -134,7 +172,8 @@ int64_t prepared_row_bytes(int fmt, int64_t K);
 bool prepared_gemv_supported(int fmt, int64_t M, int64_t K);
 Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, int64_t ldt, hipStream_t s);
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
-                     const float *bias, float *C, float alpha_eff, float beta, const void *zero, hipStream_t s);
+                     const float *bias, float *C, float alpha_eff, float beta, const void *zero, int act,
+                     hipStream_t s);
 
 // Tuning overrides for experiments (0 = heuristic).  Read from the
 // TML_GEMM_TILE / TML_GEMV_SPLIT environment variables once.

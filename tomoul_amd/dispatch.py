@@ -6,6 +6,18 @@ matmulWithWeightBias(input, weight, b)  src/core/attention.zig:132-149
 the kernel family; every branch runs on the GPU.  For quantized weights the
 reference runs the matmul and then addBiasInPlace; here the bias is fused
 into the kernel epilogue (one launch, no second pass over the output).
+
+The feed-forward up-projections that the reference follows with a GELU pass
+over the whole output are fused the same way:
+  matmulWithWeightBiasGelu(input, weight, b)
+      matmulWithWeightBias + ops.gelu (tanh form)
+      src/core/transformer.zig:213-221, ops.zig:1947-1998
+  matmulWithWeightBiasGeluExact(input, weight, b)
+      ops.matmul + addBiasInPlace + ops.geluExact (erf form)
+      src/models/whisper/encoder.zig:244-247, ops.zig:2029-2057
+The activation is applied in the kernel epilogue after the bias, per output
+element, with the reference's vector/scalar split of ops.gelu preserved (the
+flat index decides, see include/tomoul_hip.h).
 """
 from __future__ import annotations
 
@@ -50,3 +62,30 @@ def matmulWithWeightBias(a: Tensor, weight, bias: Tensor) -> Tensor:  # noqa: N8
     else:
         raise TypeError(f"unsupported weight type {type(weight).__name__}")
     return out
+
+
+def _linear_act(a: Tensor, weight, bias: Tensor, act: int) -> Tensor:
+    m, n, k = _check(a, weight.shape, bias)
+    out = Tensor.init((m, n))
+    if isinstance(weight, Tensor):
+        _abi.gemm_act(_abi.FMT_F32, m, n, k, a.data, weight.data, out.data, act=act, bias=bias.data)
+    elif isinstance(weight, qz.QuantizedTensorQ8):
+        _abi.gemm_act(_abi.FMT_Q8_0, m, n, k, a.data, weight.data, out.data, act=act, scale=weight.scale,
+                      bias=bias.data)
+    elif isinstance(weight, qz.QuantizedTensorQ4):
+        _abi.gemm_act(_abi.FMT_Q4_0, m, n, k, a.data, weight.data, out.data, act=act, scale=weight.scale,
+                      bias=bias.data)
+    elif isinstance(weight, qz.QuantizedTensorQ8K):
+        _abi.gemm_act(_abi.FMT_Q8_K, m, n, k, a.data, weight.data, out.data, act=act, scales=weight.scales,
+                      block=weight.block_size, bias=bias.data)
+    else:
+        raise TypeError(f"unsupported weight type {type(weight).__name__}")
+    return out
+
+
+def matmulWithWeightBiasGelu(a: Tensor, weight, bias: Tensor) -> Tensor:  # noqa: N802
+    return _linear_act(a, weight, bias, _abi.ACT_GELU_TANH)
+
+
+def matmulWithWeightBiasGeluExact(a: Tensor, weight, bias: Tensor) -> Tensor:  # noqa: N802
+    return _linear_act(a, weight, bias, _abi.ACT_GELU_ERF)
