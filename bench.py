@@ -314,9 +314,41 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
         torch.cuda.empty_cache()
         return res
 
+    def run_rows_f32(N, K, Ms, seed, label, ncopy):
+        # The tied vocabulary projection as the reference stores it: the f32
+        # token embedding E [n_vocab, d], logits = x . E^T, with E used in
+        # place as a rows-prepared weight (no per-step transpose, no copy).
+        e = torch.from_numpy(synth.normal_matrix(seed, N, K, 0.02)).to(dev)
+        copies = e.reshape(1, N * K).repeat(ncopy, 1)
+        del e
+        handles = [_abi.prepare_rows_dev(_abi.FMT_F32, K, N, copies[i].data_ptr(), 4 * K, 1.0, sptr)
+                   for i in range(ncopy)]
+        torch.cuda.synchronize()
+        res = {}
+        for M in Ms:
+            x = torch.from_numpy(synth.normal_matrix(1001, M, K)).to(dev)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            alg = 4 * N * K + 4 * M * K + 4 * M * N
+
+            def prep(st):
+                for h in handles:
+                    _abi.gemm_prepared(h, M, x.data_ptr(), y.data_ptr(), stream=st)
+
+            ms = timer.time_ms(prep, 3, per_replay=ncopy)
+            gbs = alg / (ms * 1e-3) / 1e9
+            res[f"M{M}"] = {"bytes": alg, "prepared_rows": {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                                             "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+            log(f"gemv {label} M={M} rows in place: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+        for h in handles:
+            _abi.prepared_free(h)
+        del copies
+        torch.cuda.empty_cache()
+        return res
+
     out["q8_1024x4096"] = run(_abi.FMT_Q8_0, 1024, 4096, [1, 8], 2002, "q8 1024x4096")
     out["q4_1280x5120"] = run(_abi.FMT_Q4_0, 1280, 5120, [1, 4, 8], 2002, "q4 1280x5120")
     out["q4_5120x1280"] = run(_abi.FMT_Q4_0, 5120, 1280, [1, 4, 8], 2003, "q4 5120x1280")
+    out["f32_vocab_rows_51866x1280"] = run_rows_f32(51866, 1280, [1, 4], 2004, "f32 vocab rows 51866x1280", 4)
     out["q8_vocab_1280x51866"] = run(_abi.FMT_Q8_0, 1280, 51866, [1], 2004, "q8 vocab 1280x51866", 12)
     out["q4_vocab_1280x51866"] = run(_abi.FMT_Q4_0, 1280, 51866, [1], 2004, "q4 vocab 1280x51866", 24)
     return out

@@ -140,6 +140,16 @@ int tml_hip_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
 int tml_hip_gemm_act(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
                      const float *scales, int64_t block, const float *bias, int act, float *C);
 
+/* tml_hip_gemm with the residual connection fused after the bias:
+ *   C = (A . dequant(B) + bias) + residual      (residual: M*N floats)
+ * Replaces the FFN / attention down-projection followed by its residual
+ * add: matmulWithWeightBias then ops.addInPlace (src/core/transformer.zig:
+ * 223-228), and Whisper's matmul, addBiasInPlace, ops.add
+ * (src/models/whisper/encoder.zig:249-253).  Same additions in the same
+ * order as the reference, so the result is the separate passes' result. */
+int tml_hip_gemm_residual(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                          const float *scales, int64_t block, const float *bias, const float *residual, float *C);
+
 /* Host-pointer form of tml_hip_quantize_dev below (synchronous): the GPU
  * replacement for the load-time quantizers quantizeQ8 / quantizeQ8K /
  * quantizeQ4 (src/core/quantization.zig:98-129, :406-446, :721-754) that
@@ -171,11 +181,14 @@ int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
                      const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
                      void *stream);
 
-/* tml_hip_gemm_dev with an activation applied after alpha, beta and bias:
- *   C = act(alpha * (A . dequant(B)) + beta * C + bias). */
-int tml_hip_gemm_act_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
-                         const float *scales, int64_t block, const float *bias, int act, float *C, float alpha,
-                         float beta, void *stream);
+/* tml_hip_gemm_dev with the full fused epilogue:
+ *   C = act((alpha * (A . dequant(B)) + beta * C + bias) + residual)
+ * residual: device pointer to M*N floats or NULL; it is read before C is
+ * written, element by element, so it may equal C.  act: TML_ACT_*.  The
+ * device-pointer form of tml_hip_gemm_act / tml_hip_gemm_residual. */
+int tml_hip_gemm_ex_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                        const float *scales, int64_t block, const float *bias, const float *residual, int act,
+                        float *C, float alpha, float beta, void *stream);
 
 /* On-device quantizers, bit-identical to the reference's Zig quantizers
  * (quantizeQ8 quantization.zig:98-129, quantizeQ8K :406-446, quantizeQ4
@@ -214,10 +227,29 @@ int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scal
                         tml_prepared_t *out);
 int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const float *bias, float *C, float alpha,
                           float beta, void *stream);
+
+/* A prepared weight from a matrix stored as N rows of K elements, i.e. B
+ * transposed: W row n (at W + n * ldw bytes) is column n of B.  This is the
+ * layout of the tied vocabulary projection, logits = x . token_embedding^T
+ * with token_embedding [n_vocab, d] (src/models/whisper/decoder.zig:
+ * 936-940, :377-383, :619-622), which the reference transposes on every
+ * decode step; here the embedding is used as it is stored.  It is also the
+ * PyTorch [out,in] layout of weights exported untransposed.
+ * fmt F32, Q8_0 (one int8 per element) or Q4_0 (two per byte, even k low;
+ * K must be even so each row starts a byte).  When a row is a multiple of
+ * 16 bytes and W and ldw are 16-byte aligned, W is used in place (no copy;
+ * it must stay valid and unchanged while the handle lives); otherwise a
+ * padded device copy is made on `stream`.  Products with more rows than the
+ * prepared kernel covers (8 f32, 4 Q8_0, 2 Q4_0) run it over consecutive
+ * row blocks.  Free with tml_hip_prepared_free.  No counterpart in the
+ * reference. */
+int tml_hip_prepare_rows_dev(int fmt, int64_t K, int64_t N, const void *W, int64_t ldw, float scale, void *stream,
+                             tml_prepared_t *out);
 int tml_hip_prepared_free(tml_prepared_t w);
-/* tml_hip_gemm_prepared with a fused activation (TML_ACT_*) after the bias. */
-int tml_hip_gemm_prepared_act(tml_prepared_t w, int64_t M, const float *A, const float *bias, int act, float *C,
-                              float alpha, float beta, void *stream);
+/* tml_hip_gemm_prepared with the fused epilogue of tml_hip_gemm_ex_dev
+ * (residual and activation after the bias). */
+int tml_hip_gemm_prepared_ex(tml_prepared_t w, int64_t M, const float *A, const float *bias, const float *residual,
+                             int act, float *C, float alpha, float beta, void *stream);
 
 #ifdef __cplusplus
 }

@@ -136,7 +136,7 @@ def test_fused_gelu_prepared(orc, act, m):
         C = torch.zeros((m, n), dtype=torch.float32, device="cuda:0")
         h = _abi.prepare_dev(fmt, k, n, B.data_ptr(), scale)
         try:
-            _abi.gemm_prepared_act(h, m, A.data_ptr(), C.data_ptr(), act=act, bias_ptr=Bias.data_ptr())
+            _abi.gemm_prepared_ex(h, m, A.data_ptr(), C.data_ptr(), act=act, bias_ptr=Bias.data_ptr())
             torch.cuda.synchronize()
         finally:
             _abi.prepared_free(h)
@@ -153,8 +153,8 @@ def test_fused_gelu_alpha_beta_dev(orc, m, n, k):
     pre = 0.5 * orc.matmul(a, w) - 2.0 * c0 + bias
     for act in ACTS:
         A, B, C, Bias = _dev(a), _dev(w), _dev(c0), _dev(bias)
-        _abi.gemm_act_dev(_abi.FMT_F32, m, n, k, A.data_ptr(), B.data_ptr(), C.data_ptr(), act=act,
-                          bias_ptr=Bias.data_ptr(), alpha=0.5, beta=-2.0)
+        _abi.gemm_ex_dev(_abi.FMT_F32, m, n, k, A.data_ptr(), B.data_ptr(), C.data_ptr(), act=act,
+                         bias_ptr=Bias.data_ptr(), alpha=0.5, beta=-2.0)
         torch.cuda.synchronize()
         assert rel_err(C.cpu().numpy(), orc.apply_act(pre, act)) <= FP32_TOL, act
 
@@ -171,3 +171,139 @@ def test_act_none_matches_plain_entry_point():
     with pytest.raises(_abi.TmlError) as e:
         _abi.gemm_act(_abi.FMT_F32, m, n, k, a, w, c1, act=7)
     assert e.value.code == _abi.TML_ERR_INVALID_ARG
+
+
+# ------------------------------------------------------------ residual add
+@pytest.mark.parametrize("m,n,k", [(1, 1024, 4096), (3, 162, 96), (64, 160, 96), (300, 262, 136),
+                                   (512, 1024, 4096)])
+def test_fused_residual_all_formats(orc, m, n, k):
+    # matmulWithWeightBias then ops.addInPlace (src/core/transformer.zig:
+    # 223-228): (A.B + bias) + residual, the same two additions in the same
+    # order, for every weight type and kernel family.
+    a = rnd(651, m, k)
+    w = rnd(652, k, n, 0.02)
+    bias = synth.normal(653, n, 0.0, 0.5)
+    res = rnd(654, m, n)
+    tb, tr = Tensor.from_numpy(bias), T(res)
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    qk, sk = orc.quantize_q8k(w)
+    cases = [
+        (T(w), orc.matmul_bias(a, w, bias), FP32_TOL),
+        (qz.QuantizedTensorQ8(s, q, (k, n)), orc.matmul_q8(a, q, s) + bias, Q_TOL),
+        (qz.QuantizedTensorQ4(s4, p, (k, n)), orc.matmul_q4(a, p, k, n, s4) + bias, Q_TOL),
+        (qz.QuantizedTensorQ8K(sk, qk, (k, n)), orc.matmul_q8k(a, qk, sk) + bias, Q_TOL),
+    ]
+    for weight, pre, tol in cases:
+        got = dispatch.matmulWithWeightBiasResidual(T(a), weight, tb, tr).numpy()
+        ref = pre + res
+        assert rel_err(got, ref) <= tol, (type(weight).__name__, rel_err(got, ref))
+    with pytest.raises(Exception):
+        dispatch.matmulWithWeightBiasResidual(T(a), T(w), tb, T(res[:, :-1]))
+
+
+@pytest.mark.parametrize("split", [1, 3])
+def test_fused_residual_in_place_dev(orc, forced_env, split):
+    # residual == C (in-place update of the residual stream) on device
+    # pointers, through the GEMM epilogue (split 1) and the split-K reduce.
+    import torch
+    forced_env["TML_GEMM_SPLIT"] = str(split)
+    m, n, k = 200, 256, 1024
+    a, w, x = rnd(661, m, k), rnd(662, k, n, 0.02), rnd(663, m, n)
+    bias = synth.normal(664, n, 0.0, 0.5)
+    A, B, X, Bias = _dev(a), _dev(w), _dev(x), _dev(bias)
+    _abi.gemm_ex_dev(_abi.FMT_F32, m, n, k, A.data_ptr(), B.data_ptr(), X.data_ptr(), residual_ptr=X.data_ptr(),
+                     bias_ptr=Bias.data_ptr())
+    torch.cuda.synchronize()
+    ref = orc.matmul_bias(a, w, bias) + x
+    assert rel_err(X.cpu().numpy(), ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("m", [1, 2, 9])
+def test_fused_residual_prepared(orc, m):
+    import torch
+    k, n = 1280, 1280
+    w, a, x = rnd(671, k, n, 0.02), rnd(672, m, k), rnd(673, m, n)
+    bias = synth.normal(674, n, 0.0, 0.5)
+    q, s = orc.quantize_q8(w)
+    for fmt, b, scale, pre, tol in [(_abi.FMT_F32, w, 1.0, orc.matmul(a, w), FP32_TOL),
+                                    (_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s), Q_TOL)]:
+        B, A, X, Bias = _dev(b), _dev(a), _dev(x), _dev(bias)
+        C = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+        h = _abi.prepare_dev(fmt, k, n, B.data_ptr(), scale)
+        try:
+            _abi.gemm_prepared_ex(h, m, A.data_ptr(), C.data_ptr(), residual_ptr=X.data_ptr(),
+                                  bias_ptr=Bias.data_ptr(), act=_abi.ACT_GELU_ERF)
+            torch.cuda.synchronize()
+        finally:
+            _abi.prepared_free(h)
+        ref = orc.gelu_exact(pre + bias + x)
+        assert rel_err(C.cpu().numpy(), ref) <= tol, (fmt, m)
+
+
+# ------------------------------------- rows-prepared weights (vocab projection)
+def _rows_cases(orc, e):
+    # e: [N, K] rows (a token embedding); the product is x . e^T.
+    n, k = e.shape
+    q, s = orc.quantize_q8(e)
+    cases = [(_abi.FMT_F32, e, 4 * k, 1.0, e.T.copy(), FP32_TOL),
+             (_abi.FMT_Q8_0, q, k, s, orc.dequantize_q8(q, s).reshape(n, k).T.copy(), Q_TOL)]
+    if k % 2 == 0:
+        p, s4 = orc.quantize_q4(e)
+        cases.append((_abi.FMT_Q4_0, p, k // 2, s4, orc.dequantize_q4(p, n * k, s4).reshape(n, k).T.copy(), Q_TOL))
+    return cases
+
+
+@pytest.mark.parametrize("n,k", [(1000, 1280), (333, 77), (130, 96), (64, 100)])
+@pytest.mark.parametrize("m", [1, 2, 3, 9, 20])
+def test_prepared_rows_vs_oracle(orc, n, k, m):
+    # logits = x . E^T with E [n_vocab, d] as stored (decoder.zig:936-940):
+    # in place when a row is a multiple of 16 bytes, a padded copy
+    # otherwise; M beyond the prepared kernel runs it over row blocks, with
+    # the tanh-GELU split and the residual following the global flat index.
+    import torch
+    e = rnd(681, n, k, 0.05)
+    a = rnd(682 + m, m, k)
+    bias = synth.normal(683, n, 0.0, 0.5)
+    x = rnd(684, m, n)
+    for fmt, rows, ldw, scale, bdeq, tol in _rows_cases(orc, e):
+        R, A, Bias, X = _dev(rows), _dev(a), _dev(bias), _dev(x)
+        C = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+        h = _abi.prepare_rows_dev(fmt, k, n, R.data_ptr(), ldw, scale)
+        try:
+            _abi.gemm_prepared(h, m, A.data_ptr(), C.data_ptr())
+            torch.cuda.synchronize()
+            ref = orc.matmul(a, bdeq)
+            assert rel_err(C.cpu().numpy(), ref) <= tol, (fmt, "plain")
+            _abi.gemm_prepared_ex(h, m, A.data_ptr(), C.data_ptr(), bias_ptr=Bias.data_ptr(),
+                                  residual_ptr=X.data_ptr(), act=_abi.ACT_GELU_TANH)
+            torch.cuda.synchronize()
+            ref = orc.gelu_tanh(orc.matmul_bias(a, bdeq, bias) + x)
+            assert rel_err(C.cpu().numpy(), ref) <= tol, (fmt, "epilogue")
+        finally:
+            _abi.prepared_free(h)
+
+
+def test_prepared_rows_in_place_and_errors(orc):
+    # An aligned f32 embedding is used where it lies: a later change to it
+    # shows in the product.  Odd K for Q4_0 rows and a short stride are
+    # rejected.
+    import torch
+    n, k, m = 256, 64, 1
+    e, a = rnd(691, n, k), rnd(692, m, k)
+    E, A = _dev(e), _dev(a)
+    C = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    h = _abi.prepare_rows_dev(_abi.FMT_F32, k, n, E.data_ptr(), 4 * k)
+    try:
+        E.mul_(2.0)
+        _abi.gemm_prepared(h, m, A.data_ptr(), C.data_ptr())
+        torch.cuda.synchronize()
+        assert rel_err(C.cpu().numpy(), orc.matmul(a, 2.0 * e.T.copy())) <= FP32_TOL
+    finally:
+        _abi.prepared_free(h)
+    with pytest.raises(_abi.TmlError) as ex:
+        _abi.prepare_rows_dev(_abi.FMT_Q4_0, 65, n, E.data_ptr(), 33)
+    assert ex.value.code == _abi.TML_ERR_INVALID_SHAPE
+    with pytest.raises(_abi.TmlError) as ex:
+        _abi.prepare_rows_dev(_abi.FMT_F32, k, n, E.data_ptr(), 4 * k - 4)
+    assert ex.value.code == _abi.TML_ERR_INVALID_ARG

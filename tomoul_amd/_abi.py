@@ -54,9 +54,13 @@ SIGNATURES = {
     "tml_hip_prepared_free": (ctypes.c_int, [_vp]),
     "tml_hip_gemm_act": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, ctypes.c_int,
                                         _vp]),
-    "tml_hip_gemm_act_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp,
-                                            ctypes.c_int, _vp, _f, _f, _vp]),
-    "tml_hip_gemm_prepared_act": (ctypes.c_int, [_vp, _i64, _vp, _vp, ctypes.c_int, _vp, _f, _f, _vp]),
+    "tml_hip_prepare_rows_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _i64, _f, _vp,
+                                                ctypes.POINTER(ctypes.c_void_p)]),
+    "tml_hip_gemm_residual": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp,
+                                             _vp]),
+    "tml_hip_gemm_ex_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp,
+                                           ctypes.c_int, _vp, _f, _f, _vp]),
+    "tml_hip_gemm_prepared_ex": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, ctypes.c_int, _vp, _f, _f, _vp]),
 }
 
 
@@ -159,6 +163,13 @@ def gemm_act(fmt: int, m: int, n: int, k: int, a: np.ndarray, b: np.ndarray, c: 
                                  _ptr(c)))
 
 
+def gemm_residual(fmt: int, m: int, n: int, k: int, a: np.ndarray, b: np.ndarray, residual: np.ndarray,
+                  c: np.ndarray, *, scale: float = 1.0, scales: np.ndarray | None = None, block: int = 32,
+                  bias: np.ndarray | None = None) -> None:
+    check(lib().tml_hip_gemm_residual(fmt, m, n, k, _ptr(a), _ptr(b), scale, _ptr(scales), block, _ptr(bias),
+                                      _ptr(residual), _ptr(c)))
+
+
 def quantize(fmt: int, w: np.ndarray, q: np.ndarray, scales: np.ndarray) -> None:
     check(lib().tml_hip_quantize(fmt, w.size, _ptr(w), _ptr(q), _ptr(scales)))
 
@@ -179,11 +190,12 @@ def gemm_dev(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr: in
                                  beta, stream))
 
 
-def gemm_act_dev(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr: int, *, act: int,
-                 scale: float = 1.0, scales_ptr: int | None = None, block: int = 32, bias_ptr: int | None = None,
-                 alpha: float = 1.0, beta: float = 0.0, stream: int | None = None) -> None:
-    check(lib().tml_hip_gemm_act_dev(fmt, m, n, k, a_ptr, b_ptr, scale, scales_ptr, block, bias_ptr, act, c_ptr,
-                                     alpha, beta, stream))
+def gemm_ex_dev(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr: int, *, act: int = ACT_NONE,
+                residual_ptr: int | None = None, scale: float = 1.0, scales_ptr: int | None = None, block: int = 32,
+                bias_ptr: int | None = None, alpha: float = 1.0, beta: float = 0.0,
+                stream: int | None = None) -> None:
+    check(lib().tml_hip_gemm_ex_dev(fmt, m, n, k, a_ptr, b_ptr, scale, scales_ptr, block, bias_ptr, residual_ptr,
+                                    act, c_ptr, alpha, beta, stream))
 
 
 def quantize_dev(fmt: int, n: int, w_ptr: int, q_ptr: int, scales_ptr: int, stream: int | None = None) -> None:
@@ -198,14 +210,24 @@ def prepare_dev(fmt: int, k: int, n: int, b_ptr: int, scale: float = 1.0, stream
     return h.value
 
 
+def prepare_rows_dev(fmt: int, k: int, n: int, w_ptr: int, ldw: int, scale: float = 1.0,
+                     stream: int | None = None) -> int:
+    """Prepared weight from N rows of K elements at w_ptr (row stride ldw bytes),
+    e.g. a token embedding [n_vocab, d] for logits = x . E^T; returns a handle."""
+    h = ctypes.c_void_p()
+    check(lib().tml_hip_prepare_rows_dev(fmt, k, n, w_ptr, ldw, scale, stream, ctypes.byref(h)))
+    return h.value
+
+
 def gemm_prepared(handle: int, m: int, a_ptr: int, c_ptr: int, *, bias_ptr: int | None = None, alpha: float = 1.0,
                   beta: float = 0.0, stream: int | None = None) -> None:
     check(lib().tml_hip_gemm_prepared(handle, m, a_ptr, bias_ptr, c_ptr, alpha, beta, stream))
 
 
-def gemm_prepared_act(handle: int, m: int, a_ptr: int, c_ptr: int, *, act: int, bias_ptr: int | None = None,
-                      alpha: float = 1.0, beta: float = 0.0, stream: int | None = None) -> None:
-    check(lib().tml_hip_gemm_prepared_act(handle, m, a_ptr, bias_ptr, act, c_ptr, alpha, beta, stream))
+def gemm_prepared_ex(handle: int, m: int, a_ptr: int, c_ptr: int, *, act: int = ACT_NONE,
+                     residual_ptr: int | None = None, bias_ptr: int | None = None, alpha: float = 1.0,
+                     beta: float = 0.0, stream: int | None = None) -> None:
+    check(lib().tml_hip_gemm_prepared_ex(handle, m, a_ptr, bias_ptr, residual_ptr, act, c_ptr, alpha, beta, stream))
 
 
 def prepared_free(handle: int) -> None:

@@ -50,6 +50,7 @@ struct DmaArgs {
     float *ws;            // split partials: [split][M][N]
     const float *zero;
     int act;              // TML_ACT_* after the bias
+    const float *res;     // [M,N] residual added after the bias, or nullptr
     long long tail0;      // tml_act_tail0(M * N)
 };
 
@@ -316,7 +317,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
                     float v = a.alpha * acc[i][j][r];
                     if (a.beta != 0.0f) v += a.beta * *cp;
                     if (a.bias) v += bcol;
-                    *cp = tml_apply_act(v, a.act, (long long)row * a.N + col, a.tail0);
+                    const long long flat = (long long)row * a.N + col;
+                    if (a.res) v += a.res[flat];
+                    *cp = tml_apply_act(v, a.act, flat, a.tail0);
                 }
             }
         }
@@ -327,8 +330,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
 // aligned.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws, int nsplit, long long mn,
                                                             int n, float *C, float alpha, float beta,
-                                                            const float *__restrict__ bias, bool vec, int act,
-                                                            long long tail0) {
+                                                            const float *__restrict__ bias,
+                                                            const float *res, bool vec, int act, long long tail0) {
     const long long stride = (long long)gridDim.x * blockDim.x;
     if (vec) {
         for (long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x; q < mn / 4; q += stride) {
@@ -338,6 +341,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
             float *cp = C + 4 * q;
             if (beta != 0.0f) v += beta * *(const floatx4 *)cp;
             if (bias) v += *(const floatx4 *)(bias + (4 * q) % n);
+            if (res) v += *(const floatx4 *)(res + 4 * q);
             if (act != TML_ACT_NONE)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) v[r] = tml_apply_act(v[r], act, 4 * q + r, tail0);
@@ -350,6 +354,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
             float v = alpha * acc;
             if (beta != 0.0f) v += beta * C[e];
             if (bias) v += bias[e % n];
+            if (res) v += res[e];
             C[e] = tml_apply_act(v, act, e, tail0);
         }
     }
@@ -395,6 +400,7 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
     a.spl = p.spl;
     a.ws = ws.partials;
     a.act = m.act;
+    a.res = m.res;
     a.tail0 = tml_act_tail0((long long)m.M * m.N);
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
     if (p.nsplit > 1 && (ws.partials == nullptr || ws.partial_floats < (size_t)p.nsplit * m.M * m.N))
@@ -421,8 +427,9 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
         const int64_t n4 = (m.M * m.N + 3) / 4;
         const int64_t blocks = (n4 + 255) / 256;
         splitk_reduce_kernel<<<dim3((unsigned)(blocks < 65535 ? blocks : 65535)), 256, 0, s>>>(
-            ws.partials, p.nsplit, m.M * m.N, m.N, m.C, m.alpha_eff, m.beta, m.bias,
-            m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0),
+            ws.partials, p.nsplit, m.M * m.N, m.N, m.C, m.alpha_eff, m.beta, m.bias, m.res,
+            m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0) &&
+                (m.res == nullptr || ((uintptr_t)m.res % 16) == 0),
             m.act, tml_act_tail0((long long)m.M * m.N));
         TML_HIP_TRY(hipGetLastError());
     }

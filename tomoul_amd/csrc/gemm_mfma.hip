@@ -51,6 +51,7 @@ struct GemmKArgs {
     int xcd_remap;
     const void *zero;
     int act;             // TML_ACT_* after the bias
+    const float *res;    // [M,N] residual added after the bias, or nullptr
     long long tail0;     // tml_act_tail0(M * N)
 };
 
@@ -340,7 +341,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_mfma_kernel(GemmKArgs a) {
                     float v = a.alpha * acc[i][j][r];
                     if (a.beta != 0.0f) v += a.beta * *cp;
                     if (a.bias) v += bcol;
-                    *cp = tml_apply_act(v, a.act, (long long)row * a.N + col, a.tail0);
+                    const long long flat = (long long)row * a.N + col;
+                    if (a.res) v += a.res[flat];
+                    *cp = tml_apply_act(v, a.act, flat, a.tail0);
                 }
             }
         }
@@ -489,7 +492,7 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
     ka.M = (int)m.M; ka.N = (int)m.N; ka.K = (int)m.K;
     ka.A = m.A; ka.B = m.B; ka.scales = m.scales; ka.block = m.block;
     ka.bias = m.bias; ka.C = m.C; ka.alpha = m.alpha_eff; ka.beta = m.beta;
-    ka.act = m.act; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
+    ka.act = m.act; ka.res = m.res; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
     ka.zero = m.zero;
     int cfg = env_int("TML_GEMM_TILE", 0) - 1;
     if (cfg < 0 || cfg >= kNumCfgs) cfg = pick_cfg(m.M, m.N, cus);

@@ -54,6 +54,7 @@ struct GemvKArgs {
     unsigned *counters;  // one per segment, zero between launches
     const void *zero;
     int act;             // TML_ACT_* after the bias
+    const float *res;    // [M,N] residual added after the bias, or nullptr
     long long tail0;     // tml_act_tail0(M * N)
 };
 
@@ -287,7 +288,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
         float v = a.alpha * p;
         if (a.beta != 0.0f) v += a.beta * *cp;
         if (a.bias) v += a.bias[col];
-        *cp = tml_apply_act(v, a.act, (long long)m * a.N + col, a.tail0);
+        const long long flat = (long long)m * a.N + col;
+        if (a.res) v += a.res[flat];
+        *cp = tml_apply_act(v, a.act, flat, a.tail0);
     };
     auto useful = [&](int o) __attribute__((always_inline)) {
         return o < NOUT && o / SC < a.M && col0 + o % SC < a.N;
@@ -506,7 +509,7 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     ka.nseg = p.nseg; ka.nsplit = p.nsplit; ka.nb = p.nb;
     ka.ws = ws.partials; ka.counters = ws.counters;
     ka.zero = m.zero;
-    ka.act = m.act; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
+    ka.act = m.act; ka.res = m.res; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
     switch (m.fmt) {
         case TML_FMT_F32: return launch_fmt<TML_FMT_F32>(ka, p, s);
         case TML_FMT_Q8_0: return launch_fmt<TML_FMT_Q8_0>(ka, p, s);

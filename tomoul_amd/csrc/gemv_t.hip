@@ -48,6 +48,7 @@ struct GemvTArgs {
     int nchunk;           // 16-byte chunks per prepared row
     const void *zero;
     int act;              // TML_ACT_* after the bias
+    const float *res;     // [M,N] residual added after the bias, or nullptr
     long long tail0;      // tml_act_tail0(M * N)
 };
 
@@ -220,7 +221,9 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
         float v = a.alpha * val;
         if (a.beta != 0.0f) v += a.beta * *cp;
         if (a.bias) v += a.bias[n];
-        *cp = tml_apply_act(v, a.act, (long long)m * a.N + n, a.tail0);
+        const long long flat = (long long)m * a.N + n;
+        if (a.res) v += a.res[flat];
+        *cp = tml_apply_act(v, a.act, flat, a.tail0);
     }
 }
 
@@ -356,6 +359,10 @@ int64_t prepared_row_bytes(int fmt, int64_t K) {
     return r > 0 ? r : 16;
 }
 
+int64_t prepared_gemv_max_m(int fmt) {
+    return fmt == TML_FMT_F32 ? 8 : fmt == TML_FMT_Q8_0 ? 4 : fmt == TML_FMT_Q4_0 ? 2 : 0;
+}
+
 bool prepared_gemv_supported(int fmt, int64_t M, int64_t K) {
     if (fmt != TML_FMT_F32 && fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0) return false;
     if (M < 1 || M > kPreparedGemvMaxM || K >= ((int64_t)1 << 30)) return false;
@@ -383,8 +390,8 @@ Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, 
 }
 
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
-                     const float *bias, float *C, float alpha_eff, float beta, const void *zero, int act,
-                     hipStream_t s) {
+                     const float *bias, const float *res, float *C, float alpha_eff, float beta,
+                     const void *zero, int act, long long tail0, hipStream_t s) {
     if (!prepared_gemv_supported(fmt, M, K)) return Status::Err(TML_ERR_INVALID_ARG, "prepared GEMV: unsupported");
     if (N >= ((int64_t)1 << 30) || K >= ((int64_t)1 << 30))
         return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV dimension exceeds 2^30");
@@ -397,7 +404,8 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     ka.nchunk = (int)((prepared_row_bytes(fmt, K) + 15) / 16);
     ka.zero = zero;
     ka.act = act;
-    ka.tail0 = tml_act_tail0((long long)M * N);
+    ka.res = res;
+    ka.tail0 = tail0;
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) {
         int n = 0;

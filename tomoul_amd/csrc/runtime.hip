@@ -67,9 +67,10 @@ struct Prepared {
     int fmt = 0;
     int64_t K = 0, N = 0;
     float scale = 1.0f;
-    const void *B = nullptr;
+    const void *B = nullptr;   // the [K,N] weight, or null for a rows-prepared weight
     void *Bt = nullptr;
     int64_t ldt = 0;
+    bool owns_bt = true;       // false: Bt is the caller's buffer, used in place
 };
 
 struct Registered {
@@ -81,7 +82,7 @@ struct Registered {
 struct DeviceCtx {
     int device = -1;
     hipStream_t stream = nullptr;
-    DevBuf a, b, c, bias, scales, qtmp;  // staging of the host-pointer API
+    DevBuf a, b, c, bias, res, scales, qtmp;  // staging of the host-pointer API
     DevBuf ws, counters;                 // split-K workspace (gemv, gemm)
     DevBuf zero;                         // kZeroBlockBytes of zeros
     std::unordered_map<const void *, Registered> weights;
@@ -166,7 +167,7 @@ bool valid_act(int act) { return act == TML_ACT_NONE || act == TML_ACT_GELU_ERF 
 
 Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B,
                 float scale, const float *scales, int64_t block, const float *bias, float *C, float alpha,
-                float beta, hipStream_t s, int act = TML_ACT_NONE) {
+                float beta, hipStream_t s, int act = TML_ACT_NONE, const float *res = nullptr) {
     if (!valid_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
     if (!valid_act(act)) return Status::Err(TML_ERR_INVALID_ARG, "unknown activation");
     if (M < 0 || N < 0 || K < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
@@ -182,6 +183,7 @@ Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const fl
     m.alpha_eff = (fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0) ? alpha * scale : alpha;
     m.zero = c->zero.p;
     m.act = act;
+    m.res = res;
     Workspace ws;
     TML_TRY(ensure_workspace(c, m, s, &ws));
     if (M <= kGemvMaxM) return launch_gemv(m, ws, s);
@@ -225,18 +227,32 @@ Status make_prepared(DeviceCtx *c, int fmt, int64_t K, int64_t N, const void *B,
 // C = alpha * A . dequant(B) + beta * C + bias with a prepared weight: the
 // K-contiguous decoder kernel when it covers M and K, else the [K,N] path.
 Status gemm_prepared(DeviceCtx *c, const Prepared *p, int64_t M, const float *A, const float *bias, float *C,
-                     float alpha, float beta, hipStream_t s, int act = TML_ACT_NONE) {
+                     float alpha, float beta, hipStream_t s, int act = TML_ACT_NONE,
+                     const float *res = nullptr) {
     if (M < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
     if (!valid_act(act)) return Status::Err(TML_ERR_INVALID_ARG, "unknown activation");
     if (M == 0 || p->N == 0) return Status::Ok();
     if (C == nullptr || (p->K > 0 && A == nullptr)) return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
-    if (prepared_gemv_supported(p->fmt, M, p->K)) {
-        const float alpha_eff = (p->fmt == TML_FMT_Q8_0 || p->fmt == TML_FMT_Q4_0) ? alpha * p->scale : alpha;
-        return launch_gemv_t(p->fmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, C, alpha_eff, beta, c->zero.p, act, s);
+    const float alpha_eff = (p->fmt == TML_FMT_Q8_0 || p->fmt == TML_FMT_Q4_0) ? alpha * p->scale : alpha;
+    const long long tail0 = tml_act_tail0((long long)M * p->N);
+    if (prepared_gemv_supported(p->fmt, M, p->K))
+        return launch_gemv_t(p->fmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, res, C, alpha_eff, beta, c->zero.p, act,
+                             tail0, s);
+    if (p->B != nullptr)
+        return gemm_dev(c, p->fmt, M, p->N, p->K, A, p->B, p->scale, nullptr, 0, bias, C, alpha, beta, s, act, res);
+    // Rows-prepared weight (no [K,N] form): the prepared kernel over
+    // consecutive blocks of rows.  Each launch reads the whole weight, so
+    // this serves short prompts; the activation's flat-index split is kept
+    // global by shifting tail0 per block.
+    const int64_t mr = prepared_gemv_max_m(p->fmt);
+    for (int64_t r0 = 0; r0 < M; r0 += mr) {
+        const int64_t rows = M - r0 < mr ? M - r0 : mr;
+        const size_t off = (size_t)r0 * (size_t)p->N;
+        TML_TRY(launch_gemv_t(p->fmt, rows, p->N, p->K, A + (size_t)r0 * p->K, p->Bt, p->ldt, bias,
+                              res ? res + off : nullptr, C + off, alpha_eff, beta, c->zero.p, act,
+                              tail0 - (long long)off, s));
     }
-    if (p->B == nullptr)
-        return Status::Err(TML_ERR_INVALID_SHAPE, "row count beyond the prepared kernel and no [K,N] weight to fall back to");
-    return gemm_dev(c, p->fmt, M, p->N, p->K, A, p->B, p->scale, nullptr, 0, bias, C, alpha, beta, s, act);
+    return Status::Ok();
 }
 
 // Resident copy of a registered host buffer of at least `bytes`, or null.
@@ -264,7 +280,7 @@ Status upload(DeviceCtx *c, DevBuf &buf, const void *host, size_t bytes, const v
 // Host-pointer call: stage operands, run, copy C back, wait.
 Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
                  const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
-                 int act = TML_ACT_NONE) {
+                 int act = TML_ACT_NONE, const float *res = nullptr) {
     if (!valid_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
     if (!valid_act(act)) return Status::Err(TML_ERR_INVALID_ARG, "unknown activation");
     if (M < 0 || N < 0 || K < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
@@ -284,6 +300,8 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
     }
     if (bias) TML_TRY(upload(c, c->bias, bias, (size_t)N * sizeof(float), &dBias));
     const size_t cbytes = (size_t)M * N * sizeof(float);
+    const void *dRes = nullptr;
+    if (res) TML_TRY(upload(c, c->res, res, cbytes, &dRes));
     TML_TRY(c->c.ensure(cbytes));
     if (beta != 0.0f) TML_HIP_TRY(hipMemcpyAsync(c->c.p, C, cbytes, hipMemcpyHostToDevice, c->stream));
     // A registered weight used at a decoder row count gets (once) and then
@@ -306,10 +324,11 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
             reg->prep = p;
         }
         TML_TRY(gemm_prepared(c, p, M, (const float *)dA, (const float *)dBias, (float *)c->c.p, alpha, beta,
-                              c->stream, act));
+                              c->stream, act, (const float *)dRes));
     } else {
         TML_TRY(gemm_dev(c, fmt, M, N, K, (const float *)dA, dB, scale, (const float *)dS, block,
-                         (const float *)dBias, (float *)c->c.p, alpha, beta, c->stream, act));
+                         (const float *)dBias, (float *)c->c.p, alpha, beta, c->stream, act,
+                         (const float *)dRes));
     }
     TML_HIP_TRY(hipMemcpyAsync(C, c->c.p, cbytes, hipMemcpyDeviceToHost, c->stream));
     TML_HIP_TRY(hipStreamSynchronize(c->stream));
@@ -425,6 +444,12 @@ int tml_hip_gemm_act(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     return report(host_gemm(fmt, M, N, K, A, B, scale, scales, block, bias, C, 1.0f, 0.0f, act));
 }
 
+int tml_hip_gemm_residual(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                          const float *scales, int64_t block, const float *bias, const float *residual, float *C) {
+    if (residual == nullptr && M > 0 && N > 0) return report(Status::Err(TML_ERR_INVALID_ARG, "null residual"));
+    return report(host_gemm(fmt, M, N, K, A, B, scale, scales, block, bias, C, 1.0f, 0.0f, TML_ACT_NONE, residual));
+}
+
 int tml_hip_quantize(int fmt, int64_t n, const float *w, void *q, float *scales) {
     if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K)
         return report(Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0 or Q8_K"));
@@ -514,14 +539,14 @@ int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     return report(gemm_dev(c, fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, (hipStream_t)stream));
 }
 
-int tml_hip_gemm_act_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
-                         const float *scales, int64_t block, const float *bias, int act, float *C, float alpha,
-                         float beta, void *stream) {
+int tml_hip_gemm_ex_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                        const float *scales, int64_t block, const float *bias, const float *residual, int act,
+                        float *C, float alpha, float beta, void *stream) {
     DeviceCtx *c = nullptr;
     Status s = current_ctx(&c);
     if (!s.ok()) return report(s);
     return report(gemm_dev(c, fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, (hipStream_t)stream,
-                           act));
+                           act, residual));
 }
 
 int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scale, void *stream,
@@ -537,6 +562,57 @@ int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scal
     return report(s);
 }
 
+int tml_hip_prepare_rows_dev(int fmt, int64_t K, int64_t N, const void *W, int64_t ldw, float scale, void *stream,
+                             tml_prepared_t *out) {
+    if (out == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null handle pointer"));
+    *out = nullptr;
+    if (!preparable_fmt(fmt))
+        return report(Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, Q8_0 or Q4_0"));
+    if (K < 0 || N < 0) return report(Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension"));
+    if (K >= ((int64_t)1 << 30) || N >= ((int64_t)1 << 30))
+        return report(Status::Err(TML_ERR_INVALID_SHAPE, "prepare: dimension exceeds 2^30"));
+    if (fmt == TML_FMT_Q4_0 && K % 2 != 0)
+        return report(Status::Err(TML_ERR_INVALID_SHAPE, "Q4_0 rows need an even K (each row starts a byte)"));
+    const int64_t row = packed_row_bytes(fmt, K);
+    if (ldw < row) return report(Status::Err(TML_ERR_INVALID_ARG, "row stride shorter than a row"));
+    if (W == nullptr && K > 0 && N > 0) return report(Status::Err(TML_ERR_INVALID_ARG, "null weight pointer"));
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    Prepared *p = new Prepared();
+    p->device = c->device;
+    p->fmt = fmt;
+    p->K = K;
+    p->N = N;
+    p->scale = scale;
+    if (K > 0 && row % 16 == 0 && ldw % 16 == 0 && ((uintptr_t)W % 16) == 0) {
+        // Already the prepared layout: use the caller's rows in place.
+        p->Bt = const_cast<void *>(W);
+        p->ldt = ldw;
+        p->owns_bt = false;
+        *out = (tml_prepared_t)p;
+        return report(Status::Ok());
+    }
+    p->ldt = prepared_row_bytes(fmt, K);
+    const size_t bytes = (size_t)(N > 0 ? N : 1) * (size_t)p->ldt;
+    auto build = [&]() -> Status {
+        TML_HIP_TRY(hipMalloc(&p->Bt, bytes));
+        TML_HIP_TRY(hipMemsetAsync(p->Bt, 0, bytes, (hipStream_t)stream));
+        if (K > 0 && N > 0)
+            TML_HIP_TRY(hipMemcpy2DAsync(p->Bt, (size_t)p->ldt, W, (size_t)ldw, (size_t)row, (size_t)N,
+                                         hipMemcpyDeviceToDevice, (hipStream_t)stream));
+        return Status::Ok();
+    };
+    s = build();
+    if (!s.ok()) {
+        if (p->Bt) (void)hipFree(p->Bt);
+        delete p;
+        return report(s);
+    }
+    *out = (tml_prepared_t)p;
+    return report(Status::Ok());
+}
+
 int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const float *bias, float *C, float alpha,
                           float beta, void *stream) {
     if (w == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null prepared weight"));
@@ -548,15 +624,15 @@ int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const flo
     return report(gemm_prepared(c, p, M, A, bias, C, alpha, beta, (hipStream_t)stream));
 }
 
-int tml_hip_gemm_prepared_act(tml_prepared_t w, int64_t M, const float *A, const float *bias, int act, float *C,
-                              float alpha, float beta, void *stream) {
+int tml_hip_gemm_prepared_ex(tml_prepared_t w, int64_t M, const float *A, const float *bias, const float *residual,
+                             int act, float *C, float alpha, float beta, void *stream) {
     if (w == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null prepared weight"));
     DeviceCtx *c = nullptr;
     Status s = current_ctx(&c);
     if (!s.ok()) return report(s);
     const Prepared *p = (const Prepared *)w;
     if (p->device != c->device) return report(Status::Err(TML_ERR_INVALID_ARG, "prepared weight of another device"));
-    return report(gemm_prepared(c, p, M, A, bias, C, alpha, beta, (hipStream_t)stream, act));
+    return report(gemm_prepared(c, p, M, A, bias, C, alpha, beta, (hipStream_t)stream, act, residual));
 }
 
 int tml_hip_prepared_free(tml_prepared_t w) {
@@ -564,7 +640,7 @@ int tml_hip_prepared_free(tml_prepared_t w) {
     Prepared *p = (Prepared *)w;
     auto run = [&]() -> Status {
         TML_HIP_TRY(hipDeviceSynchronize());
-        TML_HIP_TRY(hipFree(p->Bt));
+        if (p->owns_bt) TML_HIP_TRY(hipFree(p->Bt));
         return Status::Ok();
     };
     Status s = run();

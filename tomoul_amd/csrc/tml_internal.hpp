@@ -36,7 +36,10 @@ Status hip_status(hipError_t e, const char *what);
 // One GEMM / GEMV problem on device-resident operands:
 //   C = alpha_eff * (A . Bdeq) + beta * C + bias
 // where Bdeq is the f32 value of B's element (for Q8_0 / Q4_0 the integer
-// value; their per-tensor scale is folded into alpha_eff).
+// value; their per-tensor scale is folded into alpha_eff), then
+//   C = act(C + res)
+// with an optional [M,N] residual `res` (read before C is written, per
+// element, so it may alias C) and activation `act`.
 struct MatmulArgs {
     int64_t M, N, K;
     const float *A;        // [M,K] row-major
@@ -50,6 +53,7 @@ struct MatmulArgs {
     int fmt;
     const void *zero;      // >= 64 zero bytes of device memory (see below)
     int act = TML_ACT_NONE;  // activation after the bias (TML_ACT_*)
+    const float *res = nullptr;  // [M,N] residual added after the bias (may equal C)
 };
 
 // Activations of the epilogue, restating the reference's CPU code.
@@ -170,10 +174,17 @@ constexpr int64_t kGemvMaxM = 8;
 constexpr int64_t kPreparedGemvMaxM = 8;  // f32; Q8_0 <= 4, Q4_0 <= 2 (prepared_gemv_supported)
 int64_t prepared_row_bytes(int fmt, int64_t K);
 bool prepared_gemv_supported(int fmt, int64_t M, int64_t K);
+// Bytes of one row of K elements of fmt in the reference's packing (Q4_0:
+// two per byte), before the 16-byte padding of a prepared row.
+inline int64_t packed_row_bytes(int fmt, int64_t K) {
+    return fmt == TML_FMT_F32 ? 4 * K : (fmt == TML_FMT_Q4_0 ? (K + 1) / 2 : K);
+}
 Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, int64_t ldt, hipStream_t s);
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
-                     const float *bias, float *C, float alpha_eff, float beta, const void *zero, int act,
-                     hipStream_t s);
+                     const float *bias, const float *res, float *C, float alpha_eff, float beta,
+                     const void *zero, int act, long long tail0, hipStream_t s);
+// Largest M the prepared kernel covers for fmt (8 f32, 4 Q8_0, 2 Q4_0).
+int64_t prepared_gemv_max_m(int fmt);
 
 // Tuning overrides for experiments (0 = heuristic).  Read from the
 // TML_GEMM_TILE / TML_GEMV_SPLIT environment variables once.

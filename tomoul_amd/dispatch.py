@@ -18,6 +18,12 @@ over the whole output are fused the same way:
 The activation is applied in the kernel epilogue after the bias, per output
 element, with the reference's vector/scalar split of ops.gelu preserved (the
 flat index decides, see include/tomoul_hip.h).
+
+The down-projection followed by its residual connection is fused too:
+  matmulWithWeightBiasResidual(input, weight, b, residual)
+      matmulWithWeightBias + ops.addInPlace(out, residual)
+      src/core/transformer.zig:223-228; Whisper's matmul + addBiasInPlace +
+      ops.add(x1, fc2), src/models/whisper/encoder.zig:249-253
 """
 from __future__ import annotations
 
@@ -64,22 +70,34 @@ def matmulWithWeightBias(a: Tensor, weight, bias: Tensor) -> Tensor:  # noqa: N8
     return out
 
 
+def _weight_args(weight) -> tuple[int, dict]:
+    """(format, keyword arguments) of the C ABI for a weight of any type."""
+    if isinstance(weight, Tensor):
+        return _abi.FMT_F32, {}
+    if isinstance(weight, qz.QuantizedTensorQ8):
+        return _abi.FMT_Q8_0, {"scale": weight.scale}
+    if isinstance(weight, qz.QuantizedTensorQ4):
+        return _abi.FMT_Q4_0, {"scale": weight.scale}
+    if isinstance(weight, qz.QuantizedTensorQ8K):
+        return _abi.FMT_Q8_K, {"scales": weight.scales, "block": weight.block_size}
+    raise TypeError(f"unsupported weight type {type(weight).__name__}")
+
+
 def _linear_act(a: Tensor, weight, bias: Tensor, act: int) -> Tensor:
     m, n, k = _check(a, weight.shape, bias)
+    fmt, kw = _weight_args(weight)
     out = Tensor.init((m, n))
-    if isinstance(weight, Tensor):
-        _abi.gemm_act(_abi.FMT_F32, m, n, k, a.data, weight.data, out.data, act=act, bias=bias.data)
-    elif isinstance(weight, qz.QuantizedTensorQ8):
-        _abi.gemm_act(_abi.FMT_Q8_0, m, n, k, a.data, weight.data, out.data, act=act, scale=weight.scale,
-                      bias=bias.data)
-    elif isinstance(weight, qz.QuantizedTensorQ4):
-        _abi.gemm_act(_abi.FMT_Q4_0, m, n, k, a.data, weight.data, out.data, act=act, scale=weight.scale,
-                      bias=bias.data)
-    elif isinstance(weight, qz.QuantizedTensorQ8K):
-        _abi.gemm_act(_abi.FMT_Q8_K, m, n, k, a.data, weight.data, out.data, act=act, scales=weight.scales,
-                      block=weight.block_size, bias=bias.data)
-    else:
-        raise TypeError(f"unsupported weight type {type(weight).__name__}")
+    _abi.gemm_act(fmt, m, n, k, a.data, weight.data, out.data, act=act, bias=bias.data, **kw)
+    return out
+
+
+def matmulWithWeightBiasResidual(a: Tensor, weight, bias: Tensor, residual: Tensor) -> Tensor:  # noqa: N802
+    m, n, k = _check(a, weight.shape, bias)
+    if tuple(residual.shape) != (m, n):
+        raise ops.OpsError.ShapeMismatch(f"residual {residual.shape} does not match the output ({m}, {n})")
+    fmt, kw = _weight_args(weight)
+    out = Tensor.init((m, n))
+    _abi.gemm_residual(fmt, m, n, k, a.data, weight.data, residual.data, out.data, bias=bias.data, **kw)
     return out
 
 
