@@ -58,6 +58,8 @@ extern "C" {
 #define TML_FMT_Q8_0 1
 #define TML_FMT_Q4_0 2
 #define TML_FMT_Q8_K 3
+#define TML_FMT_F16 4  /* IEEE binary16 [K,N], F16Tensor / matmulF32F16
+                          (src/core/quantization.zig:1859-1962); .tl code 4 */
 
 /* Activation applied after the bias, in the kernel epilogue. */
 #define TML_ACT_NONE 0
@@ -120,6 +122,11 @@ int tml_hip_sgemm_q8k(int64_t M, int64_t N, int64_t K, const float *A, const int
  * SIMD loop, odd N is handled exactly (every element is addressed as
  * k*N + j). */
 int tml_hip_sgemm_q4(int64_t M, int64_t N, int64_t K, const float *A, const uint8_t *Bp, float scale, float *C);
+
+/* C[M,N] = A[M,K] . f32(Bh[K,N]) with Bh binary16: zblas.sgemmF16 at
+ * src/core/quantization.zig:1946 (matmulF32F16, :1921-1962; its fallback
+ * accumulates a * f32(b) in f32, ascending k). */
+int tml_hip_sgemm_f16(int64_t M, int64_t N, int64_t K, const float *A, const uint16_t *Bh, float *C);
 
 /* Generic host-pointer matmul with an optional fused bias:
  *   C = A . dequant(B) + bias      (bias may be NULL)
@@ -192,9 +199,11 @@ int tml_hip_gemm_ex_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A
 
 /* On-device quantizers, bit-identical to the reference's Zig quantizers
  * (quantizeQ8 quantization.zig:98-129, quantizeQ8K :406-446, quantizeQ4
- * :721-754).  w holds n floats; q receives n int8 (Q8_0 / Q8_K) or
- * ceil(n/2) packed bytes (Q4_0); scales receives 1 float (Q8_0 / Q4_0) or
- * ceil(n/32) floats (Q8_K).  Device pointers, asynchronous on stream. */
+ * :721-754) and its f32 -> f16 converter toF16 (:1907-1917, IEEE round to
+ * nearest even).  w holds n floats; q receives n int8 (Q8_0 / Q8_K),
+ * ceil(n/2) packed bytes (Q4_0) or n binary16 values (F16); scales receives
+ * 1 float (Q8_0 / Q4_0), ceil(n/32) floats (Q8_K) or nothing (F16, may be
+ * NULL).  Device pointers, asynchronous on stream. */
 int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream);
 
 /* ------------------------------------------------------ prepared weights */

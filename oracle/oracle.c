@@ -32,6 +32,14 @@
  *                                   bitwise equality with orc_matmul_f32 on the
  *                                   dequantized weights (the reference's own
  *                                   definition of the scalar path).
+ *   orc_f32_to_f16 / orc_f16_to_f32 numpy's IEEE binary16 conversions
+ *                                   bitwise: all 65536 halves exhaustively,
+ *                                   and f32 -> f16 (round to nearest even)
+ *                                   on ties, subnormals, overflow and a large
+ *                                   random sample.
+ *   orc_matmul_f16                  == orc_matmul_f32 on the widened weight,
+ *                                   bitwise (the reference's own definition of
+ *                                   its scalar path).
  *   orc_erf_as                      |erf_as - erf| <= the published A&S
  *                                   7.1.26 bound (1.5e-7) plus rounding over a
  *                                   dense grid, odd symmetry, erf(0) = 0.
@@ -384,6 +392,66 @@ void orc_matmul_q4_mt(i64 M, i64 N, i64 K, const float *A, const uint8_t *packed
                       int nthreads) {
 #pragma omp parallel for num_threads(nthreads) schedule(static)
     for (i64 i = 0; i < M; i++) orc_matmul_q4(1, N, K, A + i * K, packed, s, C + i * N);
+}
+
+/* ------------------------------------------------------------------------ */
+/* F16 weights                                                               */
+/* ------------------------------------------------------------------------ */
+
+/* toF16 (quantization.zig:1907-1917): Zig's @floatCast f32 -> f16, IEEE
+ * round to nearest even; overflow to infinity; NaN stays NaN (quiet). */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* >= 65520: rounds past 65504 */
+    if (ax < 0x38800000u) {                                   /* below 2^-14: subnormal or zero */
+        int e = (int)(ax >> 23);
+        if (e < 102) return (uint16_t)sign;                    /* below 2^-25: rounds to zero */
+        uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+        int shift = 126 - e;                                   /* 14..24 */
+        uint32_t r = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (r & 1u))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = (ax - 0x38000000u) >> 13, rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+    return (uint16_t)(sign | r);
+}
+
+/* @floatCast f16 -> f32: exact. */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, bits;
+    if (e == 0) {
+        float v = ldexpf((float)m, -24);
+        return sign ? -v : v;
+    }
+    bits = e == 31 ? (sign | 0x7F800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+void orc_to_f16(i64 n, const float *v, uint16_t *h) {
+    for (i64 i = 0; i < n; i++) h[i] = orc_f32_to_f16(v[i]);
+}
+
+void orc_from_f16(i64 n, const uint16_t *h, float *v) {
+    for (i64 i = 0; i < n; i++) v[i] = orc_f16_to_f32(h[i]);
+}
+
+/* matmulF32F16 fallback (quantization.zig:1949-1958): C zeroed, then i, k,
+ * j: c[i,j] += a[i,k] * f32(b[k,j]). */
+void orc_matmul_f16(i64 M, i64 N, i64 K, const float *A, const uint16_t *B, float *C) {
+    memset(C, 0, sizeof(float) * (size_t)(M * N));
+    for (i64 i = 0; i < M; i++)
+        for (i64 k = 0; k < K; k++) {
+            float a = A[i * K + k];
+            const uint16_t *br = B + k * N;
+            float *cr = C + i * N;
+            for (i64 j = 0; j < N; j++) cr[j] += a * orc_f16_to_f32(br[j]);
+        }
 }
 
 /* ------------------------------------------------------------------------ */

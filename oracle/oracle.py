@@ -23,6 +23,7 @@ _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
 _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _i64 = ctypes.c_int64
 
 
@@ -64,6 +65,9 @@ def lib() -> ctypes.CDLL:
         "orc_matmul_q4_mt": (None, [_i64, _i64, _i64, _f32p, _u8p, ctypes.c_float, _f32p, ctypes.c_int]),
         "orc_max_threads": (ctypes.c_int, []),
         "orc_erf_as": (ctypes.c_float, [ctypes.c_float]),
+        "orc_to_f16": (None, [_i64, _f32p, _u16p]),
+        "orc_from_f16": (None, [_i64, _u16p, _f32p]),
+        "orc_matmul_f16": (None, [_i64, _i64, _i64, _f32p, _u16p, _f32p]),
         "orc_gelu_exact": (None, [_i64, _f32p]),
         "orc_gelu_tanh": (None, [_i64, _f32p]),
     }
@@ -262,6 +266,33 @@ def matmul_q4_mt(a, packed, k: int, n: int, scale: float, nthreads: int) -> np.n
 
 def max_threads() -> int:
     return int(lib().orc_max_threads())
+
+
+# ---------------------------------------------------------------- F16 weights
+def to_f16(w) -> np.ndarray:
+    """toF16 (src/core/quantization.zig:1907-1917): binary16 bit patterns."""
+    w = _f32(w)
+    h = np.empty(w.shape, dtype=np.uint16)
+    lib().orc_to_f16(w.size, w.reshape(-1), h.reshape(-1))
+    return h
+
+
+def from_f16(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    v = np.empty(h.shape, dtype=np.float32)
+    lib().orc_from_f16(h.size, h.reshape(-1), v.reshape(-1))
+    return v
+
+
+def matmul_f16(a, h) -> np.ndarray:
+    """matmulF32F16 fallback (src/core/quantization.zig:1949-1958)."""
+    a, h = _f32(a), np.ascontiguousarray(h, dtype=np.uint16)
+    m, k = a.shape
+    k2, n = h.shape
+    assert k == k2
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul_f16(m, n, k, a, h, c)
+    return c
 
 
 # ---------------------------------------------------------------- activations

@@ -380,3 +380,42 @@ def test_gelu_tanh_vector_form_properties(orc):
     # by more than the KAT tolerance: the split is observable.
     g8 = orc.gelu_tanh(np.array([2.0] * 8 + [2.0], np.float32))
     assert abs(g8[0] - 1.9545) > 0.01 and abs(g8[8] - 1.9545) <= 0.01
+
+
+# ---------------------------------------------------------------- F16 weights
+def test_f16_widening_exhaustive(orc):
+    # Every binary16 pattern widens exactly as numpy's IEEE conversion.
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = orc.from_f16(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f16_narrowing_round_to_nearest_even(orc):
+    # numpy's f32 -> f16 cast is IEEE round to nearest even: ties, subnormal
+    # ties, the 65504 / 65520 overflow edge, signed zeros, infinities.
+    edge = np.array([0.0, -0.0, 1.0, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 65504.0, 65519.0, 65520.0, 1e6,
+                     -65520.0, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -26, 2.0 ** -14, 2.0 ** -14 - 2.0 ** -25,
+                     np.inf, -np.inf, 5.96e-8, 6.1e-5], dtype=np.float32)
+    rng = np.random.default_rng(11)
+    bits = rng.integers(0, 2 ** 32, size=400000, dtype=np.uint64).astype(np.uint32)
+    rand = bits.view(np.float32)
+    rand = rand[~np.isnan(rand)]
+    scaled = (rng.standard_normal(200000) * np.exp2(rng.integers(-30, 18, size=200000))).astype(np.float32)
+    for v in (edge, rand, scaled):
+        got = orc.to_f16(v)
+        with np.errstate(over="ignore"):
+            ref = v.astype(np.float16).view(np.uint16)
+        assert np.array_equal(got, ref)
+    nan = orc.to_f16(np.array([np.nan], np.float32))
+    assert np.isnan(nan.view(np.float16)[0])
+
+
+def test_matmul_f16_equals_widened_f32(orc):
+    rng = np.random.default_rng(12)
+    for (m, n, k) in [(1, 7, 5), (5, 33, 17), (9, 64, 40)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        h = orc.to_f16(rng.standard_normal((k, n)).astype(np.float32) * 0.1)
+        np.testing.assert_array_equal(orc.matmul_f16(a, h), orc.matmul_naive(a, orc.from_f16(h)))

@@ -24,7 +24,7 @@ TML_ERR_INVALID_ARG = -5
 TML_ERR_NO_DEVICE = -6
 TML_ERR_HIP = -7
 
-FMT_F32, FMT_Q8_0, FMT_Q4_0, FMT_Q8_K = 0, 1, 2, 3
+FMT_F32, FMT_Q8_0, FMT_Q4_0, FMT_Q8_K, FMT_F16 = 0, 1, 2, 3, 4
 ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2
 
 # Every symbol the header declares, with its ctypes signature.
@@ -56,6 +56,7 @@ SIGNATURES = {
                                         _vp]),
     "tml_hip_prepare_rows_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _i64, _f, _vp,
                                                 ctypes.POINTER(ctypes.c_void_p)]),
+    "tml_hip_sgemm_f16": (ctypes.c_int, [_i64, _i64, _i64, _vp, _vp, _vp]),
     "tml_hip_gemm_residual": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp,
                                              _vp]),
     "tml_hip_gemm_ex_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp,
@@ -151,6 +152,10 @@ def sgemm_q4(m: int, n: int, k: int, a: np.ndarray, packed: np.ndarray, scale: f
     check(lib().tml_hip_sgemm_q4(m, n, k, _ptr(a), _ptr(packed), scale, _ptr(c)))
 
 
+def sgemm_f16(m: int, n: int, k: int, a: np.ndarray, h: np.ndarray, c: np.ndarray) -> None:
+    check(lib().tml_hip_sgemm_f16(m, n, k, _ptr(a), _ptr(h), _ptr(c)))
+
+
 def gemm(fmt: int, m: int, n: int, k: int, a: np.ndarray, b: np.ndarray, c: np.ndarray, *, scale: float = 1.0,
          scales: np.ndarray | None = None, block: int = 32, bias: np.ndarray | None = None) -> None:
     check(lib().tml_hip_gemm(fmt, m, n, k, _ptr(a), _ptr(b), scale, _ptr(scales), block, _ptr(bias), _ptr(c)))
@@ -170,7 +175,7 @@ def gemm_residual(fmt: int, m: int, n: int, k: int, a: np.ndarray, b: np.ndarray
                                       _ptr(residual), _ptr(c)))
 
 
-def quantize(fmt: int, w: np.ndarray, q: np.ndarray, scales: np.ndarray) -> None:
+def quantize(fmt: int, w: np.ndarray, q: np.ndarray, scales: np.ndarray | None) -> None:
     check(lib().tml_hip_quantize(fmt, w.size, _ptr(w), _ptr(q), _ptr(scales)))
 
 

@@ -62,6 +62,7 @@ template <> struct BFmt<TML_FMT_F32> { static constexpr int EPC = 4; };
 template <> struct BFmt<TML_FMT_Q8_0> { static constexpr int EPC = 8; };
 template <> struct BFmt<TML_FMT_Q8_K> { static constexpr int EPC = 8; };
 template <> struct BFmt<TML_FMT_Q4_0> { static constexpr int EPC = 8; };
+template <> struct BFmt<TML_FMT_F16> { static constexpr int EPC = 8; };
 
 // Raw registers of one B chunk.
 struct BRaw {
@@ -84,8 +85,10 @@ template <int FMT>
 __device__ __forceinline__ void load_b_vec(const GemmKArgs &a, int k, int n, BRaw &r) {
     const bool in = (k < a.K) && (n < a.N);
     const size_t e = (size_t)(in ? k : 0) * a.N + (in ? n : 0);
-    if constexpr (FMT == TML_FMT_F32) {
-        const uintx4 v = *(const uintx4 *)(in ? (const void *)((const float *)a.B + e) : a.zero);
+    if constexpr (FMT == TML_FMT_F32 || FMT == TML_FMT_F16) {
+        const void *p = FMT == TML_FMT_F32 ? (const void *)((const float *)a.B + e)
+                                           : (const void *)((const uint16_t *)a.B + e);
+        const uintx4 v = *(const uintx4 *)(in ? p : a.zero);
         r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3];
     } else if constexpr (FMT == TML_FMT_Q8_0 || FMT == TML_FMT_Q8_K) {
         const uintx2 v = *(const uintx2 *)(in ? (const void *)((const int8_t *)a.B + e) : a.zero);
@@ -103,6 +106,8 @@ __device__ __forceinline__ float load_b_elem(const GemmKArgs &a, int k, int n) {
     const size_t e = (size_t)k * a.N + n;
     if constexpr (FMT == TML_FMT_F32) {
         return ((const float *)a.B)[e];
+    } else if constexpr (FMT == TML_FMT_F16) {
+        return tml_half_bits(((const uint16_t *)a.B)[e]);
     } else if constexpr (FMT == TML_FMT_Q8_0) {
         return (float)((const int8_t *)a.B)[e];
     } else if constexpr (FMT == TML_FMT_Q8_K) {
@@ -119,6 +124,9 @@ __device__ __forceinline__ void decode_b(const BRaw &r, float *out) {
     if constexpr (FMT == TML_FMT_F32) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(r.w[i]);
+    } else if constexpr (FMT == TML_FMT_F16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = tml_half_bits(r.w[i / 2] >> (16 * (i % 2)));
     } else if constexpr (FMT == TML_FMT_Q8_0) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) out[i] = sext8(r.w[i / 4], i % 4);
@@ -497,7 +505,7 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
     int cfg = env_int("TML_GEMM_TILE", 0) - 1;
     if (cfg < 0 || cfg >= kNumCfgs) cfg = pick_cfg(m.M, m.N, cus);
     constexpr int EPC = BFmt<FMT>::EPC;
-    const size_t bbytes = FMT == TML_FMT_F32 ? 16 : (FMT == TML_FMT_Q4_0 ? 4 : 8);
+    const size_t bbytes = (FMT == TML_FMT_F32 || FMT == TML_FMT_F16) ? 16 : (FMT == TML_FMT_Q4_0 ? 4 : 8);
     bool vec = (m.K % 4 == 0) && aligned(m.A, 16) && (m.N % EPC == 0) && aligned(m.B, bbytes);
     if (FMT == TML_FMT_Q8_K) vec = vec && (m.block % 8 == 0);
     if (!vec) cfg = 3;  // the generic path is instantiated for one tile shape
@@ -542,6 +550,7 @@ Status launch_gemm_mfma(const MatmulArgs &m, const Workspace &ws, hipStream_t s)
         case TML_FMT_Q8_0: return launch_fmt<TML_FMT_Q8_0>(m, s, cus);
         case TML_FMT_Q8_K: return launch_fmt<TML_FMT_Q8_K>(m, s, cus);
         case TML_FMT_Q4_0: return launch_fmt<TML_FMT_Q4_0>(m, s, cus);
+        case TML_FMT_F16: return launch_fmt<TML_FMT_F16>(m, s, cus);
         default: return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
     }
 }

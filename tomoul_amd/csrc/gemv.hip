@@ -64,6 +64,7 @@ template <int LW> struct Elems<TML_FMT_F32, LW> { static constexpr int value = L
 template <int LW> struct Elems<TML_FMT_Q8_0, LW> { static constexpr int value = LW; };
 template <int LW> struct Elems<TML_FMT_Q8_K, LW> { static constexpr int value = LW; };
 template <int LW> struct Elems<TML_FMT_Q4_0, LW> { static constexpr int value = 2 * LW; };
+template <int LW> struct Elems<TML_FMT_F16, LW> { static constexpr int value = LW / 2; };
 
 template <int LW> struct Raw { uint32_t w[LW / 4]; float s; };
 
@@ -95,6 +96,7 @@ __device__ __forceinline__ void load_chunk(const GemvKArgs &a, bool in, int k, i
     const size_t e = (size_t)k * a.N + n;
     const void *p = !in ? a.zero
                   : FMT == TML_FMT_F32 ? (const void *)((const float *)a.B + e)
+                  : FMT == TML_FMT_F16 ? (const void *)((const uint16_t *)a.B + e)
                   : FMT == TML_FMT_Q4_0 ? (const void *)((const uint8_t *)a.B + e / 2)
                                         : (const void *)((const int8_t *)a.B + e);
     if constexpr (LW == 16) {
@@ -115,6 +117,9 @@ __device__ __forceinline__ void decode_chunk(const Raw<LW> &r, float *w) {
     if constexpr (FMT == TML_FMT_F32) {
 #pragma unroll
         for (int i = 0; i < E; ++i) w[i] = __uint_as_float(r.w[i]);
+    } else if constexpr (FMT == TML_FMT_F16) {
+#pragma unroll
+        for (int i = 0; i < E; ++i) w[i] = tml_half_bits(r.w[i / 2] >> (16 * (i % 2)));
     } else if constexpr (FMT == TML_FMT_Q8_0) {
 #pragma unroll
         for (int i = 0; i < E; ++i) w[i] = sext8(r.w[i / 4], i % 4);
@@ -141,6 +146,7 @@ __device__ __forceinline__ void load_elems(const GemvKArgs &a, bool row_ok, int 
         if (row_ok && n + i < a.N) {
             const size_t ei = e + i;
             if constexpr (FMT == TML_FMT_F32) v = ((const float *)a.B)[ei];
+            else if constexpr (FMT == TML_FMT_F16) v = tml_half_bits(((const uint16_t *)a.B)[ei]);
             else if constexpr (FMT == TML_FMT_Q8_0) v = (float)((const int8_t *)a.B)[ei];
             else if constexpr (FMT == TML_FMT_Q8_K) v = (float)((const int8_t *)a.B)[ei] * a.scales[ei / a.block];
             else v = sext4(((const uint8_t *)a.B)[ei / 2], (int)(ei & 1));
@@ -355,7 +361,8 @@ constexpr int kMaxSplit = 8;  // default cap on K splits per segment
 
 int pick_lw(int fmt, int mr) {
     switch (fmt) {
-        case TML_FMT_F32: return 16;
+        case TML_FMT_F32:
+        case TML_FMT_F16: return 16;
         case TML_FMT_Q8_0:
         case TML_FMT_Q8_K: return mr <= 4 ? 16 : 8;
         default: return mr <= 2 ? 16 : (mr == 4 ? 8 : 4);  // Q4_0
@@ -363,7 +370,7 @@ int pick_lw(int fmt, int mr) {
 }
 
 int elems_per_lane(int fmt, int lw) {
-    return fmt == TML_FMT_F32 ? lw / 4 : (fmt == TML_FMT_Q4_0 ? 2 * lw : lw);
+    return fmt == TML_FMT_F32 ? lw / 4 : fmt == TML_FMT_F16 ? lw / 2 : (fmt == TML_FMT_Q4_0 ? 2 * lw : lw);
 }
 
 bool is_aligned(const void *p, size_t n) { return ((uintptr_t)p % n) == 0; }
@@ -394,7 +401,8 @@ GemvPlan make_plan(const MatmulArgs &m) {
     p.u = kU;
     p.vec = (m.N % p.e == 0) && is_aligned(m.B, (size_t)p.lw);
     if (m.fmt == TML_FMT_Q8_K) p.vec = p.vec && (m.block % p.e == 0) && (m.N % m.block == 0);
-    const int64_t bpe_num = m.fmt == TML_FMT_F32 ? 4 : 1, bpe_den = m.fmt == TML_FMT_Q4_0 ? 2 : 1;
+    const int64_t bpe_num = m.fmt == TML_FMT_F32 ? 4 : (m.fmt == TML_FMT_F16 ? 2 : 1),
+                  bpe_den = m.fmt == TML_FMT_Q4_0 ? 2 : 1;
     const int64_t rowbytes = (m.N * bpe_num + bpe_den - 1) / bpe_den;
     // Segment width per row: 128 bytes (one line) for f32, 64 bytes for
     // quantized B at M <= 2 and 32 bytes at M > 2 -- measured best on MI355X
@@ -402,7 +410,7 @@ GemvPlan make_plan(const MatmulArgs &m) {
     // lines, wider ones need more K splits and, with many partial sums per
     // lane, fewer but costlier reduction steps); rows narrower than that get
     // the narrowest segment that covers them.
-    const int seg_bytes = m.fmt == TML_FMT_F32 ? 128 : (p.mr <= 2 ? 64 : 32);
+    const int seg_bytes = (m.fmt == TML_FMT_F32 || m.fmt == TML_FMT_F16) ? 128 : (p.mr <= 2 ? 64 : 32);
     int lpr = seg_bytes / p.lw;
     if (lpr < 4) lpr = 4;
     if (rowbytes < seg_bytes) {
@@ -462,7 +470,7 @@ void launch_lpr(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
 
 template <int FMT, int MR>
 Status launch_mr(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
-    constexpr int LW = FMT == TML_FMT_F32 ? 16
+    constexpr int LW = (FMT == TML_FMT_F32 || FMT == TML_FMT_F16) ? 16
                      : (FMT == TML_FMT_Q4_0 ? (MR <= 2 ? 16 : (MR == 4 ? 8 : 4)) : (MR <= 4 ? 16 : 8));
     if (p.lw != LW) return Status::Err(TML_ERR_INVALID_ARG, "gemv plan/instantiation mismatch");
     launch_lpr<FMT, MR, LW>(ka, p, s);
@@ -515,6 +523,7 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
         case TML_FMT_Q8_0: return launch_fmt<TML_FMT_Q8_0>(ka, p, s);
         case TML_FMT_Q8_K: return launch_fmt<TML_FMT_Q8_K>(ka, p, s);
         case TML_FMT_Q4_0: return launch_fmt<TML_FMT_Q4_0>(ka, p, s);
+        case TML_FMT_F16: return launch_fmt<TML_FMT_F16>(ka, p, s);
         default: return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
     }
 }

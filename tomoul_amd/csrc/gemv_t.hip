@@ -56,6 +56,7 @@ template <int FMT> struct TElems;
 template <> struct TElems<TML_FMT_F32> { static constexpr int value = 4; };
 template <> struct TElems<TML_FMT_Q8_0> { static constexpr int value = 16; };
 template <> struct TElems<TML_FMT_Q4_0> { static constexpr int value = 32; };
+template <> struct TElems<TML_FMT_F16> { static constexpr int value = 8; };
 
 __device__ __forceinline__ float tsext8(uint32_t word, int byte) {
     return (float)((int32_t)(word << (24 - 8 * byte)) >> 24);
@@ -67,6 +68,7 @@ __device__ __forceinline__ float tsext4(uint32_t word, int nib) {
 template <int FMT>
 __device__ __forceinline__ float telem(const uintx4 &w, int i) {
     if constexpr (FMT == TML_FMT_F32) return __uint_as_float(w[i]);
+    else if constexpr (FMT == TML_FMT_F16) return tml_half_bits(w[i / 2] >> (16 * (i % 2)));
     else if constexpr (FMT == TML_FMT_Q8_0) return tsext8(w[i / 4], i % 4);
     else return tsext4(w[i / 8], i % 8);
 }
@@ -240,6 +242,12 @@ __global__ __launch_bounds__(256) void prepare_t_kernel(const void *B, int K, in
         if constexpr (FMT == TML_FMT_F32) {
             const long long k = wj;
             if (k < K) word = ((const uint32_t *)B)[k * N + n];
+        } else if constexpr (FMT == TML_FMT_F16) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const long long k = wj * 2 + h;
+                if (k < K) word |= (uint32_t)((const uint16_t *)B)[k * N + n] << (16 * h);
+            }
         } else if constexpr (FMT == TML_FMT_Q8_0) {
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
@@ -349,22 +357,22 @@ void launch_t0(const GemvTArgs &ka, const TPlan &p, unsigned grid, bool xvec, hi
     }
 }
 
-int t_elems(int fmt) { return fmt == TML_FMT_F32 ? 4 : (fmt == TML_FMT_Q8_0 ? 16 : 32); }
+int t_elems(int fmt) { return fmt == TML_FMT_F32 ? 4 : fmt == TML_FMT_F16 ? 8 : (fmt == TML_FMT_Q8_0 ? 16 : 32); }
 
 }  // namespace
 
 int64_t prepared_row_bytes(int fmt, int64_t K) {
-    const int64_t bytes = fmt == TML_FMT_F32 ? 4 * K : (fmt == TML_FMT_Q4_0 ? (K + 1) / 2 : K);
+    const int64_t bytes = packed_row_bytes(fmt, K);
     const int64_t r = (bytes + 15) / 16 * 16;
     return r > 0 ? r : 16;
 }
 
 int64_t prepared_gemv_max_m(int fmt) {
-    return fmt == TML_FMT_F32 ? 8 : fmt == TML_FMT_Q8_0 ? 4 : fmt == TML_FMT_Q4_0 ? 2 : 0;
+    return (fmt == TML_FMT_F32 || fmt == TML_FMT_F16) ? 8 : fmt == TML_FMT_Q8_0 ? 4 : fmt == TML_FMT_Q4_0 ? 2 : 0;
 }
 
 bool prepared_gemv_supported(int fmt, int64_t M, int64_t K) {
-    if (fmt != TML_FMT_F32 && fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0) return false;
+    if (fmt != TML_FMT_F32 && fmt != TML_FMT_F16 && fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0) return false;
     if (M < 1 || M > kPreparedGemvMaxM || K >= ((int64_t)1 << 30)) return false;
     // rows are padded to a power of two; their activations for one chunk
     // must fit the register budget: MR * E <= 64 (f32 any M <= 8, Q8_0
@@ -383,7 +391,8 @@ Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, 
         case TML_FMT_F32: prepare_t_kernel<TML_FMT_F32><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
         case TML_FMT_Q8_0: prepare_t_kernel<TML_FMT_Q8_0><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
         case TML_FMT_Q4_0: prepare_t_kernel<TML_FMT_Q4_0><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
-        default: return Status::Err(TML_ERR_INVALID_FORMAT, "prepared layout: format must be F32, Q8_0 or Q4_0");
+        case TML_FMT_F16: prepare_t_kernel<TML_FMT_F16><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
+        default: return Status::Err(TML_ERR_INVALID_FORMAT, "prepared layout: format must be F32, F16, Q8_0 or Q4_0");
     }
     TML_HIP_TRY(hipGetLastError());
     return Status::Ok();
@@ -420,6 +429,7 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     switch (fmt) {
         case TML_FMT_F32: launch_t0<TML_FMT_F32>(ka, p, (unsigned)grid, xvec, s); break;
         case TML_FMT_Q8_0: launch_t0<TML_FMT_Q8_0>(ka, p, (unsigned)grid, xvec, s); break;
+        case TML_FMT_F16: launch_t0<TML_FMT_F16>(ka, p, (unsigned)grid, xvec, s); break;
         default: launch_t0<TML_FMT_Q4_0>(ka, p, (unsigned)grid, xvec, s); break;
     }
     TML_HIP_TRY(hipGetLastError());

@@ -120,6 +120,14 @@ int grid_for(long long items) {
 
 }  // namespace
 
+// toF16 (quantization.zig:1907-1917): @floatCast, i.e. IEEE round to
+// nearest even, overflow to infinity, NaN kept NaN.
+__global__ __launch_bounds__(kThreads) void to_f16_kernel(const float *__restrict__ w, long long n,
+                                                          uint16_t *__restrict__ h) {
+    for (long long i = (long long)blockIdx.x * kThreads + threadIdx.x; i < n; i += (long long)gridDim.x * kThreads)
+        h[i] = __builtin_bit_cast(unsigned short, (_Float16)w[i]);
+}
+
 size_t quantize_tmp_floats(int fmt, int64_t n) {
     return fmt == TML_FMT_Q8_K ? 0 : (size_t)partial_blocks(n);
 }
@@ -143,8 +151,12 @@ Status launch_quantize(int fmt, int64_t n, const float *w, void *q, float *scale
             quantize_q8k_kernel<<<grid_for(((n + 31) / 32) * 32), kThreads, 0, s>>>(w, n, (int8_t *)q, scales);
             TML_HIP_TRY(hipGetLastError());
             return Status::Ok();
+        case TML_FMT_F16:
+            to_f16_kernel<<<grid_for(n), kThreads, 0, s>>>(w, n, (uint16_t *)q);
+            TML_HIP_TRY(hipGetLastError());
+            return Status::Ok();
         default:
-            return Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0 or Q8_K");
+            return Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0, Q8_K or F16");
     }
 }
 

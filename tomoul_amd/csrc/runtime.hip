@@ -150,7 +150,8 @@ Status ensure_workspace(DeviceCtx *c, const MatmulArgs &m, hipStream_t s, Worksp
 }
 
 bool valid_fmt(int fmt) {
-    return fmt == TML_FMT_F32 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0 || fmt == TML_FMT_Q8_K;
+    return fmt == TML_FMT_F32 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0 || fmt == TML_FMT_Q8_K ||
+           fmt == TML_FMT_F16;
 }
 
 // Bytes of a K x N weight in format fmt.
@@ -158,6 +159,7 @@ size_t weight_bytes(int fmt, int64_t K, int64_t N) {
     const size_t e = (size_t)K * (size_t)N;
     switch (fmt) {
         case TML_FMT_F32: return e * 4;
+        case TML_FMT_F16: return e * 2;
         case TML_FMT_Q4_0: return (e + 1) / 2;
         default: return e;
     }
@@ -190,12 +192,14 @@ Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const fl
     return launch_gemm_mfma(m, ws, s);
 }
 
-bool preparable_fmt(int fmt) { return fmt == TML_FMT_F32 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0; }
+bool preparable_fmt(int fmt) {
+    return fmt == TML_FMT_F32 || fmt == TML_FMT_F16 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0;
+}
 
 // Builds the prepared copy of the [K,N] device weight B (asynchronous on s).
 Status make_prepared(DeviceCtx *c, int fmt, int64_t K, int64_t N, const void *B, float scale, hipStream_t s,
                      Prepared **out) {
-    if (!preparable_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, Q8_0 or Q4_0");
+    if (!preparable_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, F16, Q8_0 or Q4_0");
     if (K < 0 || N < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
     if (K >= ((int64_t)1 << 30) || N >= ((int64_t)1 << 30))
         return Status::Err(TML_ERR_INVALID_SHAPE, "prepare: dimension exceeds 2^30");
@@ -336,11 +340,12 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
 }
 
 Status quantize_dev(DeviceCtx *c, int fmt, int64_t n, const float *w, void *q, float *scales, hipStream_t s) {
-    if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K)
-        return Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0 or Q8_K");
+    if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K && fmt != TML_FMT_F16)
+        return Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0, Q8_K or F16");
     if (n < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative element count");
-    if (scales == nullptr || (n > 0 && (w == nullptr || q == nullptr)))
+    if ((scales == nullptr && fmt != TML_FMT_F16) || (n > 0 && (w == nullptr || q == nullptr)))
         return Status::Err(TML_ERR_INVALID_ARG, "null pointer");
+    if (fmt == TML_FMT_F16) return launch_quantize(fmt, n, w, q, scales, nullptr, s);
     if (n == 0) {
         // The reference's all-zero rule: an empty Q8_0 / Q4_0 tensor gets
         // scale 1 (max|v| == 0); Q8_K has no blocks.
@@ -434,6 +439,10 @@ int tml_hip_sgemm_q4(int64_t M, int64_t N, int64_t K, const float *A, const uint
     return report(host_gemm(TML_FMT_Q4_0, M, N, K, A, Bp, scale, nullptr, 0, nullptr, C, 1.0f, 0.0f));
 }
 
+int tml_hip_sgemm_f16(int64_t M, int64_t N, int64_t K, const float *A, const uint16_t *Bh, float *C) {
+    return report(host_gemm(TML_FMT_F16, M, N, K, A, Bh, 1.0f, nullptr, 0, nullptr, C, 1.0f, 0.0f));
+}
+
 int tml_hip_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
                  const float *scales, int64_t block, const float *bias, float *C) {
     return report(host_gemm(fmt, M, N, K, A, B, scale, scales, block, bias, C, 1.0f, 0.0f));
@@ -451,16 +460,16 @@ int tml_hip_gemm_residual(int fmt, int64_t M, int64_t N, int64_t K, const float 
 }
 
 int tml_hip_quantize(int fmt, int64_t n, const float *w, void *q, float *scales) {
-    if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K)
-        return report(Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0 or Q8_K"));
+    if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K && fmt != TML_FMT_F16)
+        return report(Status::Err(TML_ERR_INVALID_FORMAT, "quantize: format must be Q8_0, Q4_0, Q8_K or F16"));
     if (n < 0) return report(Status::Err(TML_ERR_INVALID_SHAPE, "negative element count"));
-    if (scales == nullptr || (n > 0 && (w == nullptr || q == nullptr)))
+    if ((scales == nullptr && fmt != TML_FMT_F16) || (n > 0 && (w == nullptr || q == nullptr)))
         return report(Status::Err(TML_ERR_INVALID_ARG, "null pointer"));
     DeviceCtx *c = nullptr;
     Status s = current_ctx(&c);
     if (!s.ok()) return report(s);
-    const size_t qbytes = fmt == TML_FMT_Q4_0 ? (size_t)(n + 1) / 2 : (size_t)n;
-    const size_t nscales = fmt == TML_FMT_Q8_K ? (size_t)(n + 31) / 32 : 1;
+    const size_t qbytes = weight_bytes(fmt, 1, n);
+    const size_t nscales = fmt == TML_FMT_F16 ? 0 : fmt == TML_FMT_Q8_K ? (size_t)(n + 31) / 32 : 1;
     auto run = [&]() -> Status {
         TML_TRY(c->a.ensure((size_t)n * sizeof(float) + 16));
         TML_TRY(c->b.ensure(qbytes + 16));
@@ -468,7 +477,7 @@ int tml_hip_quantize(int fmt, int64_t n, const float *w, void *q, float *scales)
         if (n > 0) TML_HIP_TRY(hipMemcpyAsync(c->a.p, w, (size_t)n * sizeof(float), hipMemcpyHostToDevice, c->stream));
         TML_TRY(quantize_dev(c, fmt, n, (const float *)c->a.p, c->b.p, (float *)c->scales.p, c->stream));
         if (qbytes > 0) TML_HIP_TRY(hipMemcpyAsync(q, c->b.p, qbytes, hipMemcpyDeviceToHost, c->stream));
-        if (fmt != TML_FMT_Q8_K || n > 0)
+        if (nscales > 0 && (fmt != TML_FMT_Q8_K || n > 0))
             TML_HIP_TRY(hipMemcpyAsync(scales, c->scales.p, nscales * sizeof(float), hipMemcpyDeviceToHost,
                                        c->stream));
         TML_HIP_TRY(hipStreamSynchronize(c->stream));
@@ -567,7 +576,7 @@ int tml_hip_prepare_rows_dev(int fmt, int64_t K, int64_t N, const void *W, int64
     if (out == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null handle pointer"));
     *out = nullptr;
     if (!preparable_fmt(fmt))
-        return report(Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, Q8_0 or Q4_0"));
+        return report(Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, F16, Q8_0 or Q4_0"));
     if (K < 0 || N < 0) return report(Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension"));
     if (K >= ((int64_t)1 << 30) || N >= ((int64_t)1 << 30))
         return report(Status::Err(TML_ERR_INVALID_SHAPE, "prepare: dimension exceeds 2^30"));

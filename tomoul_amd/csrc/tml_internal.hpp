@@ -177,7 +177,12 @@ bool prepared_gemv_supported(int fmt, int64_t M, int64_t K);
 // Bytes of one row of K elements of fmt in the reference's packing (Q4_0:
 // two per byte), before the 16-byte padding of a prepared row.
 inline int64_t packed_row_bytes(int fmt, int64_t K) {
-    return fmt == TML_FMT_F32 ? 4 * K : (fmt == TML_FMT_Q4_0 ? (K + 1) / 2 : K);
+    return fmt == TML_FMT_F32 ? 4 * K : fmt == TML_FMT_F16 ? 2 * K : (fmt == TML_FMT_Q4_0 ? (K + 1) / 2 : K);
+}
+
+// binary16 bits -> f32 (exact, as the reference's @floatCast(f16)).
+__device__ __forceinline__ float tml_half_bits(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
 }
 Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, int64_t ldt, hipStream_t s);
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,

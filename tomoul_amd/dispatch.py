@@ -1,6 +1,7 @@
 """Weight-type dispatch of the reference's attention/transformer layers.
 
 matmulWithWeight(input, weight)         src/core/attention.zig:114-130
+                                        (f32, Q8_0, Q4_0, Q8_K and F16 weights)
 matmulWithWeightBias(input, weight, b)  src/core/attention.zig:132-149
 (duplicated at src/core/transformer.zig:129-166).  The weight's type selects
 the kernel family; every branch runs on the GPU.  For quantized weights the
@@ -50,6 +51,8 @@ def matmulWithWeight(a: Tensor, weight) -> Tensor:  # noqa: N802 (reference name
         return qz.matmulF32Q4Simd(a, weight)
     if isinstance(weight, qz.QuantizedTensorQ8K):
         return qz.matmulF32Q8KSimd(a, weight)
+    if isinstance(weight, qz.F16Tensor):
+        return qz.matmulF32F16(a, weight)
     raise TypeError(f"unsupported weight type {type(weight).__name__}")
 
 
@@ -65,6 +68,8 @@ def matmulWithWeightBias(a: Tensor, weight, bias: Tensor) -> Tensor:  # noqa: N8
     elif isinstance(weight, qz.QuantizedTensorQ8K):
         _abi.gemm(_abi.FMT_Q8_K, m, n, k, a.data, weight.data, out.data, scales=weight.scales,
                   block=weight.block_size, bias=bias.data)
+    elif isinstance(weight, qz.F16Tensor):
+        _abi.gemm(_abi.FMT_F16, m, n, k, a.data, weight.data, out.data, bias=bias.data)
     else:
         raise TypeError(f"unsupported weight type {type(weight).__name__}")
     return out
@@ -80,6 +85,8 @@ def _weight_args(weight) -> tuple[int, dict]:
         return _abi.FMT_Q4_0, {"scale": weight.scale}
     if isinstance(weight, qz.QuantizedTensorQ8K):
         return _abi.FMT_Q8_K, {"scales": weight.scales, "block": weight.block_size}
+    if isinstance(weight, qz.F16Tensor):
+        return _abi.FMT_F16, {}
     raise TypeError(f"unsupported weight type {type(weight).__name__}")
 
 

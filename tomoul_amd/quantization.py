@@ -113,7 +113,36 @@ class QuantizedTensorQ4:
         self.data[i] = (b & 0xF0) | v if idx % 2 == 0 else (b & 0x0F) | (v << 4)
 
 
+class F16Tensor:
+    """F16Tensor (quantization.zig:1859-1905): binary16 weights, held as
+    their uint16 bit patterns."""
+
+    def __init__(self, data: np.ndarray, shape):
+        self.data = np.ascontiguousarray(data, dtype=np.uint16).reshape(-1)
+        self.shape = tuple(int(s) for s in shape)
+
+    @classmethod
+    def init(cls, shape) -> "F16Tensor":
+        return cls(np.zeros(_numel(shape), dtype=np.uint16), shape)
+
+    def numel(self) -> int:
+        return _numel(self.shape)
+
+    def sizeBytes(self) -> int:  # noqa: N802
+        return self.numel() * 2
+
+    def compressionRatio(self) -> float:  # noqa: N802
+        return self.numel() * 4 / self.sizeBytes()
+
+
 # ---------------------------------------------------------------- quantizers
+def toF16(t: Tensor) -> F16Tensor:  # noqa: N802
+    """toF16 (quantization.zig:1907-1917), on the GPU: round to nearest even."""
+    h = np.empty(t.numel(), dtype=np.uint16)
+    _abi.quantize(_abi.FMT_F16, t.data, h, None)
+    return F16Tensor(h, t.shape)
+
+
 def quantizeQ8(t: Tensor) -> QuantizedTensorQ8:  # noqa: N802
     q = np.empty(t.numel(), dtype=np.int8)
     s = np.empty(1, dtype=np.float32)
@@ -159,6 +188,15 @@ def matmulF32Q8KSimd(a: Tensor, b: QuantizedTensorQ8K) -> Tensor:  # noqa: N802
     m, n, k = _shape(a, b)
     out = Tensor.init((m, n))
     _abi.sgemm_q8k(m, n, k, a.data, b.data, b.scales, b.block_size, out.data)
+    return out
+
+
+def matmulF32F16(a: Tensor, b: F16Tensor) -> Tensor:  # noqa: N802
+    """matmulF32F16 (quantization.zig:1921-1962): f32 activations x f16
+    weights, f32 accumulation."""
+    m, n, k = _shape(a, b)
+    out = Tensor.init((m, n))
+    _abi.sgemm_f16(m, n, k, a.data, b.data, out.data)
     return out
 
 
