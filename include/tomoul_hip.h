@@ -52,6 +52,13 @@ extern "C" {
 #define TML_ERR_INVALID_ARG (-5)    /* null pointer, bad block size, ...      */
 #define TML_ERR_NO_DEVICE (-6)      /* no usable HIP device                   */
 #define TML_ERR_HIP (-7)            /* a HIP runtime call failed              */
+/* .tl files: the reference's LoadError members (src/core/loader.zig:11-20). */
+#define TML_ERR_INVALID_MAGIC (-8)            /* LoadError.InvalidMagic           */
+#define TML_ERR_UNSUPPORTED_VERSION (-9)      /* LoadError.UnsupportedVersion     */
+#define TML_ERR_CORRUPTED_FILE (-10)          /* LoadError.CorruptedFile          */
+#define TML_ERR_TENSOR_NOT_FOUND (-11)        /* LoadError.TensorNotFound         */
+#define TML_ERR_FILE_NOT_FOUND (-12)          /* LoadError.FileNotFound           */
+#define TML_ERR_UNSUPPORTED_QUANT_FORMAT (-13) /* LoadError.UnsupportedQuantFormat */
 
 /* Weight formats (= .tl quant-format byte, src/core/loader.zig:23-29). */
 #define TML_FMT_F32 0
@@ -259,6 +266,68 @@ int tml_hip_prepared_free(tml_prepared_t w);
  * (residual and activation after the bias). */
 int tml_hip_gemm_prepared_ex(tml_prepared_t w, int64_t M, const float *A, const float *bias, const float *residual,
                              int act, float *C, float alpha, float beta, void *stream);
+
+/* ----------------------------------------------------------- .tl files */
+
+/* A parsed .tl file: ModelLoader (src/core/loader.zig:41-622).  Parsing and
+ * validation run on the host with the reference's checks and error codes;
+ * payloads go to HBM byte for byte, so a resident tensor equals the one the
+ * reference builds in host memory.
+ *
+ * tml_tl_open        ModelLoader.init (:55-91): reads the whole file.
+ * tml_tl_open_bytes  ModelLoader.initFromBytes (:94-111): borrows `data`,
+ *                    which must outlive the handle.
+ * tml_tl_close       deinit (:114-131).
+ * tml_tl_format      getQuantFormat (:582-585): TML_FMT_* (= the header's
+ *                    quant-format byte), or a negative error.
+ * tml_tl_count       tensorCount (:587-590): distinct names.
+ * tml_tl_name        listTensors()[i] (:592-595), file order; NULL past the
+ *                    end.  The string lives as long as the handle.
+ * tml_tl_info        getTensorInfo (:597-600): rank (ndim), up to `cap`
+ *                    dims, payload offset and size in bytes. */
+typedef struct tml_tl_file *tml_tl_t;
+int tml_tl_open(const char *path, tml_tl_t *out);
+int tml_tl_open_bytes(const void *data, uint64_t size, tml_tl_t *out);
+int tml_tl_close(tml_tl_t f);
+int tml_tl_format(tml_tl_t f);
+int64_t tml_tl_count(tml_tl_t f);
+const char *tml_tl_name(tml_tl_t f, int64_t i);
+int tml_tl_info(tml_tl_t f, const char *name, int64_t *dims, int cap, int *ndim, uint64_t *offset,
+                uint64_t *size);
+
+/* The typed getters, with the reference's checks in its order:
+ *   getter TML_FMT_F32   getTensor (:225-264)            data: n f32
+ *          TML_FMT_Q8_0  getQuantizedTensorQ8 (:267-307)  data: n int8,   *scale
+ *          TML_FMT_Q4_0  getQuantizedTensorQ4 (:310-350)  data: ceil(n/2) packed bytes, *scale
+ *          TML_FMT_Q8_K  getQuantizedTensorQ8K (:354-403) data: n int8,   scales: ceil(n/32) f32
+ *          TML_FMT_F16   getF16Tensor (:406-437)          data: n binary16
+ * n = product of the tensor's dims.  The quantized getters and getF16Tensor
+ * fail with TML_ERR_UNSUPPORTED_QUANT_FORMAT on a file of another format;
+ * an unknown name is TML_ERR_TENSOR_NOT_FOUND; a payload outside the file
+ * or of the wrong size (or a Q8_K block count that does not match) is
+ * TML_ERR_CORRUPTED_FILE.  Unused outputs may be NULL.
+ * tml_tl_read       host destinations (no GPU needed).
+ * tml_tl_read_dev   device destinations, asynchronous on `stream`; the
+ *                   handle must stay open until the stream has run them. */
+int tml_tl_read(tml_tl_t f, const char *name, int getter, void *data, float *scales, float *scale);
+int tml_tl_read_dev(tml_tl_t f, const char *name, int getter, void *data, float *scales, float *scale,
+                    void *stream);
+
+/* getTensorDequantized (:442-569) on the device: out receives n f32 values,
+ * f32(q) * scale per element (Q8_0 / Q4_0 / Q8_K with its per-32 scales),
+ * the exact widening for F16, the values themselves for F32.  Asynchronous;
+ * the handle must stay open until the stream has run it. */
+int tml_tl_read_dequantized_dev(tml_tl_t f, const char *name, float *out, void *stream);
+
+/* The XLM-R loaders loadQuantizedTransposedQ8 / Q4 / Q8K
+ * (src/models/xlm_roberta_punctuation/model.zig:1272-1362) on the device:
+ * dequantize q [rows, cols] (the PyTorch [out, in] layout), transpose to
+ * [cols, rows] (= [in, out], the matmul's [K, N]) and quantize again with
+ * the reference quantizer of the same format, bit for bit.  fmt Q8_0 / Q4_0
+ * (per-tensor `scale` in, scales_out[0] out) or Q8_K (`scales` in,
+ * ceil(rows*cols/32) scales out).  Device pointers, asynchronous. */
+int tml_hip_transpose_requant_dev(int fmt, int64_t rows, int64_t cols, const void *q, const float *scales,
+                                  float scale, void *q_out, float *scales_out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -325,3 +325,127 @@ def apply_act(v, act: int) -> np.ndarray:
     if act == ACT_GELU_TANH:
         return gelu_tanh(v)
     return _f32(v).copy()
+
+
+# --------------------------------------------------------------- .tl files
+# Pure-Python restatement of the file layout: the reader of
+# src/core/loader.zig:133-222 (header, tensor table) and :225-569 (payloads),
+# and the writer of tools/tl_format.py:250-360 (header, table with offsets
+# patched after the data, payload per format).  Small files only.
+TL_F32, TL_Q8_0, TL_Q4_0, TL_Q8_K, TL_F16 = 0, 1, 2, 3, 4
+
+
+class TlParseError(Exception):
+    def __init__(self, kind: str):
+        super().__init__(kind)
+        self.kind = kind  # the LoadError member's name
+
+
+def tl_parse(data: bytes) -> dict:
+    import struct
+    if len(data) < 16:
+        raise TlParseError("CorruptedFile")
+    if data[:4] != b"TOUL":
+        raise TlParseError("InvalidMagic")
+    version, count = struct.unpack_from("<II", data, 4)
+    if version != 1:
+        raise TlParseError("UnsupportedVersion")
+    fmt = data[12]
+    if fmt > 4:
+        raise TlParseError("UnsupportedQuantFormat")
+    pos, entries = 16, []
+    for _ in range(count):
+        if pos + 4 > len(data):
+            raise TlParseError("CorruptedFile")
+        (nlen,) = struct.unpack_from("<I", data, pos)
+        pos += 4
+        if pos + nlen > len(data):
+            raise TlParseError("CorruptedFile")
+        name = data[pos:pos + nlen].decode()
+        pos += nlen
+        if pos + 4 > len(data):
+            raise TlParseError("CorruptedFile")
+        (nd,) = struct.unpack_from("<I", data, pos)
+        pos += 4
+        if pos + 4 * nd > len(data):
+            raise TlParseError("CorruptedFile")
+        shape = struct.unpack_from(f"<{nd}I", data, pos)
+        pos += 4 * nd
+        if pos + 16 > len(data):
+            raise TlParseError("CorruptedFile")
+        off, size = struct.unpack_from("<QQ", data, pos)
+        pos += 16
+        entries.append((name, tuple(shape), off, size))
+    return {"version": version, "format": fmt, "tensors": entries}
+
+
+def tl_payload(data: bytes, entry, fmt: int) -> dict:
+    """The parts of one payload in format fmt, with the getters' size checks."""
+    import struct
+    name, shape, off, size = entry
+    n = int(np.prod(shape, dtype=np.int64)) if shape else 1
+    if off + size > len(data):
+        raise TlParseError("CorruptedFile")
+    raw = data[off:off + size]
+    want = {TL_F32: 4 * n, TL_F16: 2 * n, TL_Q8_0: 4 + n, TL_Q4_0: 4 + (n + 1) // 2,
+            TL_Q8_K: 4 + 4 * ((n + 31) // 32) + n}[fmt]
+    if size != want:
+        raise TlParseError("CorruptedFile")
+    if fmt == TL_F32:
+        return {"data": np.frombuffer(raw, dtype="<f4").copy()}
+    if fmt == TL_F16:
+        return {"data": np.frombuffer(raw, dtype="<u2").copy()}
+    if fmt in (TL_Q8_0, TL_Q4_0):
+        (scale,) = struct.unpack_from("<f", raw, 0)
+        dt = np.int8 if fmt == TL_Q8_0 else np.uint8
+        return {"scale": scale, "data": np.frombuffer(raw[4:], dtype=dt).copy()}
+    nb = (n + 31) // 32
+    (stored,) = struct.unpack_from("<I", raw, 0)
+    return {"num_blocks": stored, "scales": np.frombuffer(raw[4:4 + 4 * nb], dtype="<f4").copy(),
+            "data": np.frombuffer(raw[4 + 4 * nb:], dtype=np.int8).copy()}
+
+
+def tl_dequantize(fmt: int, parts: dict, n: int) -> np.ndarray:
+    """getTensorDequantized's per-format arithmetic (loader.zig:467-565):
+    one f32 multiply f32(q) * scale per element, exact widening of f16."""
+    if fmt == TL_F32:
+        return parts["data"].astype(np.float32)
+    if fmt == TL_F16:
+        return from_f16(parts["data"])
+    if fmt == TL_Q8_0:
+        return parts["data"].astype(np.float32) * np.float32(parts["scale"])
+    if fmt == TL_Q4_0:
+        b = parts["data"]
+        nib = np.empty(2 * b.size, dtype=np.int32)
+        nib[0::2], nib[1::2] = b & 0x0F, b >> 4
+        nib = np.where(nib & 8, nib - 16, nib)[:n]
+        return nib.astype(np.float32) * np.float32(parts["scale"])
+    idx = np.arange(n) // 32
+    return parts["data"].astype(np.float32) * parts["scales"][idx]
+
+
+def tl_write(tensors, fmt: int) -> bytes:
+    """A .tl file from (name, shape, parts) triples, parts already encoded
+    for fmt as tl_payload returns them (tools/tl_format.py:277-360)."""
+    import struct
+    head = bytearray(b"TOUL" + struct.pack("<II", 1, len(tensors)) + bytes([fmt, 0, 0, 0]))
+    patch = []
+    for name, shape, _ in tensors:
+        nb = name.encode()
+        head += struct.pack("<I", len(nb)) + nb + struct.pack("<I", len(shape))
+        head += b"".join(struct.pack("<I", d) for d in shape)
+        patch.append(len(head))
+        head += b"\0" * 16
+    body = bytearray()
+    for (name, shape, parts), at in zip(tensors, patch):
+        start = len(head) + len(body)
+        if fmt in (TL_F32, TL_F16):
+            blob = parts["data"].astype("<f4" if fmt == TL_F32 else "<u2").tobytes()
+        elif fmt in (TL_Q8_0, TL_Q4_0):
+            blob = struct.pack("<f", parts["scale"]) + parts["data"].tobytes()
+        else:
+            sc = parts["scales"].astype("<f4")
+            blob = struct.pack("<I", parts.get("num_blocks", sc.size)) + sc.tobytes() + parts["data"].tobytes()
+        body += blob
+        head[at:at + 16] = struct.pack("<QQ", start, len(blob))
+    return bytes(head + body)

@@ -20,7 +20,7 @@ HEADER = os.path.join(ROOT, "include", "tomoul_hip.h")
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(tml_hip_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(tml_(?:hip|tl)_\w+)\s*\(", text)))
 
 
 def test_header_declares_expected_entry_points():
@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_exported_symbols_have_c_linkage():
     out = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True, text=True).stdout
-    exported = set(re.findall(r"\bT (tml_hip_\w+)$", out, flags=re.M))
+    exported = set(re.findall(r"\bT (tml_(?:hip|tl)_\w+)$", out, flags=re.M))
     assert set(declared_functions()) <= exported
 
 

@@ -23,6 +23,12 @@ TML_ERR_INVALID_FORMAT = -4
 TML_ERR_INVALID_ARG = -5
 TML_ERR_NO_DEVICE = -6
 TML_ERR_HIP = -7
+TML_ERR_INVALID_MAGIC = -8
+TML_ERR_UNSUPPORTED_VERSION = -9
+TML_ERR_CORRUPTED_FILE = -10
+TML_ERR_TENSOR_NOT_FOUND = -11
+TML_ERR_FILE_NOT_FOUND = -12
+TML_ERR_UNSUPPORTED_QUANT_FORMAT = -13
 
 FMT_F32, FMT_Q8_0, FMT_Q4_0, FMT_Q8_K, FMT_F16 = 0, 1, 2, 3, 4
 ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2
@@ -62,6 +68,19 @@ SIGNATURES = {
     "tml_hip_gemm_ex_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp,
                                            ctypes.c_int, _vp, _f, _f, _vp]),
     "tml_hip_gemm_prepared_ex": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, ctypes.c_int, _vp, _f, _f, _vp]),
+    "tml_hip_transpose_requant_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _vp, _f, _vp, _vp, _vp]),
+    "tml_tl_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "tml_tl_open_bytes": (ctypes.c_int, [_vp, ctypes.c_uint64, ctypes.POINTER(_vp)]),
+    "tml_tl_close": (ctypes.c_int, [_vp]),
+    "tml_tl_format": (ctypes.c_int, [_vp]),
+    "tml_tl_count": (_i64, [_vp]),
+    "tml_tl_name": (ctypes.c_char_p, [_vp, _i64]),
+    "tml_tl_info": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int,
+                                   ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_uint64),
+                                   ctypes.POINTER(ctypes.c_uint64)]),
+    "tml_tl_read": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, _vp, _vp, ctypes.POINTER(_f)]),
+    "tml_tl_read_dev": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, _vp, _vp, ctypes.POINTER(_f), _vp]),
+    "tml_tl_read_dequantized_dev": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _vp]),
 }
 
 
@@ -237,3 +256,10 @@ def gemm_prepared_ex(handle: int, m: int, a_ptr: int, c_ptr: int, *, act: int = 
 
 def prepared_free(handle: int) -> None:
     check(lib().tml_hip_prepared_free(handle))
+
+
+def transpose_requant_dev(fmt: int, rows: int, cols: int, q_ptr: int, q_out_ptr: int, scales_out_ptr: int, *,
+                          scale: float = 1.0, scales_ptr: int | None = None, stream: int | None = None) -> None:
+    """loadQuantizedTransposed{Q8,Q4,Q8K} on device pointers: [rows, cols] -> [cols, rows]."""
+    check(lib().tml_hip_transpose_requant_dev(fmt, rows, cols, q_ptr, scales_ptr, scale, q_out_ptr, scales_out_ptr,
+                                              stream))

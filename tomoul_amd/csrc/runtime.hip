@@ -83,6 +83,7 @@ struct DeviceCtx {
     int device = -1;
     hipStream_t stream = nullptr;
     DevBuf a, b, c, bias, res, scales, qtmp;  // staging of the host-pointer API
+    DevBuf tl_raw, tl_scales, tr;            // .tl payload staging, transpose temporary
     DevBuf ws, counters;                 // split-K workspace (gemv, gemm)
     DevBuf zero;                         // kZeroBlockBytes of zeros
     std::unordered_map<const void *, Registered> weights;
@@ -385,8 +386,9 @@ void tml_hip_shutdown(void) {
             delete w.second.prep;
             (void)hipFree(w.second.dev);
         }
-        c->a.release(); c->b.release(); c->c.release(); c->bias.release();
+        c->a.release(); c->b.release(); c->c.release(); c->bias.release(); c->res.release();
         c->scales.release(); c->qtmp.release(); c->ws.release(); c->counters.release();
+        c->tl_raw.release(); c->tl_scales.release(); c->tr.release();
         c->zero.release();
         if (c->stream) (void)hipStreamDestroy(c->stream);
         (void)hipSetDevice(prev);
@@ -662,6 +664,154 @@ int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *sca
     Status s = current_ctx(&c);
     if (!s.ok()) return report(s);
     return report(quantize_dev(c, fmt, n, w, q, scales, (hipStream_t)stream));
+}
+
+int tml_hip_transpose_requant_dev(int fmt, int64_t rows, int64_t cols, const void *q, const float *scales,
+                                  float scale, void *q_out, float *scales_out, void *stream) {
+    if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0 && fmt != TML_FMT_Q8_K)
+        return report(Status::Err(TML_ERR_INVALID_FORMAT, "transpose-requantize: format must be Q8_0, Q4_0 or Q8_K"));
+    if (rows < 0 || cols < 0) return report(Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension"));
+    const int64_t n = rows * cols;
+    if (scales_out == nullptr || (n > 0 && (q == nullptr || q_out == nullptr)) ||
+        (fmt == TML_FMT_Q8_K && n > 0 && scales == nullptr))
+        return report(Status::Err(TML_ERR_INVALID_ARG, "null pointer"));
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    auto run = [&]() -> Status {
+        const hipStream_t st = (hipStream_t)stream;
+        if (n > 0) {
+            TML_TRY(c->tr.ensure((size_t)n * sizeof(float)));
+            TML_TRY(launch_dequant_transpose(fmt, rows, cols, q, scales, scale, (float *)c->tr.p, st));
+        }
+        return quantize_dev(c, fmt, n, (const float *)c->tr.p, q_out, scales_out, st);
+    };
+    return report(run());
+}
+
+// ------------------------------------------------------------ .tl files
+int tml_tl_open(const char *path, tml_tl_t *out) {
+    if (out == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null handle pointer"));
+    TlFile *f = nullptr;
+    Status s = tl_open_file(path, &f);
+    *out = (tml_tl_t)f;
+    return report(s);
+}
+
+int tml_tl_open_bytes(const void *data, uint64_t size, tml_tl_t *out) {
+    if (out == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null handle pointer"));
+    TlFile *f = nullptr;
+    Status s = tl_open_bytes(data, size, &f);
+    *out = (tml_tl_t)f;
+    return report(s);
+}
+
+int tml_tl_close(tml_tl_t f) {
+    delete (TlFile *)f;
+    return report(Status::Ok());
+}
+
+int tml_tl_format(tml_tl_t f) {
+    if (f == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null file"));
+    return ((const TlFile *)f)->format;
+}
+
+int64_t tml_tl_count(tml_tl_t f) {
+    if (f == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null file"));
+    return (int64_t)((const TlFile *)f)->index.size();
+}
+
+const char *tml_tl_name(tml_tl_t f, int64_t i) {
+    if (f == nullptr) return nullptr;
+    const TlFile *t = (const TlFile *)f;
+    if (i < 0 || (size_t)i >= t->tensors.size()) return nullptr;
+    return t->tensors[(size_t)i].name.c_str();
+}
+
+int tml_tl_info(tml_tl_t f, const char *name, int64_t *dims, int cap, int *ndim, uint64_t *offset,
+                uint64_t *size) {
+    if (f == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null file"));
+    const TlTensor *t = tl_find((const TlFile *)f, name);
+    if (t == nullptr)
+        return report(Status::Err(TML_ERR_TENSOR_NOT_FOUND, std::string("no tensor named ") + (name ? name : "")));
+    if (ndim) *ndim = (int)t->shape.size();
+    for (int i = 0; dims && i < cap && i < (int)t->shape.size(); ++i) dims[i] = t->shape[(size_t)i];
+    if (offset) *offset = t->offset;
+    if (size) *size = t->size;
+    return report(Status::Ok());
+}
+
+namespace {
+Status tl_check_getter(int getter) {
+    if (getter < TML_FMT_F32 || getter > TML_FMT_F16) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown getter format");
+    return Status::Ok();
+}
+Status tl_need(const TlParts &p, const void *data, const float *scales, const float *scale) {
+    if ((p.data_bytes > 0 && data == nullptr) || (p.nscales > 0 && scales == nullptr) ||
+        ((p.fmt == TML_FMT_Q8_0 || p.fmt == TML_FMT_Q4_0) && scale == nullptr))
+        return Status::Err(TML_ERR_INVALID_ARG, "null destination");
+    return Status::Ok();
+}
+}  // namespace
+
+int tml_tl_read(tml_tl_t f, const char *name, int getter, void *data, float *scales, float *scale) {
+    if (f == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null file"));
+    auto run = [&]() -> Status {
+        TML_TRY(tl_check_getter(getter));
+        TlParts p;
+        TML_TRY(tl_parts((const TlFile *)f, name, getter, false, &p));
+        TML_TRY(tl_need(p, data, scales, scale));
+        if (p.data_bytes) std::memcpy(data, p.data, p.data_bytes);
+        if (p.nscales) std::memcpy(scales, p.scales, p.nscales * 4);
+        if (p.fmt == TML_FMT_Q8_0 || p.fmt == TML_FMT_Q4_0) *scale = p.scale;
+        return Status::Ok();
+    };
+    return report(run());
+}
+
+int tml_tl_read_dev(tml_tl_t f, const char *name, int getter, void *data, float *scales, float *scale,
+                    void *stream) {
+    if (f == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null file"));
+    auto run = [&]() -> Status {
+        TML_TRY(tl_check_getter(getter));
+        TlParts p;
+        TML_TRY(tl_parts((const TlFile *)f, name, getter, false, &p));
+        TML_TRY(tl_need(p, data, scales, scale));
+        DeviceCtx *c = nullptr;
+        TML_TRY(current_ctx(&c));
+        const hipStream_t st = (hipStream_t)stream;
+        if (p.data_bytes)
+            TML_HIP_TRY(hipMemcpyAsync(data, p.data, p.data_bytes, hipMemcpyHostToDevice, st));
+        if (p.nscales) TML_HIP_TRY(hipMemcpyAsync(scales, p.scales, p.nscales * 4, hipMemcpyHostToDevice, st));
+        if (p.fmt == TML_FMT_Q8_0 || p.fmt == TML_FMT_Q4_0) *scale = p.scale;
+        return Status::Ok();
+    };
+    return report(run());
+}
+
+int tml_tl_read_dequantized_dev(tml_tl_t f, const char *name, float *out, void *stream) {
+    if (f == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null file"));
+    auto run = [&]() -> Status {
+        TlParts p;
+        TML_TRY(tl_parts((const TlFile *)f, name, 0, true, &p));
+        if (p.numel > 0 && out == nullptr) return Status::Err(TML_ERR_INVALID_ARG, "null destination");
+        if (p.numel == 0) return Status::Ok();
+        DeviceCtx *c = nullptr;
+        TML_TRY(current_ctx(&c));
+        const hipStream_t st = (hipStream_t)stream;
+        if (p.fmt == TML_FMT_F32) {
+            TML_HIP_TRY(hipMemcpyAsync(out, p.data, p.data_bytes, hipMemcpyHostToDevice, st));
+            return Status::Ok();
+        }
+        TML_TRY(c->tl_raw.ensure(p.data_bytes + 16));
+        TML_HIP_TRY(hipMemcpyAsync(c->tl_raw.p, p.data, p.data_bytes, hipMemcpyHostToDevice, st));
+        if (p.nscales) {
+            TML_TRY(c->tl_scales.ensure(p.nscales * 4));
+            TML_HIP_TRY(hipMemcpyAsync(c->tl_scales.p, p.scales, p.nscales * 4, hipMemcpyHostToDevice, st));
+        }
+        return launch_dequant(p.fmt, p.numel, c->tl_raw.p, (const float *)c->tl_scales.p, p.scale, out, st);
+    };
+    return report(run());
 }
 
 }  // extern "C"

@@ -5,6 +5,8 @@
 
 #include <cstdint>
 #include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "../../include/tomoul_hip.h"
 
@@ -190,6 +192,43 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
                      const void *zero, int act, long long tail0, hipStream_t s);
 // Largest M the prepared kernel covers for fmt (8 f32, 4 Q8_0, 2 Q4_0).
 int64_t prepared_gemv_max_m(int fmt);
+
+// .tl files (tl.hip).
+struct TlTensor {
+    std::string name;
+    std::vector<int64_t> shape;
+    uint64_t offset = 0, size = 0;
+};
+struct TlFile {
+    std::vector<uint8_t> owned;  // the file's bytes (tml_tl_open) ...
+    const uint8_t *data = nullptr;  // ... or the caller's (tml_tl_open_bytes)
+    uint64_t size = 0;
+    uint32_t version = 0;
+    int format = 0;                  // TML_FMT_*
+    std::vector<TlTensor> tensors;   // file order
+    std::unordered_map<std::string, size_t> index;  // name -> last entry of that name
+};
+// A validated payload: `data` (data_bytes), Q8_K `scales` (nscales floats,
+// unaligned in the file), Q8_0 / Q4_0 `scale`.
+struct TlParts {
+    int fmt = 0;
+    int64_t numel = 0;
+    const uint8_t *data = nullptr;
+    uint64_t data_bytes = 0;
+    const uint8_t *scales = nullptr;
+    uint64_t nscales = 0;
+    float scale = 1.0f;
+};
+Status tl_open_file(const char *path, TlFile **out);
+Status tl_open_bytes(const void *data, uint64_t size, TlFile **out);
+const TlTensor *tl_find(const TlFile *f, const char *name);
+// getter's checks (by_file_format = false) or getTensorDequantized's
+// (by_file_format = true: the file's format decides, getter is ignored).
+Status tl_parts(const TlFile *f, const char *name, int getter, bool by_file_format, TlParts *p);
+Status launch_dequant(int fmt, int64_t n, const void *raw, const float *scales, float scale, float *out,
+                      hipStream_t s);
+Status launch_dequant_transpose(int fmt, int64_t rows, int64_t cols, const void *raw, const float *scales,
+                                float scale, float *out, hipStream_t s);
 
 // Tuning overrides for experiments (0 = heuristic).  Read from the
 // TML_GEMM_TILE / TML_GEMV_SPLIT environment variables once.
