@@ -83,7 +83,7 @@ def test_tanh_split_follows_flat_index(orc):
 
 @pytest.fixture
 def forced_env():
-    keys = ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE")
+    keys = ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE", "TML_GEMM_FUSED")
     saved = {key: os.environ.get(key) for key in keys}
     yield os.environ
     for key, v in saved.items():

@@ -305,7 +305,7 @@ def test_registered_weight_path(orc):
 # ------------------------------------------------------- forced kernel plans
 @pytest.fixture
 def forced_env():
-    saved = {k: os.environ.get(k) for k in ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE")}
+    saved = {k: os.environ.get(k) for k in ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE", "TML_GEMM_FUSED")}
     yield os.environ
     for k, v in saved.items():
         if v is None:
@@ -327,6 +327,30 @@ def test_sgemm_dma_tiles_and_splits(orc, forced_env, tile, split):
         got = ops.matmulBias(T(a), T(b), Tensor.from_numpy(bias)).numpy()
         err = rel_err(got, orc.matmul_bias(a, b, bias))
         assert err <= FP32_TOL, (m, n, k, err)
+
+
+@pytest.mark.parametrize("tile", [1, 2, 4, 5, 7, 8])
+@pytest.mark.parametrize("split", [2, 3, 8])
+def test_sgemm_fused_split_equals_two_launch(forced_env, tile, split):
+    # Split-K partials combined inside the GEMM (last split to arrive sums
+    # them in split order) give the two-launch reduce's result bit for bit,
+    # with the fused epilogue (bias, residual, activation) on top.
+    forced_env["TML_GEMM_DMA_TILE"] = str(tile)
+    forced_env["TML_GEMM_SPLIT"] = str(split)
+    m, n, k = 300, 260, 1028
+    a, b = rnd(97, m, k), rnd(98, k, n, 0.02)
+    bias = synth.normal(99, n, 0.0, 0.02)
+    res = rnd(100, m, n)
+    out = {}
+    for fused in ("1", "0"):
+        forced_env["TML_GEMM_FUSED"] = fused
+        c = np.zeros((m, n), np.float32)
+        _abi.gemm_residual(_abi.FMT_F32, m, n, k, a, b, res, c, bias=bias)
+        g = np.zeros((m, n), np.float32)
+        _abi.gemm_act(_abi.FMT_F32, m, n, k, a, b, g, act=_abi.ACT_GELU_TANH, bias=bias)
+        out[fused] = (c, g)
+    np.testing.assert_array_equal(out["1"][0], out["0"][0])
+    np.testing.assert_array_equal(out["1"][1], out["0"][1])
 
 
 def test_sgemm_split_deterministic(forced_env):

@@ -47,7 +47,8 @@ struct DmaArgs {
     float alpha, beta;
     int tiles_m, tiles_n, group_m;
     int nsplit, spl;      // K splits and BK-slices per split
-    float *ws;            // split partials: [split][M][N]
+    float *ws;            // split partials: [split][M][N], or per tile in lane order when fused
+    unsigned *counters;   // per-tile arrival counters (fused split-K), or nullptr
     const float *zero;
     int act;              // TML_ACT_* after the bias
     const float *res;     // [M,N] residual added after the bias, or nullptr
@@ -281,7 +282,60 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
     }
 
     const int rq = g * 4;
-    if (a.nsplit > 1) {
+    if (a.nsplit > 1 && a.counters != nullptr) {
+        // Fused split-K: each split stores its raw partial in lane order
+        // (store i of every thread is one contiguous NT-float run), the last
+        // split to arrive at the tile's counter sums all splits in split
+        // order -- the order splitk_reduce_kernel uses, so the result is the
+        // same bit for bit -- and runs the epilogue.  The exchange uses
+        // agent-scope stores / loads, no device-wide fence.
+        constexpr int NT = NW * 64;
+        constexpr int TF = TM * TN * 4;
+        constexpr int XB = 4;  // splits whose partials are loaded at once
+        __shared__ unsigned xslot;
+        const int tile = tile_m * a.tiles_n + tile_n;
+        float *base = a.ws + (size_t)tile * a.nsplit * (NT * TF);
+        float *mine = base + (size_t)split * (NT * TF);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) xchg_store(mine + ((i * TN + j) * 4 + r) * NT + tid, acc[i][j][r]);
+        const unsigned arrived = xchg_arrive(a.counters + tile, &xslot);
+        if (arrived != (unsigned)(a.nsplit - 1)) return;
+        floatx4 sum[TM][TN];
+        for (int s0 = 0; s0 < a.nsplit; s0 += XB) {
+            float t[XB][TF];
+#pragma unroll
+            for (int x = 0; x < XB; ++x) {
+                const int sp = min(s0 + x, a.nsplit - 1);
+                const float *src = base + (size_t)sp * (NT * TF) + tid;
+#pragma unroll
+                for (int e = 0; e < TF; ++e) t[x][e] = (sp == split) ? 0.0f : xchg_load(src + e * NT);
+            }
+#pragma unroll
+            for (int x = 0; x < XB; ++x) {
+                const int sp = s0 + x;
+                if (sp >= a.nsplit) break;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        floatx4 v;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) v[r] = (sp == split) ? acc[i][j][r] : t[x][(i * TN + j) * 4 + r];
+                        if (sp == 0) sum[i][j] = v;
+                        else sum[i][j] += v;
+                    }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = sum[i][j];
+        xchg_reset(a.counters + tile);
+    } else if (a.nsplit > 1) {
         // Split-K: store the raw partial of this split into ws[split][M][N];
         // splitk_reduce_kernel (launched next on the same stream) sums the
         // splits in order and applies the epilogue.
@@ -378,6 +432,20 @@ void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk) {
     *bk = kDmaCfgs[cfg].bk;
 }
 
+void gemm_dma_workspace_need(const MatmulArgs &m, const GemmPlan &p, size_t *partial_floats, size_t *counters) {
+    *partial_floats = 0;
+    *counters = 0;
+    if (p.nsplit <= 1) return;
+    const int bm = kDmaCfgs[p.cfg].bm, bn = kDmaCfgs[p.cfg].bn;
+    const size_t tiles = (size_t)((m.M + bm - 1) / bm) * (size_t)((m.N + bn - 1) / bn);
+    if (p.fused) {
+        *partial_floats = tiles * (size_t)p.nsplit * (size_t)bm * bn;
+        *counters = tiles;
+    } else {
+        *partial_floats = (size_t)p.nsplit * m.M * m.N;
+    }
+}
+
 bool gemm_dma_supported(const MatmulArgs &m) {
     return m.fmt == TML_FMT_F32 && m.K % 4 == 0 && m.N % 4 == 0 && ((uintptr_t)m.A % 16) == 0 &&
            ((uintptr_t)m.B % 16) == 0;
@@ -399,12 +467,18 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
     a.nsplit = p.nsplit;
     a.spl = p.spl;
     a.ws = ws.partials;
+    a.counters = p.fused ? ws.counters : nullptr;
     a.act = m.act;
     a.res = m.res;
     a.tail0 = tml_act_tail0((long long)m.M * m.N);
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
-    if (p.nsplit > 1 && (ws.partials == nullptr || ws.partial_floats < (size_t)p.nsplit * m.M * m.N))
-        return Status::Err(TML_ERR_INVALID_ARG, "GEMM split-K workspace too small");
+    if (p.nsplit > 1) {
+        size_t need_floats = 0, need_counters = 0;
+        gemm_dma_workspace_need(m, p, &need_floats, &need_counters);
+        if (ws.partials == nullptr || ws.partial_floats < need_floats ||
+            (p.fused && (ws.counters == nullptr || ws.counter_count < need_counters)))
+            return Status::Err(TML_ERR_INVALID_ARG, "GEMM split-K workspace too small");
+    }
     const int bk = kDmaCfgs[cfg].bk;
     if (p.spl < 1 || (int64_t)p.spl * p.nsplit < (m.K + bk - 1) / bk)
         return Status::Err(TML_ERR_INVALID_ARG, "GEMM split plan does not cover K");
@@ -423,7 +497,7 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
         default: return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
     }
     TML_HIP_TRY(hipGetLastError());
-    if (p.nsplit > 1) {
+    if (p.nsplit > 1 && !p.fused) {
         const int64_t n4 = (m.M * m.N + 3) / 4;
         const int64_t blocks = (n4 + 255) / 256;
         splitk_reduce_kernel<<<dim3((unsigned)(blocks < 65535 ? blocks : 65535)), 256, 0, s>>>(

@@ -490,6 +490,12 @@ void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
         p->spl = (int)(nk > 0 ? nk : 1);
         p->tiles = (int)(((M + bm - 1) / bm) * ((N + bn - 1) / bn));
     }
+    // Split partials are combined by splitk_reduce_kernel, launched after the
+    // GEMM.  TML_GEMM_FUSED=1 combines them inside the GEMM instead (the last
+    // split of a tile sums them); on MI355X that measured ~2 us slower per
+    // headline step than the extra launch (the agent-scope round trip of the
+    // last split costs more than a reduce kernel in a graph), so it is off.
+    p->fused = p->nsplit > 1 && env_int("TML_GEMM_FUSED", 0) != 0;
 }
 
 bool aligned(const void *p, size_t n) { return ((uintptr_t)p % n) == 0; }
@@ -533,7 +539,7 @@ void gemm_workspace_need(const MatmulArgs &m, size_t *partial_floats, size_t *co
     const GemmPlan p = plan_gemm(m);
     *partial_floats = 0;
     *counters = 0;
-    if (p.dma && p.nsplit > 1) *partial_floats = (size_t)p.nsplit * m.M * m.N;
+    if (p.dma && p.nsplit > 1) gemm_dma_workspace_need(m, p, partial_floats, counters);
 }
 
 Status launch_gemm_mfma(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {

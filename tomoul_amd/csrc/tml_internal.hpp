@@ -150,6 +150,7 @@ struct GemmPlan {
     int nsplit = 1;    // K splits (dma kernel only)
     int spl = 0;       // BK-slices per split
     int tiles = 0;
+    bool fused = false;  // split-K partials combined in the GEMM kernel (no reduce launch)
 };
 GemmPlan plan_gemm(const MatmulArgs &a);
 void gemm_workspace_need(const MatmulArgs &a, size_t *partial_floats, size_t *counters);
@@ -160,6 +161,7 @@ bool gemm_dma_supported(const MatmulArgs &a);
 int gemm_dma_num_cfgs();
 void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk);
 Status launch_gemm_f32_dma(const MatmulArgs &a, const GemmPlan &p, const Workspace &ws, hipStream_t s);
+void gemm_dma_workspace_need(const MatmulArgs &a, const GemmPlan &p, size_t *partial_floats, size_t *counters);
 Status launch_gemv(const MatmulArgs &a, const Workspace &ws, hipStream_t s);
 // Workspace needed by launch_gemv for this problem.
 void gemv_workspace_need(const MatmulArgs &a, size_t *partial_floats, size_t *counters);
