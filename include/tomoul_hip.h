@@ -220,14 +220,16 @@ int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *sca
  * AttentionWeights / TransformerBlockWeights until deinit
  * (src/core/attention.zig:54-86, src/core/transformer.zig:31-68), so a
  * backend may keep them in whatever layout its kernels read best.  The
- * prepared copy stores B K-contiguous (row n = column n of B, zero padded
- * to a multiple of 16 bytes; Q4_0 keeps two k per byte, even k in the low
- * nibble), so a GEMV with M <= 2 reads each output's weights as one
- * contiguous run and needs no cross-workgroup reduction (M <= 8 for f32,
- * M <= 4 for Q8_0, M <= 2 for Q4_0).  No counterpart in
- * the reference (its CPU loops read B in place).
+ * prepared copy stores column n of B as row n, zero padded to a multiple of
+ * 16 bytes, its k in an order interleaved across 16-byte chunks so that
+ * the lanes reading consecutive chunks read contiguous activations (plain K
+ * order for f32); a GEMV then reads each output's weights as one contiguous
+ * run and needs no cross-workgroup reduction (M <= 8 for f32 / F16, M <= 4
+ * for Q8_0, M <= 2 for Q4_0).  No counterpart in the reference (its CPU
+ * loops read B in place).
  *
- * tml_hip_prepare_dev: fmt is TML_FMT_F32, TML_FMT_Q8_0 or TML_FMT_Q4_0;
+ * tml_hip_prepare_dev: fmt is TML_FMT_F32, TML_FMT_F16, TML_FMT_Q8_0 or
+ *   TML_FMT_Q4_0;
  *   B is the device [K,N] weight in the layouts above, scale the Q8_0 /
  *   Q4_0 per-tensor scale.  The copy is built asynchronously on `stream`.
  *   B must stay valid and unchanged while the handle is used: calls with
@@ -251,11 +253,11 @@ int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const flo
  * 936-940, :377-383, :619-622), which the reference transposes on every
  * decode step; here the embedding is used as it is stored.  It is also the
  * PyTorch [out,in] layout of weights exported untransposed.
- * fmt F32, Q8_0 (one int8 per element) or Q4_0 (two per byte, even k low;
- * K must be even so each row starts a byte).  When a row is a multiple of
- * 16 bytes and W and ldw are 16-byte aligned, W is used in place (no copy;
- * it must stay valid and unchanged while the handle lives); otherwise a
- * padded device copy is made on `stream`.  Products with more rows than the
+ * fmt F32, F16, Q8_0 (one int8 per element) or Q4_0 (two per byte, even k
+ * low; K must be even so each row starts a byte).  F32 rows that are a
+ * multiple of 16 bytes, with W and ldw 16-byte aligned, are used in place
+ * (no copy; W must stay valid and unchanged while the handle lives);
+ * otherwise the prepared layout is built on `stream` in a new buffer.  Products with more rows than the
  * prepared kernel covers (8 f32, 4 Q8_0, 2 Q4_0) run it over consecutive
  * row blocks.  Free with tml_hip_prepared_free.  No counterpart in the
  * reference. */

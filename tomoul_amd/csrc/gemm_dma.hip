@@ -46,6 +46,7 @@ struct DmaArgs {
     float *C;
     float alpha, beta;
     int tiles_m, tiles_n, group_m;
+    int pm, pn, ps;       // XCD partition of (m-tiles, n-tiles, splits), pm*pn*ps = 8; pm = 0: none
     int nsplit, spl;      // K splits and BK-slices per split
     float *ws;            // split partials: [split][M][N], or per tile in lane order when fused
     unsigned *counters;   // per-tile arrival counters (fused split-K), or nullptr
@@ -107,20 +108,36 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
     const int wm0 = (wave / WAVES_N) * WM;
     const int wn0 = (wave % WAVES_N) * WN;
 
-    // XCD-aware remap of the workgroup id, then GROUP_M swizzle.
+    // Workgroup -> (tile, split).  Workgroups are dispatched to the 8 XCDs
+    // round robin (id % 8), each XCD with its own L2.
     const int nblk = gridDim.x;
     const int b = blockIdx.x;
-    const int per = nblk / kNumXcd, rem = nblk % kNumXcd;
     const int xcd = b % kNumXcd, idx = b / kNumXcd;
-    const int lin = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
-    // The K splits of one tile are adjacent ids, so they run on one XCD.
-    const int split = lin % a.nsplit;
-    const int tlin = lin / a.nsplit;
-    const int group = a.group_m * a.tiles_n;
-    const int first_m = (tlin / group) * a.group_m;
-    const int gsize = min(a.tiles_m - first_m, a.group_m);
-    const int tile_m = first_m + (tlin % group) % gsize;
-    const int tile_n = (tlin % group) / gsize;
+    int tile_m, tile_n, split;
+    if (a.pm > 0) {
+        // XCD partition: XCD x owns one block of (m-tiles x n-tiles x
+        // splits), chosen by the host so that the A rows and B columns one
+        // XCD reads are as few bytes as possible; every operand byte then
+        // crosses into at most the XCDs that need it.
+        const int lm = a.tiles_m / a.pm, ln = a.tiles_n / a.pn, ls = a.nsplit / a.ps;
+        const int pz = xcd % a.ps, py = (xcd / a.ps) % a.pn, px = xcd / (a.ps * a.pn);
+        const int sp = idx / (lm * ln), r = idx % (lm * ln);
+        tile_m = px * lm + r % lm;
+        tile_n = py * ln + r / lm;
+        split = pz * ls + sp;
+    } else {
+        // Consecutive ids per XCD, then GROUP_M swizzle; the K splits of one
+        // tile are adjacent ids, so they run on one XCD.
+        const int per = nblk / kNumXcd, rem = nblk % kNumXcd;
+        const int lin = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+        split = lin % a.nsplit;
+        const int tlin = lin / a.nsplit;
+        const int group = a.group_m * a.tiles_n;
+        const int first_m = (tlin / group) * a.group_m;
+        const int gsize = min(a.tiles_m - first_m, a.group_m);
+        tile_m = first_m + (tlin % group) % gsize;
+        tile_n = (tlin % group) / gsize;
+    }
     const int m0 = tile_m * BM;
     const int n0 = tile_n * BN;
 
@@ -432,6 +449,30 @@ void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk) {
     *bk = kDmaCfgs[cfg].bk;
 }
 
+// XCD partition for the tile grid: the (pm, pn, ps) with pm * pn * ps = 8
+// that divide (tiles_m, tiles_n, nsplit) exactly and minimise the A rows
+// plus B columns one XCD reads, weighted by its share of K.  pm = 0 when
+// none divides (or TML_GEMM_XCDPART=0): the consecutive-id mapping is used.
+// The fused split-K exchange keeps its splits on one XCD, so ps = 1 there.
+void pick_xcd_partition(int tiles_m, int tiles_n, int nsplit, int bm, int bn, bool fused, int *pm, int *pn,
+                        int *ps) {
+    *pm = *pn = *ps = 0;
+    if (env_int("TML_GEMM_XCDPART", 1) == 0) return;
+    double best = 1e300;
+    for (int x = 1; x <= kNumXcd; x *= 2)
+        for (int y = 1; x * y <= kNumXcd; y *= 2) {
+            const int z = kNumXcd / (x * y);
+            if (tiles_m % x || tiles_n % y || nsplit % z || (fused && z != 1)) continue;
+            const double cost = ((double)(tiles_m / x) * bm + (double)(tiles_n / y) * bn) / z;
+            if (cost < best) {
+                best = cost;
+                *pm = x;
+                *pn = y;
+                *ps = z;
+            }
+        }
+}
+
 void gemm_dma_workspace_need(const MatmulArgs &m, const GemmPlan &p, size_t *partial_floats, size_t *counters) {
     *partial_floats = 0;
     *counters = 0;
@@ -464,6 +505,7 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
     a.tiles_m = (int)((m.M + bm - 1) / bm);
     a.tiles_n = (int)((m.N + bn - 1) / bn);
     a.group_m = 4;
+    pick_xcd_partition(a.tiles_m, a.tiles_n, p.nsplit, bm, bn, p.fused, &a.pm, &a.pn, &a.ps);
     a.nsplit = p.nsplit;
     a.spl = p.spl;
     a.ws = ws.partials;

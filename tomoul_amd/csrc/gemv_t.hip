@@ -4,9 +4,16 @@
 //   C[M,N] = alpha * A[M,K] . Bdeq[K,N] + beta * C + bias[N]
 //
 // with B held as its device-native "prepared" copy Bt[N][ldt]: row n of Bt
-// is column n of B, K contiguous (int8 one byte per k; int4 two k per byte,
-// even k in the low nibble -- the reference's nibble order, applied along
-// K; f32 four bytes per k), zero padded to ldt bytes, a multiple of 16.
+// holds column n of B (f32 four bytes per k, f16 two, int8 one; int4 two k
+// per byte, the first in the low nibble), zero padded to ldt bytes, a
+// multiple of 16.  The row is a sequence of 16-byte chunks (E = 4, 8, 16, 32
+// elements each) in groups of 64 ("superchunks", the last one `width`
+// chunks wide); element group g (four consecutive k) of chunk c of
+// superchunk s holds k = 64*E*s + 4*(g*width + c) .. +3 (tk_group).  Lane c
+// of a wave reads chunk c, so the activations of group g that the 64 lanes
+// need are one contiguous run of 1 KiB -- each activation load touches 8
+// cache lines instead of 64.  For f32 (one group per chunk) the order is
+// plain K order.
 // Weights are immutable after load in the reference (AttentionWeights owns
 // them until deinit, src/core/attention.zig:54-86), so the copy is made once.
 //
@@ -75,6 +82,13 @@ __device__ __forceinline__ float telem(const uintx4 &w, int i) {
 
 constexpr int tlog2(int v) { return v <= 1 ? 0 : 1 + tlog2(v / 2); }
 
+// First k of element group g of chunk ch (see the layout notes above).
+__device__ __forceinline__ int tk_group(int ch, int g, int nchunk, int E) {
+    const int sc = ch >> 6, c = ch & 63;
+    const int width = min(64, nchunk - (sc << 6));
+    return sc * 64 * E + 4 * (g * width + c);
+}
+
 // v of the lane selected by the DPP control CTRL within the 16-lane row.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
@@ -128,14 +142,13 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
 #pragma unroll
         for (int j = 0; j < JB; ++j) {
             const int ch = (bt * JB + j) * LK + lk;
-            const int k0 = ch * E;
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 const bool row_ok = ch < a.nchunk && m < a.M;
                 const float *xr = a.A + (size_t)m * a.K;
 #pragma unroll
                 for (int q = 0; q < E / 4; ++q) {
-                    const int k = k0 + 4 * q;
+                    const int k = tk_group(ch, q, a.nchunk, E);
                     if constexpr (XVEC) {
                         const bool in = row_ok && k < a.K;  // K % 4 == 0: all four in or out
                         x[j][m][q] = *(const floatx4 *)(in ? xr + k : (const float *)a.zero);
@@ -229,41 +242,46 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
     }
 }
 
-// ---- prepare: Bt[n][j] from B[K,N] (one thread per output 32-bit word)
-template <int FMT>
-__global__ __launch_bounds__(256) void prepare_t_kernel(const void *B, int K, int N, long long ldt, uint32_t *Bt) {
+// ---- prepare: Bt[n][j] from B[K,N] (ROWS = false) or from the rows of
+// W = B^T with a stride of ldw bytes (ROWS = true); one thread per output
+// 32-bit word, elements placed by tk_group.
+template <int FMT, bool ROWS>
+__device__ __forceinline__ uint32_t src_elem(const void *B, int N, long long ldw, int k, int n) {
+    const uint8_t *b = (const uint8_t *)B;
+    if constexpr (FMT == TML_FMT_F32) {
+        return ROWS ? *(const uint32_t *)(b + n * ldw + 4LL * k) : ((const uint32_t *)B)[(long long)k * N + n];
+    } else if constexpr (FMT == TML_FMT_F16) {
+        return ROWS ? *(const uint16_t *)(b + n * ldw + 2LL * k) : ((const uint16_t *)B)[(long long)k * N + n];
+    } else if constexpr (FMT == TML_FMT_Q8_0) {
+        return ROWS ? b[n * ldw + k] : b[(long long)k * N + n];
+    } else {
+        // int4: element e of a packed run is nibble e & 1 of byte e / 2
+        const long long e = ROWS ? k : (long long)k * N + n;
+        const uint32_t byte = ROWS ? b[n * ldw + e / 2] : b[e / 2];
+        return (e & 1) ? (byte >> 4) : (byte & 0xF);
+    }
+}
+
+template <int FMT, bool ROWS>
+__global__ __launch_bounds__(256) void prepare_t_kernel(const void *B, int K, int N, long long ldw, long long ldt,
+                                                        uint32_t *Bt) {
+    constexpr int E = TElems<FMT>::value;
+    constexpr int EPW = E / 4;      // elements per 32-bit word
+    constexpr int BITS = 32 / EPW;  // bits per element
     const long long words_per_row = ldt / 4;
     const long long total = (long long)N * words_per_row;
+    const int nchunk = (int)(words_per_row / 4);
     for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (long long)gridDim.x * blockDim.x) {
         const int n = (int)(i / words_per_row);
-        const long long wj = i % words_per_row;
+        const int wj = (int)(i % words_per_row);
+        const int ch = wj / 4;
         uint32_t word = 0;
-        if constexpr (FMT == TML_FMT_F32) {
-            const long long k = wj;
-            if (k < K) word = ((const uint32_t *)B)[k * N + n];
-        } else if constexpr (FMT == TML_FMT_F16) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const long long k = wj * 2 + h;
-                if (k < K) word |= (uint32_t)((const uint16_t *)B)[k * N + n] << (16 * h);
-            }
-        } else if constexpr (FMT == TML_FMT_Q8_0) {
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const long long k = wj * 4 + b;
-                if (k < K) word |= (uint32_t)((const uint8_t *)B)[k * N + n] << (8 * b);
-            }
-        } else {
-#pragma unroll
-            for (int h = 0; h < 8; ++h) {
-                const long long k = wj * 8 + h;
-                if (k < K) {
-                    const long long e = k * N + n;
-                    const uint32_t byte = ((const uint8_t *)B)[e / 2];
-                    word |= ((e & 1) ? (byte >> 4) : (byte & 0xF)) << (4 * h);
-                }
-            }
+        for (int h = 0; h < EPW; ++h) {
+            const int e = (wj % 4) * EPW + h;  // element within the chunk
+            const int k = tk_group(ch, e / 4, nchunk, E) + e % 4;
+            if (k < K) word |= src_elem<FMT, ROWS>(B, N, ldw, k, n) << (BITS * h);
         }
         Bt[i] = word;
     }
@@ -381,21 +399,38 @@ bool prepared_gemv_supported(int fmt, int64_t M, int64_t K) {
     return mr * t_elems(fmt) <= 64;
 }
 
-Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, int64_t ldt, hipStream_t s) {
+namespace {
+template <bool ROWS>
+Status launch_prepare(int fmt, int64_t K, int64_t N, const void *B, int64_t ldw, void *Bt, int64_t ldt,
+                      hipStream_t s) {
     if (ldt % 16 != 0 || ldt < prepared_row_bytes(fmt, K))
         return Status::Err(TML_ERR_INVALID_ARG, "prepared row stride too small");
+    if (K >= ((int64_t)1 << 30) || N >= ((int64_t)1 << 30) || ldt / 64 >= ((int64_t)1 << 30))
+        return Status::Err(TML_ERR_INVALID_SHAPE, "prepare: dimension exceeds 2^30");
     const long long words = (long long)N * (ldt / 4);
     const long long blocks = (words + 255) / 256;
     const dim3 grid((unsigned)(blocks < 65535 ? (blocks > 0 ? blocks : 1) : 65535));
+    const int k = (int)K, n = (int)N;
+    uint32_t *bt = (uint32_t *)Bt;
     switch (fmt) {
-        case TML_FMT_F32: prepare_t_kernel<TML_FMT_F32><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
-        case TML_FMT_Q8_0: prepare_t_kernel<TML_FMT_Q8_0><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
-        case TML_FMT_Q4_0: prepare_t_kernel<TML_FMT_Q4_0><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
-        case TML_FMT_F16: prepare_t_kernel<TML_FMT_F16><<<grid, 256, 0, s>>>(B, (int)K, (int)N, ldt, (uint32_t *)Bt); break;
+        case TML_FMT_F32: prepare_t_kernel<TML_FMT_F32, ROWS><<<grid, 256, 0, s>>>(B, k, n, ldw, ldt, bt); break;
+        case TML_FMT_Q8_0: prepare_t_kernel<TML_FMT_Q8_0, ROWS><<<grid, 256, 0, s>>>(B, k, n, ldw, ldt, bt); break;
+        case TML_FMT_Q4_0: prepare_t_kernel<TML_FMT_Q4_0, ROWS><<<grid, 256, 0, s>>>(B, k, n, ldw, ldt, bt); break;
+        case TML_FMT_F16: prepare_t_kernel<TML_FMT_F16, ROWS><<<grid, 256, 0, s>>>(B, k, n, ldw, ldt, bt); break;
         default: return Status::Err(TML_ERR_INVALID_FORMAT, "prepared layout: format must be F32, F16, Q8_0 or Q4_0");
     }
     TML_HIP_TRY(hipGetLastError());
     return Status::Ok();
+}
+}  // namespace
+
+Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, int64_t ldt, hipStream_t s) {
+    return launch_prepare<false>(fmt, K, N, B, 0, Bt, ldt, s);
+}
+
+Status launch_prepare_rows(int fmt, int64_t K, int64_t N, const void *W, int64_t ldw, void *Bt, int64_t ldt,
+                           hipStream_t s) {
+    return launch_prepare<true>(fmt, K, N, W, ldw, Bt, ldt, s);
 }
 
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,

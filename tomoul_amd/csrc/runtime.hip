@@ -596,8 +596,9 @@ int tml_hip_prepare_rows_dev(int fmt, int64_t K, int64_t N, const void *W, int64
     p->K = K;
     p->N = N;
     p->scale = scale;
-    if (K > 0 && row % 16 == 0 && ldw % 16 == 0 && ((uintptr_t)W % 16) == 0) {
-        // Already the prepared layout: use the caller's rows in place.
+    if (fmt == TML_FMT_F32 && K > 0 && row % 16 == 0 && ldw % 16 == 0 && ((uintptr_t)W % 16) == 0) {
+        // f32 rows in plain K order are already the prepared layout: use the
+        // caller's rows in place.
         p->Bt = const_cast<void *>(W);
         p->ldt = ldw;
         p->owns_bt = false;
@@ -608,11 +609,8 @@ int tml_hip_prepare_rows_dev(int fmt, int64_t K, int64_t N, const void *W, int64
     const size_t bytes = (size_t)(N > 0 ? N : 1) * (size_t)p->ldt;
     auto build = [&]() -> Status {
         TML_HIP_TRY(hipMalloc(&p->Bt, bytes));
-        TML_HIP_TRY(hipMemsetAsync(p->Bt, 0, bytes, (hipStream_t)stream));
-        if (K > 0 && N > 0)
-            TML_HIP_TRY(hipMemcpy2DAsync(p->Bt, (size_t)p->ldt, W, (size_t)ldw, (size_t)row, (size_t)N,
-                                         hipMemcpyDeviceToDevice, (hipStream_t)stream));
-        return Status::Ok();
+        if (N == 0) return Status::Ok();
+        return launch_prepare_rows(fmt, K, N, W, ldw, p->Bt, p->ldt, (hipStream_t)stream);
     };
     s = build();
     if (!s.ok()) {

@@ -189,6 +189,10 @@ __device__ __forceinline__ float tml_half_bits(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
 }
 Status launch_prepare_t(int fmt, int64_t K, int64_t N, const void *B, void *Bt, int64_t ldt, hipStream_t s);
+// The same layout from W = B^T stored as N rows of K elements, ldw bytes apart
+// (Q4_0: K even, each row starting a byte).
+Status launch_prepare_rows(int fmt, int64_t K, int64_t N, const void *W, int64_t ldw, void *Bt, int64_t ldt,
+                           hipStream_t s);
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
                      const float *bias, const float *res, float *C, float alpha_eff, float beta,
                      const void *zero, int act, long long tail0, hipStream_t s);
