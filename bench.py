@@ -232,7 +232,7 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": traffic_per_step(),
                 "algorithmic_bytes": int(sum(4 * (M * K + K * N + M * N) for (_, M, N, K) in XLMR_SHAPES)),
-                "kernel": "gemm_f32_dma_kernel (tiles 128x64, 32x64; + splitk_reduce_kernel), v_mfma_f32_16x16x4_f32",
+                "kernel": "gemm_dma_kernel<f32 B> (tiles 128x64, 32x64; + splitk_reduce_kernel), v_mfma_f32_16x16x4_f32",
                 "per_shape": per_shape, "per_shape_sum_tflops": round(tot_fl / tot_ms / 1e9, 2),
                 "per_shape_note": "each shape timed as 20 back-to-back launches (L2 warm)"}
     log(f"roofline: {json.dumps(roofline)}")
@@ -392,7 +392,9 @@ def bench_qgemm(torch, dev, sptr, timer, _abi, synth, np):
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
         fn = lambda st: _abi.gemm_dev(_abi.FMT_Q8_0, M, N, K, x.data_ptr(), q.data_ptr(),  # noqa: E731
                                       y.data_ptr(), scale=scale, stream=st)
-        ms = timer.time_ms(fn, 50)
+        # 20 launches per graph replay, as for the per-shape fp32 figures (a
+        # graph of one launch adds a graph launch to every kernel)
+        ms = timer.time_ms(lambda st, fn=fn: [fn(st) for _ in range(20)], 5, per_replay=20)
         tf = 2.0 * M * N * K / ms / 1e9
         res[f"q8_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
         log(f"qgemm q8 M={M}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
@@ -407,7 +409,7 @@ def bench_config1(torch, dev, sptr, timer, _abi, synth, np):
     y = torch.empty((1500, 1536), dtype=torch.float32, device=dev)
     fn = lambda st: _abi.gemm_dev(_abi.FMT_F32, 1500, 1536, 384, x.data_ptr(), w.data_ptr(),  # noqa: E731
                                   y.data_ptr(), bias_ptr=b.data_ptr(), stream=st)
-    ms = timer.time_ms(fn, 100)
+    ms = timer.time_ms(lambda st: [fn(st) for _ in range(20)], 5, per_replay=20)
     tf = 2.0 * 1500 * 1536 * 384 / ms / 1e9
     log(f"config1: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
     return {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
@@ -488,8 +490,13 @@ def bench_config5(torch, dev, sptr, _abi, layers: int = 32):
                     p, sc = row[i]
                     _abi.gemm_dev(fmt, M, N, K, a.data_ptr(), p, outs[i].data_ptr(), scale=sc, stream=sptr)
 
-        sweep()  # warm-up (workspaces, clocks)
+        # warm-up: workspaces, then sweeps until the clocks have settled
+        t_end = time.perf_counter() + 0.3
+        sweep()
         torch.cuda.synchronize()
+        while time.perf_counter() < t_end:
+            sweep()
+            torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         reps = 3
         e0.record()

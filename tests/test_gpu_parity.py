@@ -305,7 +305,8 @@ def test_registered_weight_path(orc):
 # ------------------------------------------------------- forced kernel plans
 @pytest.fixture
 def forced_env():
-    saved = {k: os.environ.get(k) for k in ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE", "TML_GEMM_FUSED")}
+    saved = {k: os.environ.get(k) for k in ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE", "TML_GEMM_FUSED",
+                                   "TML_GEMM_DMA_Q")}
     yield os.environ
     for k, v in saved.items():
         if v is None:
@@ -351,6 +352,36 @@ def test_sgemm_fused_split_equals_two_launch(forced_env, tile, split):
         out[fused] = (c, g)
     np.testing.assert_array_equal(out["1"][0], out["0"][0])
     np.testing.assert_array_equal(out["1"][1], out["0"][1])
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("split", [1, 3])
+def test_qgemm_dma_tiles(orc, forced_env, tile, split):
+    # F16 / Q8_0 / Q4_0 weights through the direct-copy kernel (raw bytes
+    # staged in LDS, widened on the fragment read), every tile config, K
+    # split or not, on ragged M and K (N a multiple of 32 so int4 rows are
+    # 16-byte aligned); the register-staged kernel gives the same result to
+    # rounding.
+    forced_env["TML_GEMM_DMA_TILE"] = str(tile)
+    forced_env["TML_GEMM_SPLIT"] = str(split)
+    m, n, k = 200, 320, 516
+    a = rnd(171, m, k)
+    w = rnd(172, k, n, 0.02)
+    bias = synth.normal(173, n, 0.0, 0.02)
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    h = orc.to_f16(w)
+    cases = [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s), Q_TOL), (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4), Q_TOL),
+             (_abi.FMT_F16, h, 1.0, orc.matmul_f16(a, h), FP32_TOL)]
+    for fmt, b, scale, ref, tol in cases:
+        out = {}
+        for dma in ("1", "0"):
+            forced_env["TML_GEMM_DMA_Q"] = dma
+            got = np.zeros((m, n), np.float32)
+            _abi.gemm(fmt, m, n, k, a, np.ascontiguousarray(b), got, scale=scale, bias=bias)
+            out[dma] = got
+            assert rel_err(got, ref + bias) <= tol, (fmt, dma, rel_err(got, ref + bias))
+        assert rel_err(out["1"], out["0"]) <= 1e-5, fmt
 
 
 def test_sgemm_split_deterministic(forced_env):

@@ -41,7 +41,8 @@ constexpr int kNumXcd = 8;
 struct DmaArgs {
     int M, N, K;
     const float *A;
-    const float *B;
+    const void *B;        // [K,N] in the kernel's format
+    long long ldb;        // bytes per row of B
     const float *bias;
     float *C;
     float alpha, beta;
@@ -77,8 +78,15 @@ __device__ __forceinline__ void raw_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int NW, int NS>
-__global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
+// Bytes per B element as a fraction (int4: half a byte).
+template <int FMT> struct BBytes;
+template <> struct BBytes<TML_FMT_F32> { static constexpr int num = 4, den = 1; };
+template <> struct BBytes<TML_FMT_F16> { static constexpr int num = 2, den = 1; };
+template <> struct BBytes<TML_FMT_Q8_0> { static constexpr int num = 1, den = 1; };
+template <> struct BBytes<TML_FMT_Q4_0> { static constexpr int num = 1, den = 2; };
+
+template <int FMT, int BM, int BN, int BK, int WM, int WN, int NW, int NS>
+__global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     static_assert(NS == 3 || NS == 4, "3 or 4 LDS stages");
     static_assert(BK == 32 || BK == 64, "slice depth");
     constexpr int NC = BK / 16;
@@ -90,17 +98,27 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
     constexpr int SLOTS_A = BK / 4;             // 16-byte slots per A row (8 or 16)
     constexpr int ROWS_A = 64 / SLOTS_A;        // A rows per copy block (8 or 4)
     constexpr int BLKS_A = BM * BK / 256;       // copy blocks per A stage
-    constexpr int SLOTS_B = BN / 4;             // 16-byte slots per B k-row
+    constexpr int BNUM = BBytes<FMT>::num, BDEN = BBytes<FMT>::den;
+    constexpr int BNB = BN * BNUM / BDEN;       // bytes per B k-row in LDS
+    constexpr int SLOTS_B = BNB / 16;           // 16-byte slots per B k-row
     constexpr int ROWS_B = 64 / SLOTS_B;        // B k-rows per copy block
-    constexpr int BLKS_B = BK * BN / 256;
+    constexpr int BLKS_B = BK * BNB / 1024;     // copy blocks per B stage
+    // Slot XOR for k-rows with odd k/4: the 16 lanes of a group read 16*BNUM/BDEN
+    // bytes of one k-row, so shift odd k/4 rows by that many slots (0 for int4,
+    // whose 8 bytes per group never collide with the neighbouring group's).
+    constexpr int XS = BNUM / BDEN;
     static_assert(SLOTS_A == 8 || SLOTS_A == 16, "A swizzle permutes the low 3 bits of the slot");
-    static_assert(SLOTS_B >= 8 && 64 % SLOTS_B == 0, "B swizzle needs >= 8 slots per k-row");
-    static_assert(BLKS_A % NW == 0 && BLKS_B % NW == 0, "copy blocks must split evenly over the waves");
-    constexpr int LPW = BLKS_A / NW + BLKS_B / NW;  // copies per wave per slice
+    static_assert(SLOTS_B >= 2 && 64 % SLOTS_B == 0 && (BK * BNB) % 1024 == 0, "B stage: whole 1 KiB copy blocks");
+    static_assert(BLKS_A % NW == 0, "A copy blocks must split evenly over the waves");
+    // B copy blocks go round robin over the waves; when they do not split
+    // evenly the first BLKS_B % NW waves copy one more per slice.
+    constexpr int BPW = (BLKS_B + NW - 1) / NW;
+    constexpr int LPW = BLKS_A / NW + BLKS_B / NW;          // copies per wave per slice
+    constexpr int LPW_HI = LPW + (BLKS_B % NW != 0 ? 1 : 0);  // ... for waves with an extra B block
 
     __shared__ __attribute__((aligned(1024))) float As0[BM * BK], As1[BM * BK], As2[BM * BK];
-    __shared__ __attribute__((aligned(1024))) float Bs0[BK * BN], Bs1[BK * BN], Bs2[BK * BN];
-    __shared__ __attribute__((aligned(1024))) float As3[NS > 3 ? BM * BK : 4], Bs3[NS > 3 ? BK * BN : 4];
+    __shared__ __attribute__((aligned(1024))) float Bs0[BK * BNB / 4], Bs1[BK * BNB / 4], Bs2[BK * BNB / 4];
+    __shared__ __attribute__((aligned(1024))) float As3[NS > 3 ? BM * BK : 4], Bs3[NS > 3 ? BK * BNB / 4 : 4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -151,15 +169,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
         a_row[i] = m0 + row;
         a_col[i] = q * 4;
     }
-    int b_row[BLKS_B / NW], b_col[BLKS_B / NW];
+    const bool extra_b = (BLKS_B % NW) != 0 && wave < BLKS_B % NW;
+    int b_row[BPW], b_colb[BPW];  // k-row in the slice, byte offset of the 16-byte chunk in the tile row
 #pragma unroll
-    for (int i = 0; i < BLKS_B / NW; ++i) {
+    for (int i = 0; i < BPW; ++i) {
         const int blk = wave + i * NW;
         const int krow = blk * ROWS_B + lane / SLOTS_B;
-        const int q = (lane % SLOTS_B) ^ (((krow >> 2) & 1) << 2);
+        const int q = (lane % SLOTS_B) ^ (((krow >> 2) & 1) * XS);
         b_row[i] = krow;
-        b_col[i] = n0 + q * 4;
+        b_colb[i] = q * 16;
     }
+    const long long n0b = (long long)n0 * BNUM / BDEN;
     auto issue = [&](float *as, float *bs, int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BLKS_A / NW; ++i) {
@@ -169,30 +189,39 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
             __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(as + (wave + i * NW) * 256), 16, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < BLKS_B / NW; ++i) {
-            const int gk = k0 + b_row[i];
-            const bool in = gk < a.K && b_col[i] < a.N;
-            const float *src = in ? a.B + (size_t)gk * a.N + b_col[i] : a.zero;
-            __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(bs + (wave + i * NW) * 256), 16, 0, 0);
+        for (int i = 0; i < BPW; ++i) {
+            const int blk = wave + i * NW;
+            if (BLKS_B % NW == 0 || blk < BLKS_B) {  // uniform per wave
+                const int gk = k0 + b_row[i];
+                const bool in = gk < a.K && n0 + b_colb[i] * BDEN / BNUM < a.N;
+                const void *src = in ? (const void *)((const uint8_t *)a.B + (size_t)gk * a.ldb + n0b + b_colb[i])
+                                     : (const void *)a.zero;
+                __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(bs + blk * 256), 16, 0, 0);
+            }
         }
     };
 
     // ---- fragments
+    // Narrow formats keep the B elements as read from LDS (raw bits) until
+    // the chunk that uses them: widening right after the read would make the
+    // compiler wait for the LDS reads there, between the two MFMA halves.
     struct Frag {
         floatx4 a[TM];
         float b[TN][4];
+        uint32_t braw[TN][4];
     };
     const int lrow = lane & 15;
     const int g = lane >> 4;  // lane group: feeds kk = g
     int a_off[TM];            // float offset of the lane's A row (chunk added per read)
 #pragma unroll
     for (int i = 0; i < TM; ++i) a_off[i] = (wm0 + i * 16 + lrow) * BK;
-    int b_off[TN];            // swizzled float offset of the lane's B column within a k-row
+    int b_off[TN];            // swizzled byte offset of the lane's B element within a k-row
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-        const int n = wn0 + j * 16 + lrow;
-        b_off[j] = (((n >> 2) ^ ((g & 1) << 2)) << 2) + (n & 3);
+        const int nb = (wn0 + j * 16 + lrow) * BNUM / BDEN;
+        b_off[j] = (((nb >> 4) ^ ((g & 1) * XS)) << 4) | (nb & 15);
     }
+    const int nib = (lrow & 1) * 4;  // int4: odd columns sit in the high nibble (N and n0 are even)
     const int aswz = lrow & 7;
     auto read_frag = [&](Frag &f, const float *as, const float *bs, int chunk) __attribute__((always_inline)) {
         const int q = chunk * 4 + g;
@@ -202,7 +231,26 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
         for (int s = 0; s < 4; ++s) {
             const int k = chunk * 16 + g * 4 + s;
 #pragma unroll
-            for (int j = 0; j < TN; ++j) f.b[j][s] = bs[k * BN + b_off[j]];
+            for (int j = 0; j < TN; ++j) {
+                const uint8_t *bp = (const uint8_t *)bs + k * BNB + b_off[j];
+                if constexpr (FMT == TML_FMT_F32) f.b[j][s] = *(const float *)bp;
+                else if constexpr (FMT == TML_FMT_F16) f.braw[j][s] = *(const uint16_t *)bp;
+                else if constexpr (FMT == TML_FMT_Q8_0) f.braw[j][s] = (uint32_t)(int32_t)*(const int8_t *)bp;
+                else f.braw[j][s] = *bp;
+            }
+        }
+    };
+    auto widen = [&](Frag &f) __attribute__((always_inline)) {
+        if constexpr (FMT != TML_FMT_F32) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const uint32_t r = f.braw[j][s];
+                    if constexpr (FMT == TML_FMT_F16) f.b[j][s] = tml_half_bits(r);
+                    else if constexpr (FMT == TML_FMT_Q8_0) f.b[j][s] = (float)(int32_t)r;
+                    else f.b[j][s] = (float)((int32_t)(r << (28 - nib)) >> 28);
+                }
         }
     };
 
@@ -251,7 +299,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
         issue(As0, Bs0, ks0 * BK);
         issue(As1, Bs1, (ks0 + min(1, nk - 1)) * BK);
         if constexpr (NS > 3) issue(As2, Bs2, (ks0 + min(2, nk - 1)) * BK);
-        wait_vmcnt<LPW * (NS - 2)>();  // own copies of slice 0 landed
+        // own copies of slice 0 landed
+        if (extra_b) wait_vmcnt<LPW_HI * (NS - 2)>();
+        else wait_vmcnt<LPW * (NS - 2)>();
         raw_barrier();                  // everyone's copies of slice 0 landed
         read_frag(f[0], As0, Bs0, 0);
 
@@ -275,11 +325,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_dma_kernel(DmaArgs a) {
                 Frag &cur = f[c % 2];
                 Frag &nxt = f[(c + 1) % 2];
                 if (c + 1 == NC) {
-                    wait_vmcnt<LPW * (NS - 2)>();  // own copies of slice kt+1 landed
+                    // own copies of slice kt+1 landed
+                    if (extra_b) wait_vmcnt<LPW_HI * (NS - 2)>();
+                    else wait_vmcnt<LPW * (NS - 2)>();
                     wait_lgkmcnt0();               // own reads of slice kt done before anyone overwrites it
                     raw_barrier();
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                widen(cur);
                 if (live) mma_half(cur, 0);
                 __builtin_amdgcn_sched_barrier(0);
                 if (c + 1 < NC) read_frag(nxt, stage_a(S), stage_b(S), c + 1);
@@ -449,6 +502,32 @@ void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk) {
     *bk = kDmaCfgs[cfg].bk;
 }
 
+static size_t weight_row_bytes(int fmt, int64_t N) {
+    switch (fmt) {
+        case TML_FMT_F32: return (size_t)N * 4;
+        case TML_FMT_F16: return (size_t)N * 2;
+        case TML_FMT_Q4_0: return (size_t)N / 2;
+        default: return (size_t)N;
+    }
+}
+
+template <int FMT>
+static Status launch_dma_cfg(int cfg, dim3 grid, const DmaArgs &a, hipStream_t s) {
+    switch (cfg) {
+        // <format, BM, BN, BK, WM, WN, waves, LDS stages>
+        case 0: gemm_dma_kernel<FMT, 128, 128, 32, 64, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 1: gemm_dma_kernel<FMT, 128, 64, 32, 32, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 2: gemm_dma_kernel<FMT, 64, 64, 32, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 3: gemm_dma_kernel<FMT, 256, 128, 32, 64, 64, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 4: gemm_dma_kernel<FMT, 128, 64, 64, 32, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
+        case 5: gemm_dma_kernel<FMT, 64, 64, 64, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 6: gemm_dma_kernel<FMT, 32, 64, 32, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 7: gemm_dma_kernel<FMT, 32, 64, 64, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        default: return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
+    }
+    return Status::Ok();
+}
+
 // XCD partition for the tile grid: the (pm, pn, ps) with pm * pn * ps = 8
 // that divide (tiles_m, tiles_n, nsplit) exactly and minimise the A rows
 // plus B columns one XCD reads, weighted by its share of K.  pm = 0 when
@@ -488,17 +567,29 @@ void gemm_dma_workspace_need(const MatmulArgs &m, const GemmPlan &p, size_t *par
 }
 
 bool gemm_dma_supported(const MatmulArgs &m) {
-    return m.fmt == TML_FMT_F32 && m.K % 4 == 0 && m.N % 4 == 0 && ((uintptr_t)m.A % 16) == 0 &&
-           ((uintptr_t)m.B % 16) == 0;
+    // Every 16-byte copy of a B row must start on a 16-byte boundary and hold
+    // whole elements of one row: N a multiple of 4 (f32), 8 (f16), 16 (int8),
+    // 32 (int4).
+    int nmul = 0;
+    switch (m.fmt) {
+        case TML_FMT_F32: nmul = 4; break;
+        case TML_FMT_F16: nmul = 8; break;
+        case TML_FMT_Q8_0: nmul = 16; break;
+        case TML_FMT_Q4_0: nmul = 32; break;
+        default: return false;
+    }
+    return m.K % 4 == 0 && m.N % nmul == 0 && ((uintptr_t)m.A % 16) == 0 && ((uintptr_t)m.B % 16) == 0;
 }
 
 Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspace &ws, hipStream_t s) {
-    if (!gemm_dma_supported(m)) return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM needs f32, K%4 == N%4 == 0, aligned");
+    if (!gemm_dma_supported(m))
+        return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM needs f32/f16/Q8_0/Q4_0 B, K % 4 == 0, 16-byte rows, aligned");
     const int cfg = p.cfg;
     if (cfg < 0 || cfg >= gemm_dma_num_cfgs()) return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
     DmaArgs a;
     a.M = (int)m.M; a.N = (int)m.N; a.K = (int)m.K;
-    a.A = m.A; a.B = (const float *)m.B; a.bias = m.bias; a.C = m.C;
+    a.A = m.A; a.B = m.B; a.bias = m.bias; a.C = m.C;
+    a.ldb = (long long)weight_row_bytes(m.fmt, m.N);
     a.alpha = m.alpha_eff; a.beta = m.beta;
     a.zero = (const float *)m.zero;
     const int bm = kDmaCfgs[cfg].bm, bn = kDmaCfgs[cfg].bn;
@@ -526,18 +617,14 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
         return Status::Err(TML_ERR_INVALID_ARG, "GEMM split plan does not cover K");
     if (tiles * p.nsplit >= ((int64_t)1 << 31)) return Status::Err(TML_ERR_INVALID_SHAPE, "GEMM grid too large");
     const dim3 grid((unsigned)(tiles * p.nsplit));
-    switch (cfg) {
-        // <BM, BN, BK, WM, WN, waves, LDS stages>
-        case 0: gemm_f32_dma_kernel<128, 128, 32, 64, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
-        case 1: gemm_f32_dma_kernel<128, 64, 32, 32, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
-        case 2: gemm_f32_dma_kernel<64, 64, 32, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
-        case 3: gemm_f32_dma_kernel<256, 128, 32, 64, 64, 8, 3><<<grid, 512, 0, s>>>(a); break;
-        case 4: gemm_f32_dma_kernel<128, 64, 64, 32, 32, 8, 3><<<grid, 512, 0, s>>>(a); break;
-        case 5: gemm_f32_dma_kernel<64, 64, 64, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
-        case 6: gemm_f32_dma_kernel<32, 64, 32, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
-        case 7: gemm_f32_dma_kernel<32, 64, 64, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
-        default: return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
+    Status st;
+    switch (m.fmt) {
+        case TML_FMT_F32: st = launch_dma_cfg<TML_FMT_F32>(cfg, grid, a, s); break;
+        case TML_FMT_F16: st = launch_dma_cfg<TML_FMT_F16>(cfg, grid, a, s); break;
+        case TML_FMT_Q8_0: st = launch_dma_cfg<TML_FMT_Q8_0>(cfg, grid, a, s); break;
+        default: st = launch_dma_cfg<TML_FMT_Q4_0>(cfg, grid, a, s); break;
     }
+    TML_TRY(st);
     TML_HIP_TRY(hipGetLastError());
     if (p.nsplit > 1 && !p.fused) {
         const int64_t n4 = (m.M * m.N + 3) / 4;

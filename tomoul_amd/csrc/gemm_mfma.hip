@@ -528,7 +528,16 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
 
 GemmPlan plan_gemm(const MatmulArgs &m) {
     GemmPlan p;
-    if (m.fmt == TML_FMT_F32 && env_int("TML_GEMM_DMA", 1) != 0 && gemm_dma_supported(m) && m.K > 0) {
+    // f32 B takes the direct-copy kernel whenever its rows allow it.  F16,
+    // Q8_0 and Q4_0 B take it from M = 1024 on: measured on MI355X, it is
+    // 14-18 % faster than the register-staged kernel at Whisper's 1500-row
+    // shapes with N = 3840, level at M = 1024-2048 with N = 4096-5120, and
+    // 4-11 % slower at M <= 512 (where the register-staged kernel widens B
+    // once per tile instead of once per fragment read).  TML_GEMM_DMA_Q=1 /
+    // 0 forces it on / off for those formats; TML_GEMM_DMA=0 turns it off.
+    const int dma_q = env_int("TML_GEMM_DMA_Q", -1);
+    const bool narrow_ok = m.fmt == TML_FMT_F32 || dma_q == 1 || (dma_q < 0 && m.M >= 1024);
+    if (narrow_ok && env_int("TML_GEMM_DMA", 1) != 0 && gemm_dma_supported(m) && m.K > 0) {
         p.dma = true;
         pick_dma(m.M, m.N, m.K, &p);
     }
