@@ -224,9 +224,9 @@ int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *sca
  * 16 bytes, its k in an order interleaved across 16-byte chunks so that
  * the lanes reading consecutive chunks read contiguous activations (plain K
  * order for f32); a GEMV then reads each output's weights as one contiguous
- * run and needs no cross-workgroup reduction (M <= 8 for f32 / F16, M <= 4
- * for Q8_0, M <= 2 for Q4_0).  No counterpart in the reference (its CPU
- * loops read B in place).
+ * run and needs no cross-workgroup reduction (M <= 8, every format; Q4_0
+ * above M = 4 runs on the [K,N] weight, measured faster there).  No
+ * counterpart in the reference (its CPU loops read B in place).
  *
  * tml_hip_prepare_dev: fmt is TML_FMT_F32, TML_FMT_F16, TML_FMT_Q8_0 or
  *   TML_FMT_Q4_0;
@@ -258,7 +258,7 @@ int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const flo
  * multiple of 16 bytes, with W and ldw 16-byte aligned, are used in place
  * (no copy; W must stay valid and unchanged while the handle lives);
  * otherwise the prepared layout is built on `stream` in a new buffer.  Products with more rows than the
- * prepared kernel covers (8 f32, 4 Q8_0, 2 Q4_0) run it over consecutive
+ * prepared kernels cover (8) run them over consecutive
  * row blocks.  Free with tml_hip_prepared_free.  No counterpart in the
  * reference. */
 int tml_hip_prepare_rows_dev(int fmt, int64_t K, int64_t N, const void *W, int64_t ldw, float scale, void *stream,

@@ -288,18 +288,25 @@ def test_gemv_deterministic():
 
 
 def test_registered_weight_path(orc):
-    a = rnd(71, 8, 512)
+    # A registered (resident) weight gives the uploaded weight's result: the
+    # same kernel bit for bit at M = 9 (the [K,N] GEMM on the resident copy),
+    # and to tolerance at M = 8, where the resident weight goes through its
+    # prepared copy (another summation order).
     w = rnd(72, 512, 768, 0.02)
     q, s = orc.quantize_q8(w)
-    c0 = np.zeros((8, 768), np.float32)
-    _abi.sgemm_q8(8, 768, 512, a, q, s, c0)
-    _abi.weight_register(q)
-    try:
-        c1 = np.zeros((8, 768), np.float32)
-        _abi.sgemm_q8(8, 768, 512, a, q, s, c1)
-        np.testing.assert_array_equal(c0, c1)
-    finally:
-        _abi.weight_release(q)
+    for m in (8, 9):
+        a = rnd(71, m, 512)
+        c0 = np.zeros((m, 768), np.float32)
+        _abi.sgemm_q8(m, 768, 512, a, q, s, c0)
+        _abi.weight_register(q)
+        try:
+            c1 = np.zeros((m, 768), np.float32)
+            _abi.sgemm_q8(m, 768, 512, a, q, s, c1)
+        finally:
+            _abi.weight_release(q)
+        if m == 9:
+            np.testing.assert_array_equal(c0, c1)
+        assert rel_err(c1, c0) <= Q_TOL and rel_err(c1, orc.matmul_q8(a, q, s)) <= Q_TOL
 
 
 # ------------------------------------------------------- forced kernel plans
@@ -532,9 +539,9 @@ def _run_prepared(fmt, b, scale, k, n, m, a, bias=None, c0=None, alpha=1.0, beta
                                  (2100, 130), (9000, 40)])
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 9])
 def test_prepared_vs_oracle(orc, k, n, m):
-    # The K-contiguous kernel covers M <= 8 (f32), <= 4 (Q8_0), <= 2 (Q4_0);
-    # other row counts run the [K,N] GEMV / GEMM on the weight the copy was
-    # made from (M = 9 always does).
+    # The prepared kernels cover M <= 8 (registers for small M x E, LDS-staged
+    # activations beyond); M = 9 runs the [K,N] GEMM on the weight the copy
+    # was made from.
     w = rnd(141, k, n, 0.02)
     a = rnd(142 + m, m, k)
     bias = synth.normal(143, n, 0.0, 0.02)
@@ -558,6 +565,31 @@ def test_prepared_plan_variants(orc, lk, cw, jb):
             a = rnd(152 + m, m, k)
             for fmt, b, scale, ref, tol in _prepared_cases(orc, w, k, n, a):
                 assert rel_err(_run_prepared(fmt, b, scale, k, n, m, a), ref) <= tol, (fmt, m)
+    finally:
+        for key, v in saved.items():
+            if v is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = v
+
+
+@pytest.mark.parametrize("cw", [1, 2, 4])
+def test_prepared_lds_kernel(orc, cw):
+    # The LDS-staged prepared kernel (forced for every row count and format)
+    # on several superchunks (K = 5000: 2.4 superchunks of int4, 4.9 of
+    # int8), an odd K (element-wise activation loads) and ragged N.
+    keys = ("TML_GEMVT_LDS", "TML_GEMVT_CW")
+    saved = {key: os.environ.get(key) for key in keys}
+    os.environ.update({"TML_GEMVT_LDS": "1", "TML_GEMVT_CW": str(cw)})
+    try:
+        for (k, n) in [(5000, 130), (77, 45), (1280, 600)]:
+            w = rnd(181, k, n, 0.02)
+            h = orc.to_f16(w)
+            for m in (1, 2, 3, 5, 8):
+                a = rnd(182 + m, m, k)
+                cases = _prepared_cases(orc, w, k, n, a) + [(_abi.FMT_F16, h, 1.0, orc.matmul_f16(a, h), FP32_TOL)]
+                for fmt, b, scale, ref, tol in cases:
+                    assert rel_err(_run_prepared(fmt, b, scale, k, n, m, a), ref) <= tol, (k, n, m, fmt)
     finally:
         for key, v in saved.items():
             if v is None:

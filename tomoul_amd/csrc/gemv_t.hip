@@ -287,6 +287,153 @@ __global__ __launch_bounds__(256) void prepare_t_kernel(const void *B, int K, in
     }
 }
 
+// ---- LDS-staged variant, for row counts whose activations do not fit the
+// direct kernel's registers (Q8_0 M > 4, Q4_0 M > 2) and wherever it is
+// faster.  One wave per column group of CW outputs; the four waves of a
+// workgroup share the activations of one superchunk (64 chunks = 64*E
+// consecutive k, all MR rows), staged in LDS by the whole workgroup.  Lane c
+// owns chunk c of every superchunk; its element group g needs the
+// activations at 4*(g*width + c), so the 64 lanes read 64 consecutive
+// 16-byte slots -- conflict-free.  The next superchunk's weights are loaded
+// while the current one is multiplied.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);  // row_half_mirror
+    v += dpp_mov<0x140>(v);  // row_mirror
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+template <int FMT, int MR, int CW, bool XVEC>
+__global__ __launch_bounds__(kThreads) void gemv_tl_kernel(GemvTArgs a) {
+    constexpr int E = TElems<FMT>::value;
+    constexpr int SK4 = 16 * E;  // float4 slots per row of a superchunk (64 * E k)
+    constexpr int V = CW * MR;
+    static_assert(V <= 64, "one published dot product per lane");
+    __shared__ floatx4 xs[MR * SK4];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int n0 = (blockIdx.x * kWaves + wave) * CW;
+    const int nsc = (a.nchunk + 63) >> 6;
+
+    uintx4 w[CW], wn[CW];
+    auto load_w = [&](uintx4 *dst, int sc) __attribute__((always_inline)) {
+        const int ch = (sc << 6) + lane;
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            const int n = n0 + c;
+            const bool ok = ch < a.nchunk && n < a.N;
+            dst[c] = *(const uintx4 *)(ok ? a.Bt + (size_t)n * a.ldt + (size_t)ch * 16 : (const uint8_t *)a.zero);
+        }
+    };
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+    load_w(w, 0);
+    for (int sc = 0; sc < nsc; ++sc) {
+        const int width = min(64, a.nchunk - (sc << 6));
+        const int kbase = sc * 64 * E;
+        __syncthreads();  // nobody still reads the previous superchunk
+        if constexpr (XVEC) {
+            // every load of the stage in flight at once, then the LDS stores;
+            // out-of-range slots read the zero block (K % 4 == 0: a slot is
+            // all in or all out)
+            constexpr int TOT = MR * SK4;
+            constexpr int ITER = (TOT + kThreads - 1) / kThreads;
+            floatx4 t[ITER];
+#pragma unroll
+            for (int it = 0; it < ITER; ++it) {
+                const int i = tid + it * kThreads;
+                const int m = i / SK4, k = kbase + 4 * (i % SK4);
+                const bool in = i < TOT && m < a.M && k < a.K;
+                t[it] = *(const floatx4 *)(in ? a.A + (size_t)m * a.K + k : (const float *)a.zero);
+            }
+#pragma unroll
+            for (int it = 0; it < ITER; ++it)
+                if (TOT % kThreads == 0 || tid + it * kThreads < TOT) xs[tid + it * kThreads] = t[it];
+        } else {
+            for (int i = tid; i < MR * SK4; i += kThreads) {
+                const int m = i / SK4, k = kbase + 4 * (i % SK4);
+                floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (m < a.M) {
+                    const float *xr = a.A + (size_t)m * a.K;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (k + r < a.K) v[r] = xr[k + r];
+                }
+                xs[i] = v;
+            }
+        }
+        __syncthreads();
+        if (sc + 1 < nsc) load_w(wn, sc + 1);
+        // Lanes past the superchunk's width hold zero weights (the zero
+        // block) and take zero activations: 0 * 0, never 0 * inf.
+        const bool live = lane < width;
+#pragma unroll
+        for (int gq = 0; gq < E / 4; ++gq) {
+            const int slot = gq * width + lane;
+            floatx4 xv[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) xv[m] = live ? xs[m * SK4 + slot] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < CW; ++c) {
+                float wv[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) wv[r] = telem<FMT>(w[c], 4 * gq + r);
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+                    acc[c * MR + m] += (xv[m][0] * wv[0] + xv[m][1] * wv[1]) + (xv[m][2] * wv[2] + xv[m][3] * wv[3]);
+            }
+        }
+        if (sc + 1 < nsc) {
+#pragma unroll
+            for (int c = 0; c < CW; ++c) w[c] = wn[c];
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = wave_sum(acc[i]);
+    if (lane >= V) return;
+    float val = acc[0];
+#pragma unroll
+    for (int i = 1; i < V; ++i)
+        if (lane == i) val = acc[i];
+    const int c = lane / MR, m = lane % MR;
+    const int n = n0 + c;
+    if (m < a.M && n < a.N) {
+        float *cp = a.C + (size_t)m * a.N + n;
+        float v = a.alpha * val;
+        if (a.beta != 0.0f) v += a.beta * *cp;
+        if (a.bias) v += a.bias[n];
+        const long long flat = (long long)m * a.N + n;
+        if (a.res) v += a.res[flat];
+        *cp = tml_apply_act(v, a.act, flat, a.tail0);
+    }
+}
+
+template <int FMT, int MR, int CW>
+void launch_tl2(const GemvTArgs &ka, unsigned grid, bool xvec, hipStream_t s) {
+    if (xvec) gemv_tl_kernel<FMT, MR, CW, true><<<dim3(grid), dim3(kThreads), 0, s>>>(ka);
+    else gemv_tl_kernel<FMT, MR, CW, false><<<dim3(grid), dim3(kThreads), 0, s>>>(ka);
+}
+template <int FMT, int MR>
+void launch_tl1(const GemvTArgs &ka, int cw, unsigned grid, bool xvec, hipStream_t s) {
+    if (cw >= 4) launch_tl2<FMT, MR, 4>(ka, grid, xvec, s);
+    else if (cw >= 2) launch_tl2<FMT, MR, 2>(ka, grid, xvec, s);
+    else launch_tl2<FMT, MR, 1>(ka, grid, xvec, s);
+}
+template <int FMT>
+void launch_tl0(const GemvTArgs &ka, int cw, unsigned grid, bool xvec, hipStream_t s) {
+    if (ka.M <= 1) launch_tl1<FMT, 1>(ka, cw, grid, xvec, s);
+    else if (ka.M <= 2) launch_tl1<FMT, 2>(ka, cw, grid, xvec, s);
+    else if (ka.M <= 4) launch_tl1<FMT, 4>(ka, cw, grid, xvec, s);
+    else launch_tl1<FMT, 8>(ka, cw, grid, xvec, s);
+}
+
 struct TPlan {
     int lk, cw, jb;
 };
@@ -386,17 +533,19 @@ int64_t prepared_row_bytes(int fmt, int64_t K) {
 }
 
 int64_t prepared_gemv_max_m(int fmt) {
-    return (fmt == TML_FMT_F32 || fmt == TML_FMT_F16) ? 8 : fmt == TML_FMT_Q8_0 ? 4 : fmt == TML_FMT_Q4_0 ? 2 : 0;
+    return (fmt == TML_FMT_F32 || fmt == TML_FMT_F16 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0) ? kPreparedGemvMaxM
+                                                                                                  : 0;
 }
+
+// Measured on MI355X at the decoder shapes (1024x4096 Q8_0 / F16, 1280x5120
+// and 5120x1280 Q4_0): the prepared kernels beat the [K,N] GEMV everywhere
+// except Q4_0 at M > 4 (15.0 / 19.7 us against 10.4 / 14.3 us), where the
+// staged activations of eight rows outweigh the halved weight bytes.
+bool prepared_gemv_preferred(int fmt, int64_t M) { return !(fmt == TML_FMT_Q4_0 && M > 4); }
 
 bool prepared_gemv_supported(int fmt, int64_t M, int64_t K) {
     if (fmt != TML_FMT_F32 && fmt != TML_FMT_F16 && fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0) return false;
-    if (M < 1 || M > kPreparedGemvMaxM || K >= ((int64_t)1 << 30)) return false;
-    // rows are padded to a power of two; their activations for one chunk
-    // must fit the register budget: MR * E <= 64 (f32 any M <= 8, Q8_0
-    // M <= 4, Q4_0 M <= 2)
-    const int64_t mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-    return mr * t_elems(fmt) <= 64;
+    return M >= 1 && M <= kPreparedGemvMaxM && K < ((int64_t)1 << 30);
 }
 
 namespace {
@@ -455,12 +604,38 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
     }
+    const bool xvec = (K % 4 == 0) && ((uintptr_t)A % 16 == 0);
+    // The direct kernel holds a chunk's activations for every row in
+    // registers (MR * E <= 64); beyond that, and where TML_GEMVT_LDS=1 asks
+    // for it, the activations are staged in LDS.
+    const int mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    // Staging wins for Q4_0 at M = 2 (4.9 against 7.0 us) and F16 at M > 4
+    // (6.3 against 6.7 us); elsewhere the direct kernel is as fast or faster.
+    const int lds_mode = env_int("TML_GEMVT_LDS", -1);
+    const bool use_lds = mr * t_elems(fmt) > 64 || lds_mode == 1 ||
+                         (lds_mode < 0 && ((fmt == TML_FMT_Q4_0 && mr == 2) || (fmt == TML_FMT_F16 && mr == 8)));
+    if (use_lds) {
+        // CW outputs per wave: the most (<= 4) that still gives a workgroup per CU
+        int cw = 4;
+        while (cw > 1 && (N + 4LL * cw - 1) / (4LL * cw) < cus) cw /= 2;
+        const int forced_cw = env_int("TML_GEMVT_CW", 0);
+        if (forced_cw == 1 || forced_cw == 2 || forced_cw == 4) cw = forced_cw;
+        const int64_t grid = (N + 4LL * cw - 1) / (4LL * cw);
+        if (grid >= ((int64_t)1 << 31)) return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV grid too large");
+        switch (fmt) {
+            case TML_FMT_F32: launch_tl0<TML_FMT_F32>(ka, cw, (unsigned)grid, xvec, s); break;
+            case TML_FMT_Q8_0: launch_tl0<TML_FMT_Q8_0>(ka, cw, (unsigned)grid, xvec, s); break;
+            case TML_FMT_F16: launch_tl0<TML_FMT_F16>(ka, cw, (unsigned)grid, xvec, s); break;
+            default: launch_tl0<TML_FMT_Q4_0>(ka, cw, (unsigned)grid, xvec, s); break;
+        }
+        TML_HIP_TRY(hipGetLastError());
+        return Status::Ok();
+    }
     const TPlan p = plan_t(fmt, M, N, ka.nchunk, cus);
     const int groups = kThreads / p.lk;
     const int64_t outs_per_wg = (int64_t)groups * p.cw;
     const int64_t grid = (N + outs_per_wg - 1) / outs_per_wg;
     if (grid >= ((int64_t)1 << 31)) return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV grid too large");
-    const bool xvec = (K % 4 == 0) && ((uintptr_t)A % 16 == 0);
     switch (fmt) {
         case TML_FMT_F32: launch_t0<TML_FMT_F32>(ka, p, (unsigned)grid, xvec, s); break;
         case TML_FMT_Q8_0: launch_t0<TML_FMT_Q8_0>(ka, p, (unsigned)grid, xvec, s); break;

@@ -240,7 +240,7 @@ Status gemm_prepared(DeviceCtx *c, const Prepared *p, int64_t M, const float *A,
     if (C == nullptr || (p->K > 0 && A == nullptr)) return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
     const float alpha_eff = (p->fmt == TML_FMT_Q8_0 || p->fmt == TML_FMT_Q4_0) ? alpha * p->scale : alpha;
     const long long tail0 = tml_act_tail0((long long)M * p->N);
-    if (prepared_gemv_supported(p->fmt, M, p->K))
+    if (prepared_gemv_supported(p->fmt, M, p->K) && (p->B == nullptr || prepared_gemv_preferred(p->fmt, M)))
         return launch_gemv_t(p->fmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, res, C, alpha_eff, beta, c->zero.p, act,
                              tail0, s);
     if (p->B != nullptr)
@@ -312,7 +312,7 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
     // A registered weight used at a decoder row count gets (once) and then
     // uses its prepared, K-contiguous copy.
     Registered *reg = nullptr;
-    if (preparable_fmt(fmt) && prepared_gemv_supported(fmt, M, K)) {
+    if (preparable_fmt(fmt) && prepared_gemv_supported(fmt, M, K) && prepared_gemv_preferred(fmt, M)) {
         auto it = c->weights.find(B);
         if (it != c->weights.end() && it->second.bytes >= weight_bytes(fmt, K, N)) reg = &it->second;
     }

@@ -175,9 +175,12 @@ constexpr int64_t kGemvMaxM = 8;
 // Prepared (device-native, K-contiguous) weights for decoder GEMVs
 // (gemv_t.hip): row n holds column n of B, zero padded to a multiple of 16
 // bytes; int4 keeps two k per byte, even k in the low nibble.
-constexpr int64_t kPreparedGemvMaxM = 8;  // f32; Q8_0 <= 4, Q4_0 <= 2 (prepared_gemv_supported)
+constexpr int64_t kPreparedGemvMaxM = 8;  // every prepared format
 int64_t prepared_row_bytes(int fmt, int64_t K);
 bool prepared_gemv_supported(int fmt, int64_t M, int64_t K);
+// Whether the prepared kernels are the faster choice at M rows when the
+// [K,N] weight is also at hand.
+bool prepared_gemv_preferred(int fmt, int64_t M);
 // Bytes of one row of K elements of fmt in the reference's packing (Q4_0:
 // two per byte), before the 16-byte padding of a prepared row.
 inline int64_t packed_row_bytes(int fmt, int64_t K) {
