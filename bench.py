@@ -416,11 +416,13 @@ def bench_config1(torch, dev, sptr, timer, _abi, synth, np):
 
 
 def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
-    """Decoder GEMVs at M = 1 for kernel traces / counters: Q8_0 1024x4096,
-    Q4_0 1280x5120 and 5120x1280, each on its prepared copy and in the [K,N]
-    layout, `launches` times over 16 distinct weight copies (eager launches,
-    one kernel per call)."""
-    for fmt, K, N in ((_abi.FMT_Q8_0, 1024, 4096), (_abi.FMT_Q4_0, 1280, 5120), (_abi.FMT_Q4_0, 5120, 1280)):
+    """Decoder GEMVs for kernel traces / counters: Q8_0 1024x4096 at M = 1
+    and 8, Q4_0 1280x5120 and 5120x1280 at M = 1 and 4, each on its prepared
+    copy and in the [K,N] layout, `launches` times over 16 distinct weight
+    copies (eager launches, one kernel per call)."""
+    for fmt, K, N, M in ((_abi.FMT_Q8_0, 1024, 4096, 1), (_abi.FMT_Q8_0, 1024, 4096, 8),
+                         (_abi.FMT_Q4_0, 1280, 5120, 1), (_abi.FMT_Q4_0, 1280, 5120, 4),
+                         (_abi.FMT_Q4_0, 5120, 1280, 1), (_abi.FMT_Q4_0, 5120, 1280, 4)):
         w = torch.from_numpy(synth.normal_matrix(2002, K, N, 0.02)).to(dev)
         nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
         q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -430,12 +432,12 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
         scale = float(sc.item())
         copies = q.repeat(16).view(16, nbytes)
         hs = [_abi.prepare_dev(fmt, K, N, copies[i].data_ptr(), scale, sptr) for i in range(16)]
-        x = torch.from_numpy(synth.normal_matrix(1001, 1, K)).to(dev)
-        y = torch.empty((1, N), dtype=torch.float32, device=dev)
+        x = torch.from_numpy(synth.normal_matrix(1001, M, K)).to(dev)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
         for i in range(launches):
-            _abi.gemm_prepared(hs[i % 16], 1, x.data_ptr(), y.data_ptr(), stream=sptr)
+            _abi.gemm_prepared(hs[i % 16], M, x.data_ptr(), y.data_ptr(), stream=sptr)
         for i in range(launches):
-            _abi.gemm_dev(fmt, 1, N, K, x.data_ptr(), copies[i % 16].data_ptr(), y.data_ptr(), scale=scale,
+            _abi.gemm_dev(fmt, M, N, K, x.data_ptr(), copies[i % 16].data_ptr(), y.data_ptr(), scale=scale,
                           stream=sptr)
         torch.cuda.synchronize()
         for h_ in hs:
