@@ -542,11 +542,28 @@ def cpu_baseline(budget_s: float):
         steps += 1
     tf = step_flops * steps / t_tot / 1e12
     log(f"cpu baseline: {steps} steps in {t_tot:.1f} s, {tf * 1e3:.2f} GFLOP/s (1 thread)")
+    # The same loops row-parallel (rows are independent, results bitwise
+    # unchanged) with the reference's matmulParallel cap of 4 threads
+    # (src/core/context.zig:285) and with every host thread the oracle's
+    # OpenMP runtime offers; a few steps each, reported beside the baseline.
+    threaded = {}
+    for nt in sorted({4, max(1, orc.max_threads())}):
+        n_mt, t_mt = 0, 0.0
+        while t_mt < budget_s / 4 and n_mt < 50:
+            t0 = time.perf_counter()
+            for i in range(4):
+                orc.matmul_mt(ins[i], wts[i], nt)
+            t_mt += time.perf_counter() - t0
+            n_mt += 1
+        threaded[f"{nt}_threads"] = {"value": round(step_flops * n_mt / t_mt / 1e12, 6), "steps": n_mt,
+                                     "seconds": round(t_mt, 2)}
+        log(f"cpu baseline, {nt} threads: {n_mt} steps in {t_mt:.1f} s, "
+            f"{step_flops * n_mt / t_mt / 1e9:.2f} GFLOP/s")
     return {"value": round(tf, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"{steps} full headline steps (4 GEMMs, {step_flops / 1e9:.2f} GFLOP each) with the "
                       f"oracle's restatement of the ops.zig:277-414 fallback, 1 thread, -O3 AVX2, "
                       f"{t_tot:.1f} s; zblas (the reference default) is not vendored and cannot be timed",
-            "host_cpus": os.cpu_count()}
+            "host_cpus": os.cpu_count(), "threaded": threaded}
 
 
 if __name__ == "__main__":

@@ -93,3 +93,22 @@ def test_tensor_container():
     assert t.data.dtype == np.float32 and not t.data.any() and t.shape == (2, 3)
     with pytest.raises(ValueError):
         Tensor(np.zeros(5, np.float32), (2, 3))
+
+
+def test_c_program_links_and_runs(tmp_path):
+    # The header compiles as C99 (-Wall -Werror), the library links into a C
+    # program, and the no-GPU entry points behave (tests/c/abi_smoke.c).
+    import shutil
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    exe = tmp_path / "abi_smoke"
+    libdir = os.path.dirname(_abi.LIB_PATH)
+    cmd = [gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"),
+           os.path.join(ROOT, "tests", "c", "abi_smoke.c"), "-o", str(exe), "-L", libdir, "-ltomoul_hip",
+           f"-Wl,-rpath,{libdir}", "-Wl,-rpath,/opt/rocm/lib", "-Wl,--allow-shlib-undefined"]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    fixture = os.path.join(ROOT, "tests", "golden", "tl", "linear_model.tl")
+    out = subprocess.run([str(exe), fixture], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "y(10) = 21" in out.stdout
