@@ -289,7 +289,8 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
     Two paths per shape: "prepared" -- the device-native K-contiguous copy
     made once per weight (tml_hip_prepare_dev), used where its kernel covers
     M -- and "kn" -- the weight in the reference's [K,N] layout, per call.
-    Algorithmic bytes per launch = weight bytes + 4 (scale) + 4*M*K + 4*M*N.
+    Algorithmic bytes per launch = weight bytes + scale bytes (4, or 4*N for
+    the per-column formats) + 4*M*K + 4*M*N.
     Each timed pass walks >= 1 GB of distinct weight copies, so neither L2
     nor the 256 MB Infinity Cache serves them."""
     out = {}
@@ -298,28 +299,35 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
     def run(fmt, K, N, Ms, seed, label, max_copies=256):
         w = synth.normal_matrix(seed, K, N, 0.02)
         wt = torch.from_numpy(w).to(dev)
-        wbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+        cols = fmt in (_abi.FMT_Q8_0_PC, _abi.FMT_Q4_0_PC)
+        wbytes = K * N if fmt in (_abi.FMT_Q8_0, _abi.FMT_Q8_0_PC) else (K * N + 1) // 2
+        sbytes = 4 * N if cols else 4
         q = torch.empty(wbytes, dtype=torch.uint8, device=dev)
-        sc = torch.empty(1, dtype=torch.float32, device=dev)
-        _abi.quantize_dev(fmt, K * N, wt.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
+        sc = torch.empty(sbytes // 4, dtype=torch.float32, device=dev)
+        if cols:
+            _abi.quantize_cols_dev(fmt, K, N, wt.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
+        else:
+            _abi.quantize_dev(fmt, K * N, wt.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
         torch.cuda.synchronize()
-        scale = float(sc.item())
+        scale = 1.0 if cols else float(sc.item())
+        sc_ptr = sc.data_ptr() if cols else None
         ncopy = min(max_copies, max(2, rot_bytes // wbytes))
         copies = q.repeat(ncopy).view(ncopy, wbytes)
         del wt
         ptrs = [copies[i].data_ptr() for i in range(ncopy)]
-        handles = [_abi.prepare_dev(fmt, K, N, p, scale, sptr) for p in ptrs]
+        handles = [_abi.prepare_ex_dev(fmt, K, N, p, scale=scale, scales_ptr=sc_ptr, stream=sptr) for p in ptrs]
         torch.cuda.synchronize()
         res = {}
         for M in Ms:
             x = torch.from_numpy(synth.normal_matrix(1001, M, K)).to(dev)
             y = torch.empty((M, N), dtype=torch.float32, device=dev)
-            alg = wbytes + 4 + 4 * M * K + 4 * M * N
+            alg = wbytes + sbytes + 4 * M * K + 4 * M * N
             entry = {"bytes": alg}
 
             def kn(st):
                 for p in ptrs:
-                    _abi.gemm_dev(fmt, M, N, K, x.data_ptr(), p, y.data_ptr(), scale=scale, stream=st)
+                    _abi.gemm_dev(fmt, M, N, K, x.data_ptr(), p, y.data_ptr(), scale=scale, scales_ptr=sc_ptr,
+                                  stream=st)
 
             def prep(st):
                 for h in handles:
@@ -371,6 +379,10 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
     out["q8_1024x4096"] = run(_abi.FMT_Q8_0, 1024, 4096, [1, 8], 2002, "q8 1024x4096")
     out["q4_1280x5120"] = run(_abi.FMT_Q4_0, 1280, 5120, [1, 4, 8], 2002, "q4 1280x5120")
     out["q4_5120x1280"] = run(_abi.FMT_Q4_0, 5120, 1280, [1, 4, 8], 2003, "q4 5120x1280")
+    # config 3 read as "one scale per output column" (Q8_0_PC, an extension)
+    # and the same for the int4 pair's first shape (Q4_0_PC)
+    out["q8pc_1024x4096"] = run(_abi.FMT_Q8_0_PC, 1024, 4096, [1, 8], 2002, "q8pc 1024x4096")
+    out["q4pc_1280x5120"] = run(_abi.FMT_Q4_0_PC, 1280, 5120, [1, 4], 2002, "q4pc 1280x5120")
     out["f32_vocab_rows_51866x1280"] = run_rows_f32(51866, 1280, [1, 4], 2004, "f32 vocab rows 51866x1280", 4)
     out["q8_vocab_1280x51866"] = run(_abi.FMT_Q8_0, 1280, 51866, [1], 2004, "q8 vocab 1280x51866", 12)
     out["q4_vocab_1280x51866"] = run(_abi.FMT_Q4_0, 1280, 51866, [1], 2004, "q4 vocab 1280x51866", 24)

@@ -67,6 +67,15 @@ extern "C" {
 #define TML_FMT_Q8_K 3
 #define TML_FMT_F16 4  /* IEEE binary16 [K,N], F16Tensor / matmulF32F16
                           (src/core/quantization.zig:1859-1962); .tl code 4 */
+/* Per-output-column scales: an extension, not a reference format (the
+ * reference quantizes per tensor, Q8_0 / Q4_0, or per 32 elements, Q8_K).
+ * Data exactly as Q8_0 / Q4_0; `scales` holds N floats, scale of column n =
+ * scales[n]; the per-tensor `scale` argument is ignored.  Column n is
+ * quantized by the per-tensor quantizer applied to that column alone
+ * (tml_hip_quantize_cols).  For weights quantized "symmetric int8 with a
+ * per-output-row fp32 scale" ([out,in] row = [in,out] column). */
+#define TML_FMT_Q8_0_PC 17
+#define TML_FMT_Q4_0_PC 18
 
 /* Activation applied after the bias, in the kernel epilogue. */
 #define TML_ACT_NONE 0
@@ -213,6 +222,13 @@ int tml_hip_gemm_ex_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A
  * NULL).  Device pointers, asynchronous on stream. */
 int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream);
 
+/* Per-output-column quantizers for TML_FMT_Q8_0_PC / TML_FMT_Q4_0_PC: w is
+ * W[K,N] row-major; q receives the Q8_0 / Q4_0 data of W, scales the N
+ * column scales.  No counterpart in the reference (see TML_FMT_Q8_0_PC).
+ * _dev: device pointers, asynchronous; the other: host pointers, blocking. */
+int tml_hip_quantize_cols_dev(int fmt, int64_t K, int64_t N, const float *w, void *q, float *scales, void *stream);
+int tml_hip_quantize_cols(int fmt, int64_t K, int64_t N, const float *w, void *q, float *scales);
+
 /* ------------------------------------------------------ prepared weights */
 
 /* Device-native copy of an immutable weight for decoder products.  The
@@ -243,6 +259,11 @@ int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *sca
 typedef struct tml_prepared_weight *tml_prepared_t;
 int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scale, void *stream,
                         tml_prepared_t *out);
+/* tml_hip_prepare_dev for every preparable format, per-channel ones
+ * included: `scales` is the device pointer to their N column scales (copied
+ * into the handle), NULL for the other formats. */
+int tml_hip_prepare_ex_dev(int fmt, int64_t K, int64_t N, const void *B, float scale, const float *scales,
+                           void *stream, tml_prepared_t *out);
 int tml_hip_gemm_prepared(tml_prepared_t w, int64_t M, const float *A, const float *bias, float *C, float alpha,
                           float beta, void *stream);
 

@@ -449,3 +449,56 @@ def tl_write(tensors, fmt: int) -> bytes:
         body += blob
         head[at:at + 16] = struct.pack("<QQ", start, len(blob))
     return bytes(head + body)
+
+
+# ------------------------------------------------ per-column quantization
+# An extension, not a reference format: column n of W[K,N] quantized by the
+# reference's per-tensor quantizer applied to that column alone; the product
+# is the reference's dequantize-then-f32-accumulate (matmulF32Q8,
+# src/core/quantization.zig:158-203) with scale s[n] for column n.
+def quantize_q8_cols(w) -> tuple[np.ndarray, np.ndarray]:
+    w = _f32(w)
+    k, n = w.shape
+    q = np.empty((k, n), dtype=np.int8)
+    s = np.empty(n, dtype=np.float32)
+    for j in range(n):
+        qj, s[j] = quantize_q8(np.ascontiguousarray(w[:, j]))
+        q[:, j] = qj.reshape(-1)
+    return q, s
+
+
+def _unpack_q4(packed: np.ndarray, count: int) -> np.ndarray:
+    b = np.asarray(packed, dtype=np.uint8)
+    nib = np.empty(2 * b.size, dtype=np.int8)
+    nib[0::2] = (b & 0x0F).astype(np.int8)
+    nib[1::2] = (b >> 4).astype(np.int8)
+    nib = np.where(nib & 8, nib - 16, nib).astype(np.int8)
+    return nib[:count]
+
+
+def _pack_q4(vals: np.ndarray) -> np.ndarray:
+    v = np.asarray(vals, dtype=np.int8).reshape(-1).astype(np.uint8) & 0x0F
+    if v.size % 2:
+        v = np.concatenate([v, np.zeros(1, np.uint8)])
+    return (v[0::2] | (v[1::2] << 4)).astype(np.uint8)
+
+
+def quantize_q4_cols(w) -> tuple[np.ndarray, np.ndarray]:
+    """Packed like Q4_0 over the flattened [K,N] (even element in the low nibble)."""
+    w = _f32(w)
+    k, n = w.shape
+    vals = np.empty((k, n), dtype=np.int8)
+    s = np.empty(n, dtype=np.float32)
+    for j in range(n):
+        pj, s[j] = quantize_q4(np.ascontiguousarray(w[:, j]))
+        vals[:, j] = _unpack_q4(pj, k)
+    return _pack_q4(vals), s
+
+
+def dequantize_cols(fmt: int, data, scales, k: int, n: int) -> np.ndarray:
+    vals = np.asarray(data, dtype=np.int8).reshape(k, n) if fmt == 17 else _unpack_q4(data, k * n).reshape(k, n)
+    return vals.astype(np.float32) * np.asarray(scales, dtype=np.float32)[None, :]
+
+
+def matmul_cols(a, fmt: int, data, scales, k: int, n: int) -> np.ndarray:
+    return matmul(a, dequantize_cols(fmt, data, scales, k, n))

@@ -419,3 +419,50 @@ def test_matmul_f16_equals_widened_f32(orc):
         a = rng.standard_normal((m, k)).astype(np.float32)
         h = orc.to_f16(rng.standard_normal((k, n)).astype(np.float32) * 0.1)
         np.testing.assert_array_equal(orc.matmul_f16(a, h), orc.matmul_naive(a, orc.from_f16(h)))
+
+
+# ------------------------------------------------ per-column quantization
+def test_quantize_cols_definition(orc):
+    # Per-column = the pinned per-tensor quantizer on each column; the packed
+    # int4 layout round-trips; a zero column gets scale 1 and q = 0; the
+    # product equals the f32 matmul of the dequantized weight (the
+    # reference's dequantize-then-accumulate) bitwise.
+    rng = np.random.default_rng(31)
+    w = (rng.standard_normal((37, 11)) * np.exp(rng.standard_normal(11))[None, :]).astype(np.float32)
+    w[:, 3] = 0.0
+    q, s = orc.quantize_q8_cols(w)
+    for j in range(11):
+        qj, sj = orc.quantize_q8(np.ascontiguousarray(w[:, j]))
+        np.testing.assert_array_equal(q[:, j], qj.reshape(-1))
+        assert s[j] == np.float32(sj)
+    assert s[3] == 1.0 and not q[:, 3].any()
+    p, s4 = orc.quantize_q4_cols(w)
+    vals = orc._unpack_q4(p, w.size).reshape(37, 11)
+    for j in range(11):
+        pj, sj = orc.quantize_q4(np.ascontiguousarray(w[:, j]))
+        np.testing.assert_array_equal(vals[:, j], orc._unpack_q4(pj, 37))
+        assert s4[j] == np.float32(sj)
+    np.testing.assert_array_equal(orc._pack_q4(vals), p)
+    a = rng.standard_normal((5, 37)).astype(np.float32)
+    deq = orc.dequantize_cols(17, q, s, 37, 11)
+    np.testing.assert_array_equal(orc.matmul_cols(a, 17, q, s, 37, 11), orc.matmul_naive(a, deq))
+    ref = np.zeros((5, 11), np.float32)
+    for i in range(5):
+        for kk in range(37):
+            ref[i] += a[i, kk] * (q[kk].astype(np.float32) * s)
+    np.testing.assert_array_equal(orc.matmul_cols(a, 17, q, s, 37, 11), ref)
+    # Columns that share one max reduce to the per-tensor formats: same bytes,
+    # same scale in every column, and the per-tensor matmuls' result.
+    w2 = np.clip(w, -0.9, 0.9)
+    w2[0, :] = 1.0
+    w2[1, ::2] = -1.0
+    q8, s8 = orc.quantize_q8_cols(w2)
+    qt, st = orc.quantize_q8(w2)
+    np.testing.assert_array_equal(q8.reshape(-1), qt.reshape(-1))
+    assert (s8 == np.float32(st)).all()
+    np.testing.assert_array_equal(orc.matmul_cols(a, 17, q8, s8, 37, 11), orc.matmul_q8(a, qt.reshape(37, 11), st))
+    p4, s4b = orc.quantize_q4_cols(w2)
+    pt, st4 = orc.quantize_q4(w2)
+    np.testing.assert_array_equal(p4, pt.reshape(-1))
+    assert (s4b == np.float32(st4)).all()
+    np.testing.assert_array_equal(orc.matmul_cols(a, 18, p4, s4b, 37, 11), orc.matmul_q4(a, pt, 37, 11, st4))

@@ -31,6 +31,7 @@ TML_ERR_FILE_NOT_FOUND = -12
 TML_ERR_UNSUPPORTED_QUANT_FORMAT = -13
 
 FMT_F32, FMT_Q8_0, FMT_Q4_0, FMT_Q8_K, FMT_F16 = 0, 1, 2, 3, 4
+FMT_Q8_0_PC, FMT_Q4_0_PC = 17, 18  # per-output-column scales (not reference formats)
 ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2
 
 # Every symbol the header declares, with its ctypes signature.
@@ -68,6 +69,9 @@ SIGNATURES = {
     "tml_hip_gemm_ex_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp,
                                            ctypes.c_int, _vp, _f, _f, _vp]),
     "tml_hip_gemm_prepared_ex": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, ctypes.c_int, _vp, _f, _f, _vp]),
+    "tml_hip_quantize_cols_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "tml_hip_quantize_cols": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _vp, _vp]),
+    "tml_hip_prepare_ex_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _f, _vp, _vp, ctypes.POINTER(_vp)]),
     "tml_hip_transpose_requant_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _vp, _f, _vp, _vp, _vp]),
     "tml_tl_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "tml_tl_open_bytes": (ctypes.c_int, [_vp, ctypes.c_uint64, ctypes.POINTER(_vp)]),
@@ -263,3 +267,21 @@ def transpose_requant_dev(fmt: int, rows: int, cols: int, q_ptr: int, q_out_ptr:
     """loadQuantizedTransposed{Q8,Q4,Q8K} on device pointers: [rows, cols] -> [cols, rows]."""
     check(lib().tml_hip_transpose_requant_dev(fmt, rows, cols, q_ptr, scales_ptr, scale, q_out_ptr, scales_out_ptr,
                                               stream))
+
+
+def quantize_cols(fmt: int, w: np.ndarray, q: np.ndarray, scales: np.ndarray) -> None:
+    """Per-output-column quantizer (FMT_Q8_0_PC / FMT_Q4_0_PC) of w [K,N]."""
+    k, n = w.shape
+    check(lib().tml_hip_quantize_cols(fmt, k, n, _ptr(w), _ptr(q), _ptr(scales)))
+
+
+def quantize_cols_dev(fmt: int, k: int, n: int, w_ptr: int, q_ptr: int, scales_ptr: int,
+                      stream: int | None = None) -> None:
+    check(lib().tml_hip_quantize_cols_dev(fmt, k, n, w_ptr, q_ptr, scales_ptr, stream))
+
+
+def prepare_ex_dev(fmt: int, k: int, n: int, b_ptr: int, *, scale: float = 1.0, scales_ptr: int | None = None,
+                   stream: int | None = None) -> int:
+    h = ctypes.c_void_p()
+    check(lib().tml_hip_prepare_ex_dev(fmt, k, n, b_ptr, scale, scales_ptr, stream, ctypes.byref(h)))
+    return h.value

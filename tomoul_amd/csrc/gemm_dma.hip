@@ -49,6 +49,7 @@ struct DmaArgs {
     int tiles_m, tiles_n, group_m;
     int pm, pn, ps;       // XCD partition of (m-tiles, n-tiles, splits), pm*pn*ps = 8; pm = 0: none
     int nsplit, spl;      // K splits and BK-slices per split
+    const float *colscale;  // [N] per-column factor on A.B, or nullptr
     float *ws;            // split partials: [split][M][N], or per tile in lane order when fused
     unsigned *counters;   // per-tile arrival counters (fused split-K), or nullptr
     const float *zero;
@@ -433,12 +434,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
             const int col = n0 + wn0 + j * 16 + lrow;
             if (col >= a.N) continue;
             const float bcol = a.bias ? a.bias[col] : 0.0f;
+            const float acol = a.colscale ? a.alpha * a.colscale[col] : a.alpha;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = m0 + wm0 + i * 16 + rq + r;
                 if (row < a.M) {
                     float *cp = a.C + (size_t)row * a.N + col;
-                    float v = a.alpha * acc[i][j][r];
+                    float v = acol * acc[i][j][r];
                     if (a.beta != 0.0f) v += a.beta * *cp;
                     if (a.bias) v += bcol;
                     const long long flat = (long long)row * a.N + col;
@@ -455,13 +457,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws, int nsplit, long long mn,
                                                             int n, float *C, float alpha, float beta,
                                                             const float *__restrict__ bias,
-                                                            const float *res, bool vec, int act, long long tail0) {
+                                                            const float *res, const float *colscale, bool vec,
+                                                            int act, long long tail0) {
     const long long stride = (long long)gridDim.x * blockDim.x;
     if (vec) {
         for (long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x; q < mn / 4; q += stride) {
             floatx4 acc = *(const floatx4 *)(ws + 4 * q);
             for (int s = 1; s < nsplit; ++s) acc += *(const floatx4 *)(ws + (size_t)s * mn + 4 * q);
             floatx4 v = alpha * acc;
+            if (colscale) v = (alpha * *(const floatx4 *)(colscale + (4 * q) % n)) * acc;
             float *cp = C + 4 * q;
             if (beta != 0.0f) v += beta * *(const floatx4 *)cp;
             if (bias) v += *(const floatx4 *)(bias + (4 * q) % n);
@@ -475,7 +479,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
         for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < mn; e += stride) {
             float acc = ws[e];
             for (int s = 1; s < nsplit; ++s) acc += ws[(size_t)s * mn + e];
-            float v = alpha * acc;
+            float v = (colscale ? alpha * colscale[e % n] : alpha) * acc;
             if (beta != 0.0f) v += beta * C[e];
             if (bias) v += bias[e % n];
             if (res) v += res[e];
@@ -603,6 +607,7 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
     a.counters = p.fused ? ws.counters : nullptr;
     a.act = m.act;
     a.res = m.res;
+    a.colscale = m.colscale;
     a.tail0 = tml_act_tail0((long long)m.M * m.N);
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
     if (p.nsplit > 1) {
@@ -630,9 +635,10 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
         const int64_t n4 = (m.M * m.N + 3) / 4;
         const int64_t blocks = (n4 + 255) / 256;
         splitk_reduce_kernel<<<dim3((unsigned)(blocks < 65535 ? blocks : 65535)), 256, 0, s>>>(
-            ws.partials, p.nsplit, m.M * m.N, m.N, m.C, m.alpha_eff, m.beta, m.bias, m.res,
+            ws.partials, p.nsplit, m.M * m.N, m.N, m.C, m.alpha_eff, m.beta, m.bias, m.res, m.colscale,
             m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0) &&
-                (m.res == nullptr || ((uintptr_t)m.res % 16) == 0),
+                (m.res == nullptr || ((uintptr_t)m.res % 16) == 0) &&
+                (m.colscale == nullptr || ((uintptr_t)m.colscale % 16) == 0),
             m.act, tml_act_tail0((long long)m.M * m.N));
         TML_HIP_TRY(hipGetLastError());
     }

@@ -44,6 +44,7 @@ struct GemmKArgs {
     const float *scales;
     long long block;
     const float *bias;
+    const float *colscale;  // [N] per-column factor on A.B, or nullptr
     float *C;
     float alpha;
     float beta;
@@ -341,12 +342,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_mfma_kernel(GemmKArgs a) {
             const int col = n0 + wn0 + j * 16 + lrow;
             if (col >= a.N) continue;
             const float bcol = a.bias ? a.bias[col] : 0.0f;
+            const float acol = a.colscale ? a.alpha * a.colscale[col] : a.alpha;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = m0 + wm0 + i * 16 + rq + r;
                 if (row < a.M) {
                     float *cp = a.C + (size_t)row * a.N + col;
-                    float v = a.alpha * acc[i][j][r];
+                    float v = acol * acc[i][j][r];
                     if (a.beta != 0.0f) v += a.beta * *cp;
                     if (a.bias) v += bcol;
                     const long long flat = (long long)row * a.N + col;
@@ -506,7 +508,7 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
     ka.M = (int)m.M; ka.N = (int)m.N; ka.K = (int)m.K;
     ka.A = m.A; ka.B = m.B; ka.scales = m.scales; ka.block = m.block;
     ka.bias = m.bias; ka.C = m.C; ka.alpha = m.alpha_eff; ka.beta = m.beta;
-    ka.act = m.act; ka.res = m.res; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
+    ka.act = m.act; ka.res = m.res; ka.colscale = m.colscale; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
     ka.zero = m.zero;
     int cfg = env_int("TML_GEMM_TILE", 0) - 1;
     if (cfg < 0 || cfg >= kNumCfgs) cfg = pick_cfg(m.M, m.N, cus);

@@ -45,6 +45,7 @@ struct GemvKArgs {
     const float *scales;
     long long block;
     const float *bias;
+    const float *colscale;  // [N] per-column factor on A.B, or nullptr
     float *C;
     float alpha, beta;
     int nseg;            // column segments
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
     auto epilogue = [&](int o, float p) __attribute__((always_inline)) {
         const int m = o / SC, col = col0 + o % SC;
         float *cp = a.C + (size_t)m * a.N + col;
-        float v = a.alpha * p;
+        float v = (a.colscale ? a.alpha * a.colscale[col] : a.alpha) * p;
         if (a.beta != 0.0f) v += a.beta * *cp;
         if (a.bias) v += a.bias[col];
         const long long flat = (long long)m * a.N + col;
@@ -517,7 +518,7 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     ka.nseg = p.nseg; ka.nsplit = p.nsplit; ka.nb = p.nb;
     ka.ws = ws.partials; ka.counters = ws.counters;
     ka.zero = m.zero;
-    ka.act = m.act; ka.res = m.res; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
+    ka.act = m.act; ka.res = m.res; ka.colscale = m.colscale; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
     switch (m.fmt) {
         case TML_FMT_F32: return launch_fmt<TML_FMT_F32>(ka, p, s);
         case TML_FMT_Q8_0: return launch_fmt<TML_FMT_Q8_0>(ka, p, s);

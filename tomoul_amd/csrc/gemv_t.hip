@@ -50,6 +50,7 @@ struct GemvTArgs {
     const uint8_t *Bt;
     long long ldt;        // bytes per prepared row
     const float *bias;
+    const float *colscale;  // [N] per-column factor on A.B, or nullptr
     float *C;
     float alpha, beta;
     int nchunk;           // 16-byte chunks per prepared row
@@ -58,6 +59,20 @@ struct GemvTArgs {
     const float *res;     // [M,N] residual added after the bias, or nullptr
     long long tail0;      // tml_act_tail0(M * N)
 };
+
+// C = act((scale*acc + beta*C + bias) + residual) for output (m, n), the
+// reference's order.  (Loading the column factor and bias ahead of the main
+// loop -- into VGPRs, SGPRs or LDS -- was measured and is slower overall.)
+__device__ __forceinline__ void epi_store(const GemvTArgs &a, int m, int n, float acc) {
+    if (m < a.M && n < a.N) {
+        const long long flat = (long long)m * a.N + n;
+        float v = (a.colscale ? a.alpha * a.colscale[n] : a.alpha) * acc;
+        if (a.beta != 0.0f) v += a.beta * a.C[flat];
+        if (a.bias) v += a.bias[n];
+        if (a.res) v += a.res[flat];
+        a.C[flat] = tml_apply_act(v, a.act, flat, a.tail0);
+    }
+}
 
 template <int FMT> struct TElems;
 template <> struct TElems<TML_FMT_F32> { static constexpr int value = 4; };
@@ -116,6 +131,8 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
     const int lane = tid & 63, wave = tid >> 6;
     const int grp = tid / LK, lk = tid % LK;
     const int n0 = (blockIdx.x * GROUPS + grp) * CW;
+    // the lane that publishes dot product lk % 64 (wave 0 when the group
+    // spans the workgroup) owns output (m, n0 + c) of the epilogue
 
     // One batch = JB chunks per lane: the 16-byte weight chunk of each of
     // the CW outputs plus the E activations of every row m at those k, all
@@ -229,17 +246,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
     } else {
         if (idx >= V) return;
     }
-    const int c = idx / MR, m = idx % MR;
-    const int n = n0 + c;
-    if (m < a.M && n < a.N) {
-        float *cp = a.C + (size_t)m * a.N + n;
-        float v = a.alpha * val;
-        if (a.beta != 0.0f) v += a.beta * *cp;
-        if (a.bias) v += a.bias[n];
-        const long long flat = (long long)m * a.N + n;
-        if (a.res) v += a.res[flat];
-        *cp = tml_apply_act(v, a.act, flat, a.tail0);
-    }
+    epi_store(a, idx % MR, n0 + idx / MR, val);
 }
 
 // ---- prepare: Bt[n][j] from B[K,N] (ROWS = false) or from the rows of
@@ -402,17 +409,7 @@ __global__ __launch_bounds__(kThreads) void gemv_tl_kernel(GemvTArgs a) {
 #pragma unroll
     for (int i = 1; i < V; ++i)
         if (lane == i) val = acc[i];
-    const int c = lane / MR, m = lane % MR;
-    const int n = n0 + c;
-    if (m < a.M && n < a.N) {
-        float *cp = a.C + (size_t)m * a.N + n;
-        float v = a.alpha * val;
-        if (a.beta != 0.0f) v += a.beta * *cp;
-        if (a.bias) v += a.bias[n];
-        const long long flat = (long long)m * a.N + n;
-        if (a.res) v += a.res[flat];
-        *cp = tml_apply_act(v, a.act, flat, a.tail0);
-    }
+    epi_store(a, lane % MR, n0 + lane / MR, val);
 }
 
 template <int FMT, int MR, int CW>
@@ -584,7 +581,7 @@ Status launch_prepare_rows(int fmt, int64_t K, int64_t N, const void *W, int64_t
 
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
                      const float *bias, const float *res, float *C, float alpha_eff, float beta,
-                     const void *zero, int act, long long tail0, hipStream_t s) {
+                     const void *zero, int act, long long tail0, const float *colscale, hipStream_t s) {
     if (!prepared_gemv_supported(fmt, M, K)) return Status::Err(TML_ERR_INVALID_ARG, "prepared GEMV: unsupported");
     if (N >= ((int64_t)1 << 30) || K >= ((int64_t)1 << 30))
         return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV dimension exceeds 2^30");
@@ -594,6 +591,7 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     ka.M = (int)M; ka.N = (int)N; ka.K = (int)K;
     ka.A = A; ka.Bt = (const uint8_t *)Bt; ka.ldt = ldt;
     ka.bias = bias; ka.C = C; ka.alpha = alpha_eff; ka.beta = beta;
+    ka.colscale = colscale;
     ka.nchunk = (int)((prepared_row_bytes(fmt, K) + 15) / 16);
     ka.zero = zero;
     ka.act = act;

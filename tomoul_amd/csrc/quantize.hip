@@ -108,6 +108,47 @@ __global__ __launch_bounds__(kThreads) void quantize_q8k_kernel(const float *__r
     }
 }
 
+// Per-output-column quantizers (an extension: the reference quantizes per
+// tensor or per 32-element block): column n of W[K,N] gets exactly the
+// per-tensor quantizer above applied to that column alone.
+__global__ __launch_bounds__(kThreads) void colmax_kernel(const float *__restrict__ w, int K, int N,
+                                                          float *__restrict__ mx) {
+    for (long long n = (long long)blockIdx.x * kThreads + threadIdx.x; n < N; n += (long long)gridDim.x * kThreads) {
+        float m = 0.0f;
+        for (int k = 0; k < K; ++k) m = fold_max(m, w[(long long)k * N + n]);
+        mx[n] = m;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void quantize_cols_kernel(const float *__restrict__ w, long long ne, int N,
+                                                                 const float *__restrict__ mx, bool int4,
+                                                                 void *__restrict__ q, float *__restrict__ scales) {
+    const long long stride = (long long)gridDim.x * kThreads;
+    const long long t0 = (long long)blockIdx.x * kThreads + threadIdx.x;
+    const float lim = int4 ? 7.0f : 127.0f;
+    for (long long n = t0; n < N; n += stride) scales[n] = mx[n] == 0.0f ? 1.0f : mx[n] / lim;
+    if (!int4) {
+        for (long long i = t0; i < ne; i += stride) {
+            const float m = mx[i % N];
+            ((int8_t *)q)[i] = m == 0.0f ? (int8_t)0 : (int8_t)quant(w[i], 127.0f / m, 127.0f);
+        }
+    } else {
+        // one output byte (elements 2j, 2j+1) per step: low nibble = even index
+        for (long long j = t0; j < (ne + 1) / 2; j += stride) {
+            uint32_t nib[2] = {0, 0};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const long long e = 2 * j + h;
+                if (e < ne) {
+                    const float m = mx[e % N];
+                    if (m != 0.0f) nib[h] = (uint32_t)(int)quant(w[e], 7.0f / m, 7.0f) & 0xF;
+                }
+            }
+            ((uint8_t *)q)[j] = (uint8_t)(nib[0] | (nib[1] << 4));
+        }
+    }
+}
+
 int partial_blocks(long long n) {
     long long b = (n + kThreads - 1) / kThreads;
     return (int)(b < 1 ? 1 : (b > kMaxPartials ? kMaxPartials : b));
@@ -126,6 +167,23 @@ __global__ __launch_bounds__(kThreads) void to_f16_kernel(const float *__restric
                                                           uint16_t *__restrict__ h) {
     for (long long i = (long long)blockIdx.x * kThreads + threadIdx.x; i < n; i += (long long)gridDim.x * kThreads)
         h[i] = __builtin_bit_cast(unsigned short, (_Float16)w[i]);
+}
+
+Status launch_quantize_cols(int fmt, int64_t K, int64_t N, const float *w, void *q, float *scales, float *tmp,
+                           hipStream_t s) {
+    if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0)
+        return Status::Err(TML_ERR_INVALID_FORMAT, "column quantizer: data format must be Q8_0 or Q4_0");
+    if (K < 0 || N < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
+    if (K >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31))
+        return Status::Err(TML_ERR_INVALID_SHAPE, "column quantizer: dimension exceeds 2^31");
+    if (N == 0) return Status::Ok();
+    colmax_kernel<<<grid_for(N), kThreads, 0, s>>>(w, (int)K, (int)N, tmp);
+    TML_HIP_TRY(hipGetLastError());
+    const long long ne = (long long)K * N;
+    quantize_cols_kernel<<<grid_for(ne > N ? ne : N), kThreads, 0, s>>>(w, ne, (int)N, tmp, fmt == TML_FMT_Q4_0, q,
+                                                                        scales);
+    TML_HIP_TRY(hipGetLastError());
+    return Status::Ok();
 }
 
 size_t quantize_tmp_floats(int fmt, int64_t n) {

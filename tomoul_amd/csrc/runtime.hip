@@ -71,7 +71,16 @@ struct Prepared {
     void *Bt = nullptr;
     int64_t ldt = 0;
     bool owns_bt = true;       // false: Bt is the caller's buffer, used in place
+    float *colscale = nullptr;  // per-channel formats: device copy of the N column scales
+    std::vector<float> host_colscale;  // ... and the host values it was made from (host-pointer path)
 };
+
+void free_prepared(Prepared *p) {
+    if (p == nullptr) return;
+    if (p->owns_bt && p->Bt) (void)hipFree(p->Bt);
+    if (p->colscale) (void)hipFree(p->colscale);
+    delete p;
+}
 
 struct Registered {
     void *dev = nullptr;
@@ -150,15 +159,21 @@ Status ensure_workspace(DeviceCtx *c, const MatmulArgs &m, hipStream_t s, Worksp
     return Status::Ok();
 }
 
+bool per_channel(int fmt) { return fmt == TML_FMT_Q8_0_PC || fmt == TML_FMT_Q4_0_PC; }
+// The kernels' data format of fmt (per-channel formats store Q8_0 / Q4_0 data).
+int data_fmt(int fmt) {
+    return fmt == TML_FMT_Q8_0_PC ? TML_FMT_Q8_0 : (fmt == TML_FMT_Q4_0_PC ? TML_FMT_Q4_0 : fmt);
+}
+
 bool valid_fmt(int fmt) {
     return fmt == TML_FMT_F32 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0 || fmt == TML_FMT_Q8_K ||
-           fmt == TML_FMT_F16;
+           fmt == TML_FMT_F16 || per_channel(fmt);
 }
 
 // Bytes of a K x N weight in format fmt.
 size_t weight_bytes(int fmt, int64_t K, int64_t N) {
     const size_t e = (size_t)K * (size_t)N;
-    switch (fmt) {
+    switch (data_fmt(fmt)) {
         case TML_FMT_F32: return e * 4;
         case TML_FMT_F16: return e * 2;
         case TML_FMT_Q4_0: return (e + 1) / 2;
@@ -179,10 +194,14 @@ Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const fl
         return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
     if (fmt == TML_FMT_Q8_K && (block <= 0 || (K > 0 && scales == nullptr)))
         return Status::Err(TML_ERR_INVALID_ARG, "Q8_K needs scales and a positive block size");
+    if (per_channel(fmt) && scales == nullptr)
+        return Status::Err(TML_ERR_INVALID_ARG, "per-channel formats need their N column scales");
     MatmulArgs m;
     m.M = M; m.N = N; m.K = K;
-    m.A = A; m.B = B; m.scales = scales; m.block = fmt == TML_FMT_Q8_K ? block : 1;
-    m.bias = bias; m.C = C; m.beta = beta; m.fmt = fmt;
+    m.A = A; m.B = B; m.block = fmt == TML_FMT_Q8_K ? block : 1;
+    m.scales = fmt == TML_FMT_Q8_K ? scales : nullptr;
+    m.colscale = per_channel(fmt) ? scales : nullptr;
+    m.bias = bias; m.C = C; m.beta = beta; m.fmt = data_fmt(fmt);
     m.alpha_eff = (fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0) ? alpha * scale : alpha;
     m.zero = c->zero.p;
     m.act = act;
@@ -194,13 +213,16 @@ Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const fl
 }
 
 bool preparable_fmt(int fmt) {
-    return fmt == TML_FMT_F32 || fmt == TML_FMT_F16 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0;
+    return fmt == TML_FMT_F32 || fmt == TML_FMT_F16 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0 || per_channel(fmt);
 }
 
 // Builds the prepared copy of the [K,N] device weight B (asynchronous on s).
-Status make_prepared(DeviceCtx *c, int fmt, int64_t K, int64_t N, const void *B, float scale, hipStream_t s,
-                     Prepared **out) {
-    if (!preparable_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, F16, Q8_0 or Q4_0");
+Status make_prepared(DeviceCtx *c, int fmt, int64_t K, int64_t N, const void *B, float scale,
+                     const float *colscale, hipStream_t s, Prepared **out) {
+    if (!preparable_fmt(fmt))
+        return Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, F16, Q8_0, Q4_0 or their per-channel forms");
+    if (per_channel(fmt) && colscale == nullptr && N > 0)
+        return Status::Err(TML_ERR_INVALID_ARG, "per-channel formats need their N column scales");
     if (K < 0 || N < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
     if (K >= ((int64_t)1 << 30) || N >= ((int64_t)1 << 30))
         return Status::Err(TML_ERR_INVALID_SHAPE, "prepare: dimension exceeds 2^30");
@@ -212,17 +234,19 @@ Status make_prepared(DeviceCtx *c, int fmt, int64_t K, int64_t N, const void *B,
     p->N = N;
     p->scale = scale;
     p->B = B;
-    p->ldt = prepared_row_bytes(fmt, K);
+    p->ldt = prepared_row_bytes(data_fmt(fmt), K);
     const size_t bytes = (size_t)(N > 0 ? N : 1) * (size_t)p->ldt;
-    hipError_t e = hipMalloc(&p->Bt, bytes);
-    if (e != hipSuccess) {
-        delete p;
-        return hip_status(e, "hipMalloc(prepared weight)");
-    }
-    Status st = N > 0 ? launch_prepare_t(fmt, K, N, B, p->Bt, p->ldt, s) : Status::Ok();
+    auto build = [&]() -> Status {
+        TML_HIP_TRY(hipMalloc(&p->Bt, bytes));
+        if (per_channel(fmt) && N > 0) {
+            TML_HIP_TRY(hipMalloc((void **)&p->colscale, (size_t)N * sizeof(float)));
+            TML_HIP_TRY(hipMemcpyAsync(p->colscale, colscale, (size_t)N * sizeof(float), hipMemcpyDeviceToDevice, s));
+        }
+        return N > 0 ? launch_prepare_t(data_fmt(fmt), K, N, B, p->Bt, p->ldt, s) : Status::Ok();
+    };
+    Status st = build();
     if (!st.ok()) {
-        (void)hipFree(p->Bt);
-        delete p;
+        free_prepared(p);
         return st;
     }
     *out = p;
@@ -240,22 +264,24 @@ Status gemm_prepared(DeviceCtx *c, const Prepared *p, int64_t M, const float *A,
     if (C == nullptr || (p->K > 0 && A == nullptr)) return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
     const float alpha_eff = (p->fmt == TML_FMT_Q8_0 || p->fmt == TML_FMT_Q4_0) ? alpha * p->scale : alpha;
     const long long tail0 = tml_act_tail0((long long)M * p->N);
-    if (prepared_gemv_supported(p->fmt, M, p->K) && (p->B == nullptr || prepared_gemv_preferred(p->fmt, M)))
-        return launch_gemv_t(p->fmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, res, C, alpha_eff, beta, c->zero.p, act,
-                             tail0, s);
+    const int dfmt = data_fmt(p->fmt);
+    if (prepared_gemv_supported(dfmt, M, p->K) && (p->B == nullptr || prepared_gemv_preferred(dfmt, M)))
+        return launch_gemv_t(dfmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, res, C, alpha_eff, beta, c->zero.p, act,
+                             tail0, p->colscale, s);
     if (p->B != nullptr)
-        return gemm_dev(c, p->fmt, M, p->N, p->K, A, p->B, p->scale, nullptr, 0, bias, C, alpha, beta, s, act, res);
+        return gemm_dev(c, p->fmt, M, p->N, p->K, A, p->B, p->scale, p->colscale, 0, bias, C, alpha, beta, s, act,
+                        res);
     // Rows-prepared weight (no [K,N] form): the prepared kernel over
     // consecutive blocks of rows.  Each launch reads the whole weight, so
     // this serves short prompts; the activation's flat-index split is kept
     // global by shifting tail0 per block.
-    const int64_t mr = prepared_gemv_max_m(p->fmt);
+    const int64_t mr = prepared_gemv_max_m(dfmt);
     for (int64_t r0 = 0; r0 < M; r0 += mr) {
         const int64_t rows = M - r0 < mr ? M - r0 : mr;
         const size_t off = (size_t)r0 * (size_t)p->N;
-        TML_TRY(launch_gemv_t(p->fmt, rows, p->N, p->K, A + (size_t)r0 * p->K, p->Bt, p->ldt, bias,
+        TML_TRY(launch_gemv_t(dfmt, rows, p->N, p->K, A + (size_t)r0 * p->K, p->Bt, p->ldt, bias,
                               res ? res + off : nullptr, C + off, alpha_eff, beta, c->zero.p, act,
-                              tail0 - (long long)off, s));
+                              tail0 - (long long)off, p->colscale, s));
     }
     return Status::Ok();
 }
@@ -294,6 +320,8 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
         return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
     if (fmt == TML_FMT_Q8_K && (block <= 0 || (K > 0 && scales == nullptr)))
         return Status::Err(TML_ERR_INVALID_ARG, "Q8_K needs scales and a positive block size");
+    if (per_channel(fmt) && scales == nullptr)
+        return Status::Err(TML_ERR_INVALID_ARG, "per-channel formats need their N column scales");
     DeviceCtx *c = nullptr;
     TML_TRY(current_ctx(&c));
     const void *dA = nullptr, *dB = nullptr, *dS = nullptr, *dBias = nullptr;
@@ -303,6 +331,7 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
         const size_t ns = ((size_t)K * N + block - 1) / block;
         TML_TRY(upload(c, c->scales, scales, ns * sizeof(float), &dS));
     }
+    if (per_channel(fmt)) TML_TRY(upload(c, c->scales, scales, (size_t)N * sizeof(float), &dS));
     if (bias) TML_TRY(upload(c, c->bias, bias, (size_t)N * sizeof(float), &dBias));
     const size_t cbytes = (size_t)M * N * sizeof(float);
     const void *dRes = nullptr;
@@ -318,14 +347,17 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
     }
     if (reg) {
         Prepared *p = reg->prep;
-        if (p && (p->fmt != fmt || p->K != K || p->N != N || p->scale != scale)) {
+        const bool same_cols = !per_channel(fmt) ||
+                               (p && p->host_colscale.size() == (size_t)N &&
+                                std::memcmp(p->host_colscale.data(), scales, (size_t)N * sizeof(float)) == 0);
+        if (p && (p->fmt != fmt || p->K != K || p->N != N || p->scale != scale || !same_cols)) {
             TML_HIP_TRY(hipStreamSynchronize(c->stream));
-            TML_HIP_TRY(hipFree(p->Bt));
-            delete p;
+            free_prepared(p);
             p = reg->prep = nullptr;
         }
         if (!p) {
-            TML_TRY(make_prepared(c, fmt, K, N, reg->dev, scale, c->stream, &p));
+            TML_TRY(make_prepared(c, fmt, K, N, reg->dev, scale, (const float *)dS, c->stream, &p));
+            if (per_channel(fmt)) p->host_colscale.assign(scales, scales + N);
             reg->prep = p;
         }
         TML_TRY(gemm_prepared(c, p, M, (const float *)dA, (const float *)dBias, (float *)c->c.p, alpha, beta,
@@ -382,8 +414,7 @@ void tml_hip_shutdown(void) {
         (void)hipSetDevice(c->device);
         (void)hipDeviceSynchronize();
         for (auto &w : c->weights) {
-            if (w.second.prep) (void)hipFree(w.second.prep->Bt);
-            delete w.second.prep;
+            free_prepared(w.second.prep);
             (void)hipFree(w.second.dev);
         }
         c->a.release(); c->b.release(); c->c.release(); c->bias.release(); c->res.release();
@@ -498,11 +529,8 @@ int tml_hip_weight_register(const void *host, size_t bytes) {
         if (it != c->weights.end()) {
             // a refreshed weight invalidates its prepared copy
             TML_HIP_TRY(hipStreamSynchronize(c->stream));
-            if (it->second.prep) {
-                TML_HIP_TRY(hipFree(it->second.prep->Bt));
-                delete it->second.prep;
-                it->second.prep = nullptr;
-            }
+            free_prepared(it->second.prep);
+            it->second.prep = nullptr;
             if (it->second.bytes != bytes) {
                 TML_HIP_TRY(hipFree(it->second.dev));
                 c->weights.erase(it);
@@ -530,10 +558,7 @@ int tml_hip_weight_release(const void *host) {
     if (it == c->weights.end()) return report(Status::Err(TML_ERR_INVALID_ARG, "weight not registered"));
     auto run = [&]() -> Status {
         TML_HIP_TRY(hipStreamSynchronize(c->stream));
-        if (it->second.prep) {
-            TML_HIP_TRY(hipFree(it->second.prep->Bt));
-            delete it->second.prep;
-        }
+        free_prepared(it->second.prep);
         TML_HIP_TRY(hipFree(it->second.dev));
         c->weights.erase(it);
         return Status::Ok();
@@ -568,7 +593,20 @@ int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scal
     Status s = current_ctx(&c);
     if (!s.ok()) return report(s);
     Prepared *p = nullptr;
-    s = make_prepared(c, fmt, K, N, B, scale, (hipStream_t)stream, &p);
+    s = make_prepared(c, fmt, K, N, B, scale, nullptr, (hipStream_t)stream, &p);
+    if (s.ok()) *out = (tml_prepared_t)p;
+    return report(s);
+}
+
+int tml_hip_prepare_ex_dev(int fmt, int64_t K, int64_t N, const void *B, float scale, const float *scales,
+                           void *stream, tml_prepared_t *out) {
+    if (out == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null handle pointer"));
+    *out = nullptr;
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    Prepared *p = nullptr;
+    s = make_prepared(c, fmt, K, N, B, scale, scales, (hipStream_t)stream, &p);
     if (s.ok()) *out = (tml_prepared_t)p;
     return report(s);
 }
@@ -577,8 +615,8 @@ int tml_hip_prepare_rows_dev(int fmt, int64_t K, int64_t N, const void *W, int64
                              tml_prepared_t *out) {
     if (out == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null handle pointer"));
     *out = nullptr;
-    if (!preparable_fmt(fmt))
-        return report(Status::Err(TML_ERR_INVALID_FORMAT, "prepare: format must be F32, F16, Q8_0 or Q4_0"));
+    if (!preparable_fmt(fmt) || per_channel(fmt))
+        return report(Status::Err(TML_ERR_INVALID_FORMAT, "prepare rows: format must be F32, F16, Q8_0 or Q4_0"));
     if (K < 0 || N < 0) return report(Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension"));
     if (K >= ((int64_t)1 << 30) || N >= ((int64_t)1 << 30))
         return report(Status::Err(TML_ERR_INVALID_SHAPE, "prepare: dimension exceeds 2^30"));
@@ -614,8 +652,7 @@ int tml_hip_prepare_rows_dev(int fmt, int64_t K, int64_t N, const void *W, int64
     };
     s = build();
     if (!s.ok()) {
-        if (p->Bt) (void)hipFree(p->Bt);
-        delete p;
+        free_prepared(p);
         return report(s);
     }
     *out = (tml_prepared_t)p;
@@ -647,14 +684,9 @@ int tml_hip_gemm_prepared_ex(tml_prepared_t w, int64_t M, const float *A, const 
 int tml_hip_prepared_free(tml_prepared_t w) {
     if (w == nullptr) return report(Status::Ok());
     Prepared *p = (Prepared *)w;
-    auto run = [&]() -> Status {
-        TML_HIP_TRY(hipDeviceSynchronize());
-        if (p->owns_bt) TML_HIP_TRY(hipFree(p->Bt));
-        return Status::Ok();
-    };
-    Status s = run();
-    delete p;
-    return report(s);
+    const hipError_t e = hipDeviceSynchronize();
+    free_prepared(p);
+    return report(e == hipSuccess ? Status::Ok() : hip_status(e, "hipDeviceSynchronize"));
 }
 
 int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream) {
@@ -662,6 +694,50 @@ int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *sca
     Status s = current_ctx(&c);
     if (!s.ok()) return report(s);
     return report(quantize_dev(c, fmt, n, w, q, scales, (hipStream_t)stream));
+}
+
+int tml_hip_quantize_cols_dev(int fmt, int64_t K, int64_t N, const float *w, void *q, float *scales, void *stream) {
+    if (!per_channel(fmt))
+        return report(Status::Err(TML_ERR_INVALID_FORMAT, "column quantizer: format must be Q8_0_PC or Q4_0_PC"));
+    if (K < 0 || N < 0) return report(Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension"));
+    if ((N > 0 && scales == nullptr) || (K * N > 0 && (w == nullptr || q == nullptr)))
+        return report(Status::Err(TML_ERR_INVALID_ARG, "null pointer"));
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    auto run = [&]() -> Status {
+        TML_TRY(c->qtmp.ensure((size_t)(N > 0 ? N : 1) * sizeof(float)));
+        return launch_quantize_cols(data_fmt(fmt), K, N, w, q, scales, (float *)c->qtmp.p, (hipStream_t)stream);
+    };
+    return report(run());
+}
+
+int tml_hip_quantize_cols(int fmt, int64_t K, int64_t N, const float *w, void *q, float *scales) {
+    if (!per_channel(fmt))
+        return report(Status::Err(TML_ERR_INVALID_FORMAT, "column quantizer: format must be Q8_0_PC or Q4_0_PC"));
+    if (K < 0 || N < 0) return report(Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension"));
+    if ((N > 0 && scales == nullptr) || (K * N > 0 && (w == nullptr || q == nullptr)))
+        return report(Status::Err(TML_ERR_INVALID_ARG, "null pointer"));
+    if (N == 0) return report(Status::Ok());
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    const size_t n = (size_t)K * (size_t)N;
+    const size_t qbytes = weight_bytes(fmt, K, N);
+    auto run = [&]() -> Status {
+        TML_TRY(c->a.ensure(n * sizeof(float) + 16));
+        TML_TRY(c->b.ensure(qbytes + 16));
+        TML_TRY(c->scales.ensure((size_t)N * sizeof(float)));
+        TML_TRY(c->qtmp.ensure((size_t)N * sizeof(float)));
+        if (n > 0) TML_HIP_TRY(hipMemcpyAsync(c->a.p, w, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        TML_TRY(launch_quantize_cols(data_fmt(fmt), K, N, (const float *)c->a.p, c->b.p, (float *)c->scales.p,
+                                     (float *)c->qtmp.p, c->stream));
+        if (qbytes > 0) TML_HIP_TRY(hipMemcpyAsync(q, c->b.p, qbytes, hipMemcpyDeviceToHost, c->stream));
+        TML_HIP_TRY(hipMemcpyAsync(scales, c->scales.p, (size_t)N * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        TML_HIP_TRY(hipStreamSynchronize(c->stream));
+        return Status::Ok();
+    };
+    return report(run());
 }
 
 int tml_hip_transpose_requant_dev(int fmt, int64_t rows, int64_t cols, const void *q, const float *scales,

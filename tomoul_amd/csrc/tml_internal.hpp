@@ -38,7 +38,8 @@ Status hip_status(hipError_t e, const char *what);
 // One GEMM / GEMV problem on device-resident operands:
 //   C = alpha_eff * (A . Bdeq) + beta * C + bias
 // where Bdeq is the f32 value of B's element (for Q8_0 / Q4_0 the integer
-// value; their per-tensor scale is folded into alpha_eff), then
+// value; their per-tensor scale is folded into alpha_eff, a per-column scale
+// multiplies column n of A.Bdeq: alpha_eff * colscale[n]), then
 //   C = act(C + res)
 // with an optional [M,N] residual `res` (read before C is written, per
 // element, so it may alias C) and activation `act`.
@@ -56,6 +57,7 @@ struct MatmulArgs {
     const void *zero;      // >= 64 zero bytes of device memory (see below)
     int act = TML_ACT_NONE;  // activation after the bias (TML_ACT_*)
     const float *res = nullptr;  // [M,N] residual added after the bias (may equal C)
+    const float *colscale = nullptr;  // [N] per-column factor on A.B (per-channel formats), or nullptr
 };
 
 // Activations of the epilogue, restating the reference's CPU code.
@@ -168,6 +170,9 @@ void gemv_workspace_need(const MatmulArgs &a, size_t *partial_floats, size_t *co
 Status launch_quantize(int fmt, int64_t n, const float *w, void *q, float *scales, float *tmp_max,
                        hipStream_t s);
 size_t quantize_tmp_floats(int fmt, int64_t n);
+// Per-output-column Q8_0 / Q4_0 quantizer of W[K,N]: scales[N]; tmp holds N floats.
+Status launch_quantize_cols(int fmt, int64_t K, int64_t N, const float *w, void *q, float *scales, float *tmp,
+                           hipStream_t s);
 
 // Largest M routed to the GEMV family (skinny decoder shapes).
 constexpr int64_t kGemvMaxM = 8;
@@ -198,7 +203,7 @@ Status launch_prepare_rows(int fmt, int64_t K, int64_t N, const void *W, int64_t
                            hipStream_t s);
 Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
                      const float *bias, const float *res, float *C, float alpha_eff, float beta,
-                     const void *zero, int act, long long tail0, hipStream_t s);
+                     const void *zero, int act, long long tail0, const float *colscale, hipStream_t s);
 // Largest M the prepared kernel covers for fmt (8 f32, 4 Q8_0, 2 Q4_0).
 int64_t prepared_gemv_max_m(int fmt);
 

@@ -25,6 +25,10 @@ The down-projection followed by its residual connection is fused too:
       matmulWithWeightBias + ops.addInPlace(out, residual)
       src/core/transformer.zig:223-228; Whisper's matmul + addBiasInPlace +
       ops.add(x1, fc2), src/models/whisper/encoder.zig:249-253
+
+Weights quantized with one scale per output column (QuantizedTensorColsQ8 /
+QuantizedTensorColsQ4, not reference types) take every one of these entry
+points too; the column scales are applied in the same epilogue.
 """
 from __future__ import annotations
 
@@ -53,6 +57,8 @@ def matmulWithWeight(a: Tensor, weight) -> Tensor:  # noqa: N802 (reference name
         return qz.matmulF32Q8KSimd(a, weight)
     if isinstance(weight, qz.F16Tensor):
         return qz.matmulF32F16(a, weight)
+    if isinstance(weight, (qz.QuantizedTensorColsQ8, qz.QuantizedTensorColsQ4)):
+        return qz.matmulF32Cols(a, weight)
     raise TypeError(f"unsupported weight type {type(weight).__name__}")
 
 
@@ -70,6 +76,9 @@ def matmulWithWeightBias(a: Tensor, weight, bias: Tensor) -> Tensor:  # noqa: N8
                   block=weight.block_size, bias=bias.data)
     elif isinstance(weight, qz.F16Tensor):
         _abi.gemm(_abi.FMT_F16, m, n, k, a.data, weight.data, out.data, bias=bias.data)
+    elif isinstance(weight, (qz.QuantizedTensorColsQ8, qz.QuantizedTensorColsQ4)):
+        fmt, kw = _weight_args(weight)
+        _abi.gemm(fmt, m, n, k, a.data, weight.data, out.data, bias=bias.data, **kw)
     else:
         raise TypeError(f"unsupported weight type {type(weight).__name__}")
     return out
@@ -87,6 +96,10 @@ def _weight_args(weight) -> tuple[int, dict]:
         return _abi.FMT_Q8_K, {"scales": weight.scales, "block": weight.block_size}
     if isinstance(weight, qz.F16Tensor):
         return _abi.FMT_F16, {}
+    if isinstance(weight, qz.QuantizedTensorColsQ8):
+        return _abi.FMT_Q8_0_PC, {"scales": weight.scales}
+    if isinstance(weight, qz.QuantizedTensorColsQ4):
+        return _abi.FMT_Q4_0_PC, {"scales": weight.scales}
     raise TypeError(f"unsupported weight type {type(weight).__name__}")
 
 

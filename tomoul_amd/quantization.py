@@ -135,6 +135,46 @@ class F16Tensor:
         return self.numel() * 4 / self.sizeBytes()
 
 
+class QuantizedTensorColsQ8:
+    """Not a reference type: a [K,N] weight quantized like QuantizedTensorQ8
+    but with one scale per output column n (column n alone goes through the
+    reference's Q8_0 quantizer, quantization.zig:39-90)."""
+
+    def __init__(self, scales: np.ndarray, data: np.ndarray, shape):
+        self.scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+        self.data = np.ascontiguousarray(data, dtype=np.int8).reshape(-1)
+        self.shape = tuple(int(s) for s in shape)
+
+    def numel(self) -> int:
+        return _numel(self.shape)
+
+    def sizeBytes(self) -> int:  # noqa: N802
+        return 4 * self.scales.size + self.data.size
+
+    def compressionRatio(self) -> float:  # noqa: N802
+        return self.numel() * 4 / self.sizeBytes()
+
+
+class QuantizedTensorColsQ4:
+    """Not a reference type: Q4_0 nibbles (packed over the flattened [K,N],
+    low nibble = even index, as QuantizedTensorQ4) with one scale per output
+    column."""
+
+    def __init__(self, scales: np.ndarray, data: np.ndarray, shape):
+        self.scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+        self.data = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+        self.shape = tuple(int(s) for s in shape)
+
+    def numel(self) -> int:
+        return _numel(self.shape)
+
+    def sizeBytes(self) -> int:  # noqa: N802
+        return 4 * self.scales.size + self.data.size
+
+    def compressionRatio(self) -> float:  # noqa: N802
+        return self.numel() * 4 / self.sizeBytes()
+
+
 # ---------------------------------------------------------------- quantizers
 def toF16(t: Tensor) -> F16Tensor:  # noqa: N802
     """toF16 (quantization.zig:1907-1917), on the GPU: round to nearest even."""
@@ -164,6 +204,30 @@ def quantizeQ4(t: Tensor) -> QuantizedTensorQ4:  # noqa: N802
     s = np.empty(1, dtype=np.float32)
     _abi.quantize(_abi.FMT_Q4_0, t.data, q, s)
     return QuantizedTensorQ4(float(s[0]), q[: (n + 1) // 2], t.shape)
+
+
+def _cols_shape(t: Tensor):
+    if len(t.shape) != 2:
+        raise InvalidShape(f"per-column quantization needs a 2-D [K,N] tensor, got {t.shape}")
+    return int(t.shape[0]), int(t.shape[1])
+
+
+def quantizeColsQ8(t: Tensor) -> QuantizedTensorColsQ8:  # noqa: N802
+    """Per-output-column int8 (an extension; bit-exact on the GPU)."""
+    k, n = _cols_shape(t)
+    q = np.empty(max(k * n, 1), dtype=np.int8)
+    s = np.empty(max(n, 1), dtype=np.float32)
+    _abi.quantize_cols(_abi.FMT_Q8_0_PC, t.data.reshape(k, n), q, s)
+    return QuantizedTensorColsQ8(s[:n], q[: k * n], t.shape)
+
+
+def quantizeColsQ4(t: Tensor) -> QuantizedTensorColsQ4:  # noqa: N802
+    """Per-output-column int4 (an extension; bit-exact on the GPU)."""
+    k, n = _cols_shape(t)
+    q = np.empty(max((k * n + 1) // 2, 1), dtype=np.uint8)
+    s = np.empty(max(n, 1), dtype=np.float32)
+    _abi.quantize_cols(_abi.FMT_Q4_0_PC, t.data.reshape(k, n), q, s)
+    return QuantizedTensorColsQ4(s[:n], q[: (k * n + 1) // 2], t.shape)
 
 
 # ---------------------------------------------------------------- matmuls
@@ -204,4 +268,14 @@ def matmulF32Q4Simd(a: Tensor, b: QuantizedTensorQ4) -> Tensor:  # noqa: N802
     m, n, k = _shape(a, b)
     out = Tensor.init((m, n))
     _abi.sgemm_q4(m, n, k, a.data, b.data, b.scale, out.data)
+    return out
+
+
+def matmulF32Cols(a: Tensor, b) -> Tensor:  # noqa: N802
+    """f32 activations x a per-column quantized weight: column n of the
+    product is scaled by b.scales[n] (an extension)."""
+    m, n, k = _shape(a, b)
+    fmt = _abi.FMT_Q8_0_PC if isinstance(b, QuantizedTensorColsQ8) else _abi.FMT_Q4_0_PC
+    out = Tensor.init((m, n))
+    _abi.gemm(fmt, m, n, k, a.data, b.data, out.data, scales=b.scales)
     return out
