@@ -494,11 +494,18 @@ struct DmaCfg {
 // Tile configs (index = TML_GEMM_DMA_TILE - 1); see launch_gemm_f32_dma for
 // the wave tiling and LDS stages of each.
 constexpr DmaCfg kDmaCfgs[] = {{128, 128, 32}, {128, 64, 32}, {64, 64, 32}, {256, 128, 32},
-                               {128, 64, 64},  {64, 64, 64},  {32, 64, 32}, {32, 64, 64}};
+                               {128, 64, 64},  {64, 64, 64},  {32, 64, 32}, {32, 64, 64},
+                               {96, 32, 32}};
 
 }  // namespace
 
 int gemm_dma_num_cfgs() { return (int)(sizeof(kDmaCfgs) / sizeof(kDmaCfgs[0])); }
+
+bool gemm_dma_cfg_ok(int cfg, int fmt) {
+    if (cfg < 0 || cfg >= gemm_dma_num_cfgs()) return false;
+    const int bn = kDmaCfgs[cfg].bn;
+    return fmt != TML_FMT_Q4_0 || bn >= 64;  // a k-row of int4 B holds >= 32 bytes
+}
 
 void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk) {
     *bm = kDmaCfgs[cfg].bm;
@@ -527,6 +534,14 @@ static Status launch_dma_cfg(int cfg, dim3 grid, const DmaArgs &a, hipStream_t s
         case 5: gemm_dma_kernel<FMT, 64, 64, 64, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
         case 6: gemm_dma_kernel<FMT, 32, 64, 32, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
         case 7: gemm_dma_kernel<FMT, 32, 64, 64, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 8:
+            // 32 int4 columns are 16 bytes a k-row: less than a copy block's two slots
+            if constexpr (FMT != TML_FMT_Q4_0) {
+                gemm_dma_kernel<FMT, 96, 32, 32, 48, 16, 4, 3><<<grid, 256, 0, s>>>(a);
+                break;
+            } else {
+                return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM tile 96x32 has no int4 variant");
+            }
         default: return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
     }
     return Status::Ok();

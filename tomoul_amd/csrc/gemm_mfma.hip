@@ -444,20 +444,24 @@ int device_cus() {
 // with per 32-deep slice costs measured on MI355X (us, one / several per CU):
 // 128x128 2.05, 128x64 1.09, 64x64 0.61 / 0.56, 256x128 4.05,
 // 128x64 (BK 64) 1.21, 64x64 (BK 64) 0.62, 32x64 0.40 / 0.33,
-// 32x64 (BK 64) 0.38 / 0.35; t_fill (pipeline fill, epilogue, launch)
+// 32x64 (BK 64) 0.38 / 0.35, 96x32 0.46 / 0.50 (no int4 variant; its three
+// co-resident workgroups per CU share the matrix cores, so a slice of each
+// is charged in full: fitted on 1500x1536x384, where the 768 tiles are three
+// per CU exactly); t_fill (pipeline fill, epilogue, launch)
 // ~3.5 us; t_reduce (the second launch that sums the splits' partials)
 // ~3.6 us plus the partials' traffic, splits * M * N * 8 bytes at ~6 TB/s.
-void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
-    static const double t_one[] = {2.05, 1.09, 0.61, 4.05, 1.21, 0.62, 0.40, 0.38};
-    static const double t_many[] = {2.05, 1.09, 0.56, 4.05, 1.21, 0.62, 0.33, 0.35};
+void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
+    static const double t_one[] = {2.05, 1.09, 0.61, 4.05, 1.21, 0.62, 0.40, 0.38, 0.46};
+    static const double t_many[] = {2.05, 1.09, 0.56, 4.05, 1.21, 0.62, 0.33, 0.35, 0.50};
     static const int splits[] = {1, 2, 3, 4, 6, 8};
     constexpr double kFill = 3.5, kReduce = 3.6, kBytesPerUs = 6.0e6;
     const int cus = device_cus();
-    const int forced_tile = env_int("TML_GEMM_DMA_TILE", 0) - 1;
+    int forced_tile = env_int("TML_GEMM_DMA_TILE", 0) - 1;
+    if (!gemm_dma_cfg_ok(forced_tile, fmt)) forced_tile = -1;  // unset, or no kernel for this format
     const int forced_split = env_int("TML_GEMM_SPLIT", 0);
     double best_t = 1e300;
     for (int c = 0; c < gemm_dma_num_cfgs(); ++c) {
-        if (forced_tile >= 0 && c != forced_tile) continue;
+        if ((forced_tile >= 0 && c != forced_tile) || !gemm_dma_cfg_ok(c, fmt)) continue;
         int bm = 0, bn = 0, bk = 32;
         gemm_dma_tile(c, &bm, &bn, &bk);
         const int64_t nk = (K + bk - 1) / bk;
@@ -483,7 +487,7 @@ void pick_dma(int64_t M, int64_t N, int64_t K, GemmPlan *p) {
     }
     if (best_t == 1e300) {
         // a forced split too deep for this K: run the forced (or first) tile unsplit
-        const int c = forced_tile >= 0 && forced_tile < gemm_dma_num_cfgs() ? forced_tile : 0;
+        const int c = forced_tile >= 0 ? forced_tile : 0;
         int bm = 0, bn = 0, bk = 32;
         gemm_dma_tile(c, &bm, &bn, &bk);
         const int64_t nk = (K + bk - 1) / bk;
@@ -541,7 +545,7 @@ GemmPlan plan_gemm(const MatmulArgs &m) {
     const bool narrow_ok = m.fmt == TML_FMT_F32 || dma_q == 1 || (dma_q < 0 && m.M >= 1024);
     if (narrow_ok && env_int("TML_GEMM_DMA", 1) != 0 && gemm_dma_supported(m) && m.K > 0) {
         p.dma = true;
-        pick_dma(m.M, m.N, m.K, &p);
+        pick_dma(m.M, m.N, m.K, m.fmt, &p);
     }
     return p;
 }

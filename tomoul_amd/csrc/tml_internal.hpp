@@ -161,6 +161,7 @@ Status launch_gemm_mfma(const MatmulArgs &a, const Workspace &ws, hipStream_t s)
 // K % 4 == N % 4 == 0 and A, B are 16-byte aligned.
 bool gemm_dma_supported(const MatmulArgs &a);
 int gemm_dma_num_cfgs();
+bool gemm_dma_cfg_ok(int cfg, int fmt);  // the tile config has a kernel for B format fmt
 void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk);
 Status launch_gemm_f32_dma(const MatmulArgs &a, const GemmPlan &p, const Workspace &ws, hipStream_t s);
 void gemm_dma_workspace_need(const MatmulArgs &a, const GemmPlan &p, size_t *partial_floats, size_t *counters);
