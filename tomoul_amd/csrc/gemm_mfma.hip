@@ -539,10 +539,22 @@ GemmPlan plan_gemm(const MatmulArgs &m) {
     // 14-18 % faster than the register-staged kernel at Whisper's 1500-row
     // shapes with N = 3840, level at M = 1024-2048 with N = 4096-5120, and
     // 4-11 % slower at M <= 512 (where the register-staged kernel widens B
-    // once per tile instead of once per fragment read).  TML_GEMM_DMA_Q=1 /
-    // 0 forces it on / off for those formats; TML_GEMM_DMA=0 turns it off.
+    // once per tile instead of once per fragment read) -- unless the
+    // register-staged kernel's best tiling leaves most CUs idle (it has no
+    // K split): at 256x768x3072 Q8_0 the direct-copy kernel with its split
+    // takes 23.1 us against 45.1, at 512x384x1536 16.3 against 24.8, at
+    // 256x768x768 10.9 against 14.5 (96 register tiles each), while with
+    // 192 register tiles (256x3072x768, 512x1536x384) it is 2-9 % slower.
+    // TML_GEMM_DMA_Q=1 / 0 forces it on / off for those formats;
+    // TML_GEMM_DMA=0 turns it off.
     const int dma_q = env_int("TML_GEMM_DMA_Q", -1);
-    const bool narrow_ok = m.fmt == TML_FMT_F32 || dma_q == 1 || (dma_q < 0 && m.M >= 1024);
+    bool few_tiles = false;
+    if (m.fmt != TML_FMT_F32 && m.M < 1024) {
+        const int cus = device_cus();
+        const int c = pick_cfg(m.M, m.N, cus);
+        few_tiles = ((m.M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((m.N + kCfgs[c].bn - 1) / kCfgs[c].bn) < cus / 2;
+    }
+    const bool narrow_ok = m.fmt == TML_FMT_F32 || dma_q == 1 || (dma_q < 0 && (m.M >= 1024 || few_tiles));
     if (narrow_ok && env_int("TML_GEMM_DMA", 1) != 0 && gemm_dma_supported(m) && m.K > 0) {
         p.dma = true;
         pick_dma(m.M, m.N, m.K, m.fmt, &p);
