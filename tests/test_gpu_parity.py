@@ -364,8 +364,9 @@ def test_sgemm_fused_split_equals_two_launch(forced_env, tile, split):
 @pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9])
 @pytest.mark.parametrize("split", [1, 3])
 def test_qgemm_dma_tiles(orc, forced_env, tile, split):
-    # F16 / Q8_0 / Q4_0 weights through the direct-copy kernel (raw bytes
-    # staged in LDS, widened on the fragment read), every tile config, K
+    # F16 / Q8_0 / Q4_0 / Q8_K weights through the direct-copy kernel (raw
+    # bytes staged in LDS, widened on the fragment read; Q8_K's block scales
+    # staged beside them), every tile config, K
     # split or not, on ragged M and K (N a multiple of 32 so int4 rows are
     # 16-byte aligned); the register-staged kernel gives the same result to
     # rounding.  Tile 9 (96x32) has no int4 variant: the planner ignores the
@@ -379,14 +380,17 @@ def test_qgemm_dma_tiles(orc, forced_env, tile, split):
     q, s = orc.quantize_q8(w)
     p, s4 = orc.quantize_q4(w)
     h = orc.to_f16(w)
+    qk, sk = orc.quantize_q8k(w)
     cases = [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s), Q_TOL), (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4), Q_TOL),
-             (_abi.FMT_F16, h, 1.0, orc.matmul_f16(a, h), FP32_TOL)]
+             (_abi.FMT_F16, h, 1.0, orc.matmul_f16(a, h), FP32_TOL),
+             (_abi.FMT_Q8_K, qk, sk, orc.matmul_q8k(a, qk, sk), Q_TOL)]
     for fmt, b, scale, ref, tol in cases:
         out = {}
+        kw = {"scales": np.ascontiguousarray(scale, np.float32), "block": 32} if fmt == _abi.FMT_Q8_K else {"scale": scale}
         for dma in ("1", "0"):
             forced_env["TML_GEMM_DMA_Q"] = dma
             got = np.zeros((m, n), np.float32)
-            _abi.gemm(fmt, m, n, k, a, np.ascontiguousarray(b), got, scale=scale, bias=bias)
+            _abi.gemm(fmt, m, n, k, a, np.ascontiguousarray(b), got, bias=bias, **kw)
             out[dma] = got
             assert rel_err(got, ref + bias) <= tol, (fmt, dma, rel_err(got, ref + bias))
         assert rel_err(out["1"], out["0"]) <= 1e-5, fmt

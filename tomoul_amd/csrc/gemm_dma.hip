@@ -50,6 +50,8 @@ struct DmaArgs {
     int pm, pn, ps;       // XCD partition of (m-tiles, n-tiles, splits), pm*pn*ps = 8; pm = 0: none
     int nsplit, spl;      // K splits and BK-slices per split
     const float *colscale;  // [N] per-column factor on A.B, or nullptr
+    const float *kscales;   // Q8_K: scale of element (k, n) at kscales[k * sld + n / 32]
+    int sld;                // Q8_K: scale blocks per k-row (N / 32)
     float *ws;            // split partials: [split][M][N], or per tile in lane order when fused
     unsigned *counters;   // per-tile arrival counters (fused split-K), or nullptr
     const float *zero;
@@ -84,6 +86,7 @@ template <int FMT> struct BBytes;
 template <> struct BBytes<TML_FMT_F32> { static constexpr int num = 4, den = 1; };
 template <> struct BBytes<TML_FMT_F16> { static constexpr int num = 2, den = 1; };
 template <> struct BBytes<TML_FMT_Q8_0> { static constexpr int num = 1, den = 1; };
+template <> struct BBytes<TML_FMT_Q8_K> { static constexpr int num = 1, den = 1; };
 template <> struct BBytes<TML_FMT_Q4_0> { static constexpr int num = 1, den = 2; };
 
 template <int FMT, int BM, int BN, int BK, int WM, int WN, int NW, int NS>
@@ -116,10 +119,20 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     constexpr int BPW = (BLKS_B + NW - 1) / NW;
     constexpr int LPW = BLKS_A / NW + BLKS_B / NW;          // copies per wave per slice
     constexpr int LPW_HI = LPW + (BLKS_B % NW != 0 ? 1 : 0);  // ... for waves with an extra B block
+    // Q8_K: the slice's block scales, BK k-rows x BN/32 blocks, stored
+    // [block][k] in LDS, copied 4 bytes a lane by the last wave (never one
+    // with an extra B block) in SCI instructions.
+    constexpr bool KS = FMT == TML_FMT_Q8_K;
+    static_assert(!KS || BN % 32 == 0, "Q8_K tiles hold whole 32-column scale blocks");
+    constexpr int SCN = KS ? BK * (BN / 32) : 0;
+    constexpr int SCI = (SCN + 63) / 64;
+    constexpr int LPW_S = LPW + SCI;  // copies per slice of the wave that also copies the scales
 
     __shared__ __attribute__((aligned(1024))) float As0[BM * BK], As1[BM * BK], As2[BM * BK];
     __shared__ __attribute__((aligned(1024))) float Bs0[BK * BNB / 4], Bs1[BK * BNB / 4], Bs2[BK * BNB / 4];
     __shared__ __attribute__((aligned(1024))) float As3[NS > 3 ? BM * BK : 4], Bs3[NS > 3 ? BK * BNB / 4 : 4];
+    __shared__ __attribute__((aligned(16))) float Ss0[KS ? SCI * 64 : 4], Ss1[KS ? SCI * 64 : 4],
+        Ss2[KS ? SCI * 64 : 4], Ss3[KS && NS > 3 ? SCI * 64 : 4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -181,7 +194,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         b_colb[i] = q * 16;
     }
     const long long n0b = (long long)n0 * BNUM / BDEN;
-    auto issue = [&](float *as, float *bs, int k0) __attribute__((always_inline)) {
+    const bool scale_wave = KS && wave == NW - 1;
+    auto issue = [&](float *as, float *bs, float *ss, int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BLKS_A / NW; ++i) {
             const int gk = k0 + a_col[i];
@@ -200,6 +214,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                 __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(bs + blk * 256), 16, 0, 0);
             }
         }
+        if constexpr (KS) {
+            if (scale_wave) {
+#pragma unroll
+                for (int ci = 0; ci < SCI; ++ci) {
+                    const int l = lane + 64 * ci;
+                    const int nb = l / BK, k = l % BK;
+                    const bool in = l < SCN && k0 + k < a.K && n0 / 32 + nb < a.sld;
+                    const float *src = in ? a.kscales + (size_t)(k0 + k) * a.sld + n0 / 32 + nb : a.zero;
+                    __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(ss + ci * 64), 4, 0, 0);
+                }
+            }
+        }
     };
 
     // ---- fragments
@@ -210,6 +236,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         floatx4 a[TM];
         float b[TN][4];
         uint32_t braw[TN][4];
+        floatx4 sc[KS ? TN : 1];  // Q8_K: the scales of b's four k
     };
     const int lrow = lane & 15;
     const int g = lane >> 4;  // lane group: feeds kk = g
@@ -224,8 +251,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     }
     const int nib = (lrow & 1) * 4;  // int4: odd columns sit in the high nibble (N and n0 are even)
     const int aswz = lrow & 7;
-    auto read_frag = [&](Frag &f, const float *as, const float *bs, int chunk) __attribute__((always_inline)) {
+    auto read_frag = [&](Frag &f, const float *as, const float *bs, const float *ss, int chunk)
+                         __attribute__((always_inline)) {
         const int q = chunk * 4 + g;
+        if constexpr (KS) {
+            // fragment j's 16 columns lie in scale block (wn0 + j * 16) / 32
+#pragma unroll
+            for (int j = 0; j < TN; ++j) f.sc[j] = *(const floatx4 *)&ss[((wn0 + j * 16) / 32) * BK + chunk * 16 + g * 4];
+        }
 #pragma unroll
         for (int i = 0; i < TM; ++i) f.a[i] = *(const floatx4 *)&as[a_off[i] + ((q ^ aswz) << 2)];
 #pragma unroll
@@ -236,7 +269,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                 const uint8_t *bp = (const uint8_t *)bs + k * BNB + b_off[j];
                 if constexpr (FMT == TML_FMT_F32) f.b[j][s] = *(const float *)bp;
                 else if constexpr (FMT == TML_FMT_F16) f.braw[j][s] = *(const uint16_t *)bp;
-                else if constexpr (FMT == TML_FMT_Q8_0) f.braw[j][s] = (uint32_t)(int32_t)*(const int8_t *)bp;
+                else if constexpr (FMT == TML_FMT_Q8_0 || FMT == TML_FMT_Q8_K)
+                    f.braw[j][s] = (uint32_t)(int32_t)*(const int8_t *)bp;
                 else f.braw[j][s] = *bp;
             }
         }
@@ -250,6 +284,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                     const uint32_t r = f.braw[j][s];
                     if constexpr (FMT == TML_FMT_F16) f.b[j][s] = tml_half_bits(r);
                     else if constexpr (FMT == TML_FMT_Q8_0) f.b[j][s] = (float)(int32_t)r;
+                    // reference dequantization: f32(q) * scale, rounded per element
+                    else if constexpr (FMT == TML_FMT_Q8_K) f.b[j][s] = (float)(int32_t)r * f.sc[j][s];
                     else f.b[j][s] = (float)((int32_t)(r << (28 - nib)) >> 28);
                 }
         }
@@ -286,6 +322,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         else if constexpr (decltype(S)::value == 2) return Bs2;
         else return Bs3;
     };
+    auto stage_s = [&](auto S) -> float * {
+        if constexpr (decltype(S)::value == 0) return Ss0;
+        else if constexpr (decltype(S)::value == 1) return Ss1;
+        else if constexpr (decltype(S)::value == 2) return Ss2;
+        else return Ss3;
+    };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
@@ -297,14 +339,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     if (nk > 0) {
         Frag f[2];
         // Prologue: slices 0 .. NS-2 in flight, slice 0 landed.
-        issue(As0, Bs0, ks0 * BK);
-        issue(As1, Bs1, (ks0 + min(1, nk - 1)) * BK);
-        if constexpr (NS > 3) issue(As2, Bs2, (ks0 + min(2, nk - 1)) * BK);
+        issue(As0, Bs0, Ss0, ks0 * BK);
+        issue(As1, Bs1, Ss1, (ks0 + min(1, nk - 1)) * BK);
+        if constexpr (NS > 3) issue(As2, Bs2, Ss2, (ks0 + min(2, nk - 1)) * BK);
         // own copies of slice 0 landed
         if (extra_b) wait_vmcnt<LPW_HI * (NS - 2)>();
+        else if (scale_wave) wait_vmcnt<LPW_S * (NS - 2)>();
         else wait_vmcnt<LPW * (NS - 2)>();
         raw_barrier();                  // everyone's copies of slice 0 landed
-        read_frag(f[0], As0, Bs0, 0);
+        read_frag(f[0], As0, Bs0, Ss0, 0);
 
         // One slice: stage S holds slice kt; stage S-1 (mod NS, slice kt-1,
         // fully read before the previous barrier) receives slice kt+NS-1.
@@ -316,7 +359,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
             using SN = std::integral_constant<int, (s + 1) % NS>;
             using SF = std::integral_constant<int, (s + NS - 1) % NS>;
             const bool live = kt < nk;
-            issue(stage_a(SF{}), stage_b(SF{}), (ks0 + min(kt + NS - 1, nk - 1)) * BK);
+            issue(stage_a(SF{}), stage_b(SF{}), stage_s(SF{}), (ks0 + min(kt + NS - 1, nk - 1)) * BK);
             // Chunk c's fragments sit in f[c % 2].  The reads of the next
             // chunk go between the two halves of chunk c's MFMAs: while copies
             // to LDS are in flight the compiler can only wait for LDS reads
@@ -328,6 +371,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                 if (c + 1 == NC) {
                     // own copies of slice kt+1 landed
                     if (extra_b) wait_vmcnt<LPW_HI * (NS - 2)>();
+                    else if (scale_wave) wait_vmcnt<LPW_S * (NS - 2)>();
                     else wait_vmcnt<LPW * (NS - 2)>();
                     wait_lgkmcnt0();               // own reads of slice kt done before anyone overwrites it
                     raw_barrier();
@@ -336,8 +380,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                 widen(cur);
                 if (live) mma_half(cur, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                if (c + 1 < NC) read_frag(nxt, stage_a(S), stage_b(S), c + 1);
-                else read_frag(nxt, stage_a(SN{}), stage_b(SN{}), 0);
+                if (c + 1 < NC) read_frag(nxt, stage_a(S), stage_b(S), stage_s(S), c + 1);
+                else read_frag(nxt, stage_a(SN{}), stage_b(SN{}), stage_s(SN{}), 0);
                 __builtin_amdgcn_sched_barrier(0);
                 if (live) mma_half(cur, 1);
                 __builtin_amdgcn_sched_barrier(0);
@@ -588,13 +632,19 @@ void gemm_dma_workspace_need(const MatmulArgs &m, const GemmPlan &p, size_t *par
 bool gemm_dma_supported(const MatmulArgs &m) {
     // Every 16-byte copy of a B row must start on a 16-byte boundary and hold
     // whole elements of one row: N a multiple of 4 (f32), 8 (f16), 16 (int8),
-    // 32 (int4).
+    // 32 (int4).  Q8_K needs 32-element blocks that tile each row (N a
+    // multiple of 32), so that element (k, n) has the scale (k * N + n) / 32
+    // = k * (N / 32) + n / 32.
     int nmul = 0;
     switch (m.fmt) {
         case TML_FMT_F32: nmul = 4; break;
         case TML_FMT_F16: nmul = 8; break;
         case TML_FMT_Q8_0: nmul = 16; break;
         case TML_FMT_Q4_0: nmul = 32; break;
+        case TML_FMT_Q8_K:
+            if (m.block != 32 || m.scales == nullptr) return false;
+            nmul = 32;
+            break;
         default: return false;
     }
     return m.K % 4 == 0 && m.N % nmul == 0 && ((uintptr_t)m.A % 16) == 0 && ((uintptr_t)m.B % 16) == 0;
@@ -602,7 +652,7 @@ bool gemm_dma_supported(const MatmulArgs &m) {
 
 Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspace &ws, hipStream_t s) {
     if (!gemm_dma_supported(m))
-        return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM needs f32/f16/Q8_0/Q4_0 B, K % 4 == 0, 16-byte rows, aligned");
+        return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM needs f32/f16/Q8_0/Q8_K/Q4_0 B, K % 4 == 0, 16-byte rows, aligned");
     const int cfg = p.cfg;
     if (cfg < 0 || cfg >= gemm_dma_num_cfgs()) return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
     DmaArgs a;
@@ -623,6 +673,8 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
     a.act = m.act;
     a.res = m.res;
     a.colscale = m.colscale;
+    a.kscales = m.fmt == TML_FMT_Q8_K ? m.scales : nullptr;
+    a.sld = (int)(m.N / 32);
     a.tail0 = tml_act_tail0((long long)m.M * m.N);
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
     if (p.nsplit > 1) {
@@ -642,6 +694,7 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
         case TML_FMT_F32: st = launch_dma_cfg<TML_FMT_F32>(cfg, grid, a, s); break;
         case TML_FMT_F16: st = launch_dma_cfg<TML_FMT_F16>(cfg, grid, a, s); break;
         case TML_FMT_Q8_0: st = launch_dma_cfg<TML_FMT_Q8_0>(cfg, grid, a, s); break;
+        case TML_FMT_Q8_K: st = launch_dma_cfg<TML_FMT_Q8_K>(cfg, grid, a, s); break;
         default: st = launch_dma_cfg<TML_FMT_Q4_0>(cfg, grid, a, s); break;
     }
     TML_TRY(st);
