@@ -263,6 +263,7 @@ def main():
         result["qgemm"] = bench_qgemm(torch, dev, sptr, timer, _abi, synth, np)
         result["config1"] = bench_config1(torch, dev, sptr, timer, _abi, synth, np)
         result["config5"] = bench_config5(torch, dev, sptr, _abi)
+        result["sentence_transformer"] = bench_sentence_transformer(torch, dev, sptr, timer, _abi, synth)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
@@ -425,6 +426,54 @@ def bench_config1(torch, dev, sptr, timer, _abi, synth, np):
     tf = 2.0 * 1500 * 1536 * 384 / ms / 1e9
     log(f"config1: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
     return {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+
+
+def bench_sentence_transformer(torch, dev, sptr, timer, _abi, synth, tokens: int = 512, layers: int = 6):
+    """The sentence-transformer encoder's linears (src/models/sentence_transformer/model.zig:40-46:
+    hidden 384, intermediate 1536, 6 layers) over `tokens` tokens: per layer
+    Q, K, V, O [384x384], FFN up [384x1536] and down [1536x384], each layer
+    with its own weights, in fp32, F16 and Q8_K (the formats its .tl files
+    carry; quantized / converted on the device by the reference's
+    quantizers).  One sweep = 6 layers x 6 GEMMs, 20 sweeps per graph replay."""
+    d, ff, M = 384, 1536, tokens
+    shapes = [(d, d)] * 4 + [(d, ff), (ff, d)]
+    flops = layers * sum(2.0 * M * K * N for (K, N) in shapes)
+    x = torch.from_numpy(synth.normal_matrix(1001, M, d)).to(dev)
+    h = torch.from_numpy(synth.normal_matrix(1002, M, ff)).to(dev)
+    y = torch.empty((M, ff), dtype=torch.float32, device=dev)
+    res = {}
+    for fmt, name in ((_abi.FMT_F32, "fp32"), (_abi.FMT_F16, "f16"), (_abi.FMT_Q8_K, "q8_k")):
+        keep, row = [], []
+        for layer in range(layers):
+            for i, (K, N) in enumerate(shapes):
+                w = torch.from_numpy(synth.normal_matrix(2002 + 8 * layer + i, K, N, 0.02)).to(dev)
+                if fmt == _abi.FMT_F32:
+                    keep.append(w)
+                    row.append((K, N, w.data_ptr(), None))
+                    continue
+                b = torch.empty(K * N * (2 if fmt == _abi.FMT_F16 else 1), dtype=torch.uint8, device=dev)
+                sc = torch.empty(max(K * N // 32, 1), dtype=torch.float32, device=dev)
+                _abi.quantize_dev(fmt, K * N, w.data_ptr(), b.data_ptr(), sc.data_ptr(), sptr)
+                keep += [b, sc]
+                row.append((K, N, b.data_ptr(), sc.data_ptr() if fmt == _abi.FMT_Q8_K else None))
+        torch.cuda.synchronize()
+
+        def sweep(st, row=row, fmt=fmt):
+            for (K, N, bp, sp_) in row:
+                a = x if K == d else h
+                _abi.gemm_dev(fmt, M, N, K, a.data_ptr(), bp, y.data_ptr(), scales_ptr=sp_, stream=st)
+
+        ms = timer.time_ms(lambda st: [sweep(st) for _ in range(20)], 3, per_replay=20)
+        tf = flops / ms / 1e9
+        res[name] = {"us_per_sweep": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2),
+                     "frac": round(tf / FP32_PEAK_TFLOPS, 4)}
+        log(f"sentence-transformer {name}: {tokens} tokens x {layers} layers, {ms * 1e3:.1f} us/sweep, "
+            f"{tf:.1f} TFLOP/s")
+        del keep
+    res["tokens"] = tokens
+    res["layers"] = layers
+    res["flops_per_sweep"] = flops
+    return res
 
 
 def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
