@@ -83,17 +83,33 @@ template <> struct TElems<TML_FMT_F16> { static constexpr int value = 8; };
 __device__ __forceinline__ float tsext8(uint32_t word, int byte) {
     return (float)((int32_t)(word << (24 - 8 * byte)) >> 24);
 }
-__device__ __forceinline__ float tsext4(uint32_t word, int nib) {
-    return (float)((int32_t)(word << (28 - 4 * nib)) >> 28);
+
+// 16 times the signed nibble `nib` of a word: the nibble moved to the top
+// of its own byte (even nibbles shifted up by 4, odd ones in place) and that
+// byte read as a signed byte -- one masked word per parity shared by four
+// nibbles, then one byte-select convert each (v_cvt_f32_i32 with an SDWA
+// sign-extended byte operand), where extracting the nibble itself costs a
+// bit-field extract more per element.
+__device__ __forceinline__ float tsext4x16(uint32_t word, int nib) {
+    const uint32_t t = (nib & 1) ? (word & 0xF0F0F0F0u) : ((word << 4) & 0xF0F0F0F0u);
+    return (float)(int8_t)(t >> (8 * (nib >> 1)));
 }
 
-template <int FMT>
+// Element i of a prepared chunk.  With X16, Q4_0 elements come back 16 times
+// their value (tsext4x16) and the kernel's alpha carries the 1/16: scaling by
+// a power of two is exact, so every product and partial sum is exactly 16
+// times the unscaled one and the result is the same bit for bit.  (The
+// direct kernel uses it; in the LDS-staged kernel it measured slower at
+// M = 4: 7.56 against 6.47 us at 1280x5120.)
+template <int FMT, bool X16 = false>
 __device__ __forceinline__ float telem(const uintx4 &w, int i) {
     if constexpr (FMT == TML_FMT_F32) return __uint_as_float(w[i]);
     else if constexpr (FMT == TML_FMT_F16) return tml_half_bits(w[i / 2] >> (16 * (i % 2)));
     else if constexpr (FMT == TML_FMT_Q8_0) return tsext8(w[i / 4], i % 4);
-    else return tsext4(w[i / 8], i % 8);
+    else if constexpr (X16) return tsext4x16(w[i / 8], i % 8);
+    else return (float)((int32_t)(w[i / 8] << (28 - 4 * (i % 8))) >> 28);
 }
+template <int FMT> constexpr float telem_x16_alpha() { return FMT == TML_FMT_Q4_0 ? 0.0625f : 1.0f; }
 
 constexpr int tlog2(int v) { return v <= 1 ? 0 : 1 + tlog2(v / 2); }
 
@@ -191,7 +207,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
             for (int c = 0; c < CW; ++c) {
                 float wv[E];
 #pragma unroll
-                for (int e = 0; e < E; ++e) wv[e] = telem<FMT>(w[c][j], e);
+                for (int e = 0; e < E; ++e) wv[e] = telem<FMT, true>(w[c][j], e);
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
                     float s0 = 0.0f, s1 = 0.0f;  // two chains halve the add latency
@@ -471,7 +487,9 @@ TPlan plan_t(int fmt, int64_t M, int64_t N, int64_t nchunk, int cus) {
 }
 
 template <int FMT, int MR, int LK, int CW, int JB>
-void launch_t4(const GemvTArgs &ka, unsigned grid, bool xvec, hipStream_t s) {
+void launch_t4(const GemvTArgs &ka_in, unsigned grid, bool xvec, hipStream_t s) {
+    GemvTArgs ka = ka_in;
+    ka.alpha *= telem_x16_alpha<FMT>();  // the direct kernel widens Q4_0 to 16x its values
     if (xvec) gemv_t_kernel<FMT, MR, LK, CW, JB, true><<<dim3(grid), dim3(kThreads), 0, s>>>(ka);
     else gemv_t_kernel<FMT, MR, LK, CW, JB, false><<<dim3(grid), dim3(kThreads), 0, s>>>(ka);
 }
