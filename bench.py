@@ -377,6 +377,29 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
         torch.cuda.empty_cache()
         return res
 
+    def copy_floor(nbytes):
+        # Context for the decoder shapes: torch's own device copy moving
+        # 2 * nbytes per launch (nbytes read, nbytes written), rotating over
+        # >= 1 GB like the GEMVs.  A launch that moves a few MB costs this
+        # much on MI355X whatever it computes.
+        ncopy = min(256, max(2, rot_bytes // nbytes))
+        src = torch.empty((ncopy, nbytes), dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+
+        def fn(st):
+            for i in range(ncopy):
+                dst[i].copy_(src[i])
+
+        ms = timer.time_ms(fn, 3, per_replay=ncopy)
+        gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+        log(f"copy floor {nbytes >> 20} MiB -> {nbytes >> 20} MiB: {ms * 1e3:.2f} us, {gbs:.0f} GB/s moved")
+        del src, dst
+        torch.cuda.empty_cache()
+        return {"bytes_moved": 2 * nbytes, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    out["torch_copy_floor"] = {"2MiB": copy_floor(2 << 20), "4MiB": copy_floor(4 << 20),
+                               "32MiB": copy_floor(32 << 20)}
     out["q8_1024x4096"] = run(_abi.FMT_Q8_0, 1024, 4096, [1, 8], 2002, "q8 1024x4096")
     out["q4_1280x5120"] = run(_abi.FMT_Q4_0, 1280, 5120, [1, 4, 8], 2002, "q4 1280x5120")
     out["q4_5120x1280"] = run(_abi.FMT_Q4_0, 5120, 1280, [1, 4, 8], 2003, "q4 5120x1280")

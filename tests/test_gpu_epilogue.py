@@ -100,7 +100,7 @@ def test_fused_gelu_split_reduce(orc, forced_env, split, act):
     # kernel applies bias and activation (its 4-wide path); split 1 takes
     # the GEMM's own epilogue.
     forced_env["TML_GEMM_SPLIT"] = str(split)
-    for tile in ("1", "4", "7"):
+    for tile in ("1", "4", "7", "10"):
         forced_env["TML_GEMM_DMA_TILE"] = tile
         for (m, n, k) in [(129, 68, 1028), (300, 260, 516)]:
             a, w = rnd(611, m, k), rnd(612, k, n, 0.03)

@@ -89,15 +89,25 @@ template <> struct BBytes<TML_FMT_Q8_0> { static constexpr int num = 1, den = 1;
 template <> struct BBytes<TML_FMT_Q8_K> { static constexpr int num = 1, den = 1; };
 template <> struct BBytes<TML_FMT_Q4_0> { static constexpr int num = 1, den = 2; };
 
-template <int FMT, int BM, int BN, int BK, int WM, int WN, int NW, int NS>
+// KW: wave groups splitting each slice's depth.  With KW = 2 the waves
+// [0, NW/2) multiply the first half of every BK slice and [NW/2, NW) the
+// second half, each wave on the same WM x WN sub-tile as its partner; the two
+// accumulators are added through LDS before the epilogue.  Twice the waves
+// per SIMD for the same tile, so one wave's LDS and barrier waits are covered
+// by the other's MFMAs.
+template <int FMT, int BM, int BN, int BK, int WM, int WN, int NW, int NS, int KW = 1>
 __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     static_assert(NS == 3 || NS == 4, "3 or 4 LDS stages");
     static_assert(BK == 32 || BK == 64, "slice depth");
+    static_assert(KW == 1 || KW == 2, "one or two wave groups along K");
     constexpr int NC = BK / 16;
+    constexpr int NCW = NC / KW;  // chunks of a slice multiplied by one wave
+    constexpr int NWS = NW / KW;  // waves per group (one per sub-tile)
     constexpr int WAVES_N = BN / WN;
     constexpr int TM = WM / 16, TN = WN / 16;
-    static_assert((BM / WM) * (BN / WN) == NW, "one wave per WM x WN sub-tile");
-    static_assert(NC % 2 == 0, "fragment double-buffering alternates two buffers over the chunks");
+    static_assert((BM / WM) * (BN / WN) == NWS, "one wave of each group per WM x WN sub-tile");
+    static_assert(NCW % 2 == 0, "fragment double-buffering alternates two buffers over a wave's chunks");
+    static_assert(KW == 1 || BN <= BK, "the groups' accumulators are exchanged through one A stage");
     // 1 KiB copy blocks per stage and their shapes.
     constexpr int SLOTS_A = BK / 4;             // 16-byte slots per A row (8 or 16)
     constexpr int ROWS_A = 64 / SLOTS_A;        // A rows per copy block (8 or 4)
@@ -137,8 +147,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm0 = (wave / WAVES_N) * WM;
-    const int wn0 = (wave % WAVES_N) * WN;
+    const int kg = wave / NWS;        // wave group: chunks [kg * NCW, (kg + 1) * NCW) of each slice
+    const int sw = wave % NWS;        // sub-tile of the wave
+    const int wm0 = (sw / WAVES_N) * WM;
+    const int wn0 = (sw % WAVES_N) * WN;
+    const int c0 = kg * NCW;
 
     // Workgroup -> (tile, split).  Workgroups are dispatched to the 8 XCDs
     // round robin (id % 8), each XCD with its own L2.
@@ -347,7 +360,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         else if (scale_wave) wait_vmcnt<LPW_S * (NS - 2)>();
         else wait_vmcnt<LPW * (NS - 2)>();
         raw_barrier();                  // everyone's copies of slice 0 landed
-        read_frag(f[0], As0, Bs0, Ss0, 0);
+        read_frag(f[0], As0, Bs0, Ss0, c0);
 
         // One slice: stage S holds slice kt; stage S-1 (mod NS, slice kt-1,
         // fully read before the previous barrier) receives slice kt+NS-1.
@@ -365,10 +378,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
             // to LDS are in flight the compiler can only wait for LDS reads
             // with lgkmcnt(0), so the next wait must find nothing recent.
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
+            for (int c = 0; c < NCW; ++c) {
                 Frag &cur = f[c % 2];
                 Frag &nxt = f[(c + 1) % 2];
-                if (c + 1 == NC) {
+                if (c + 1 == NCW) {
                     // own copies of slice kt+1 landed
                     if (extra_b) wait_vmcnt<LPW_HI * (NS - 2)>();
                     else if (scale_wave) wait_vmcnt<LPW_S * (NS - 2)>();
@@ -380,8 +393,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                 widen(cur);
                 if (live) mma_half(cur, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                if (c + 1 < NC) read_frag(nxt, stage_a(S), stage_b(S), stage_s(S), c + 1);
-                else read_frag(nxt, stage_a(SN{}), stage_b(SN{}), stage_s(SN{}), 0);
+                if (c + 1 < NCW) read_frag(nxt, stage_a(S), stage_b(S), stage_s(S), c0 + c + 1);
+                else read_frag(nxt, stage_a(SN{}), stage_b(SN{}), stage_s(SN{}), c0);
                 __builtin_amdgcn_sched_barrier(0);
                 if (live) mma_half(cur, 1);
                 __builtin_amdgcn_sched_barrier(0);
@@ -394,6 +407,32 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
             if constexpr (NS > 3) step(kt + 3, S3{});
         }
         wait_vmcnt<0>();  // no copy may still be landing when the waves retire
+    }
+
+    if constexpr (KW > 1) {
+        // Group 1 hands its accumulators to group 0 through A stage 0: every
+        // wave's copies have landed (vmcnt(0) above) and its reads are done
+        // before the barrier, so nobody touches the stages any more.
+        float *xb = As0 + sw * (TM * TN * 4 * 64) + lane;
+        wait_lgkmcnt0();
+        raw_barrier();
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) xb[((i * TN + j) * 4 + r) * 64] = acc[i][j][r];
+        }
+        wait_lgkmcnt0();
+        raw_barrier();
+        if (kg != 0) return;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][j][r] += xb[((i * TN + j) * 4 + r) * 64];
     }
 
     const int rq = g * 4;
@@ -533,17 +572,21 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 }
 
 struct DmaCfg {
-    int bm, bn, bk;
+    int bm, bn, bk, kw;  // kw: wave groups along K (gemm_dma_kernel's KW)
 };
 // Tile configs (index = TML_GEMM_DMA_TILE - 1); see launch_gemm_f32_dma for
 // the wave tiling and LDS stages of each.
-constexpr DmaCfg kDmaCfgs[] = {{128, 128, 32}, {128, 64, 32}, {64, 64, 32}, {256, 128, 32},
-                               {128, 64, 64},  {64, 64, 64},  {32, 64, 32}, {32, 64, 64},
-                               {96, 32, 32}};
+constexpr DmaCfg kDmaCfgs[] = {{128, 128, 32, 1}, {128, 64, 32, 1}, {64, 64, 32, 1}, {256, 128, 32, 1},
+                               {128, 64, 64, 1},  {64, 64, 64, 1},  {32, 64, 32, 1}, {32, 64, 64, 1},
+                               {96, 32, 32, 1},   {32, 64, 64, 2}};
 
 }  // namespace
 
 int gemm_dma_num_cfgs() { return (int)(sizeof(kDmaCfgs) / sizeof(kDmaCfgs[0])); }
+
+// Configs whose two wave groups add their accumulators in the workgroup
+// cannot take the fused split-K exchange (every thread stores its partial).
+bool gemm_dma_cfg_fusable(int cfg) { return cfg >= 0 && cfg < gemm_dma_num_cfgs() && kDmaCfgs[cfg].kw == 1; }
 
 bool gemm_dma_cfg_ok(int cfg, int fmt) {
     if (cfg < 0 || cfg >= gemm_dma_num_cfgs()) return false;
@@ -578,6 +621,7 @@ static Status launch_dma_cfg(int cfg, dim3 grid, const DmaArgs &a, hipStream_t s
         case 5: gemm_dma_kernel<FMT, 64, 64, 64, 32, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
         case 6: gemm_dma_kernel<FMT, 32, 64, 32, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
         case 7: gemm_dma_kernel<FMT, 32, 64, 64, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
+        case 9: gemm_dma_kernel<FMT, 32, 64, 64, 16, 32, 8, 3, 2><<<grid, 512, 0, s>>>(a); break;
         case 8:
             // 32 int4 columns are 16 bytes a k-row: less than a copy block's two slots
             if constexpr (FMT != TML_FMT_Q4_0) {
@@ -655,6 +699,8 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
         return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM needs f32/f16/Q8_0/Q8_K/Q4_0 B, K % 4 == 0, 16-byte rows, aligned");
     const int cfg = p.cfg;
     if (cfg < 0 || cfg >= gemm_dma_num_cfgs()) return Status::Err(TML_ERR_INVALID_ARG, "bad dma GEMM config");
+    if (p.fused && p.nsplit > 1 && !gemm_dma_cfg_fusable(cfg))
+        return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM config with two K wave groups has no fused split-K");
     DmaArgs a;
     a.M = (int)m.M; a.N = (int)m.N; a.K = (int)m.K;
     a.A = m.A; a.B = m.B; a.bias = m.bias; a.C = m.C;

@@ -444,15 +444,17 @@ int device_cus() {
 // with per 32-deep slice costs measured on MI355X (us, one / several per CU):
 // 128x128 2.05, 128x64 1.09, 64x64 0.61 / 0.56, 256x128 4.05,
 // 128x64 (BK 64) 1.21, 64x64 (BK 64) 0.62, 32x64 0.40 / 0.33,
-// 32x64 (BK 64) 0.38 / 0.35, 96x32 0.46 / 0.50 (no int4 variant; its three
+// 32x64 (BK 64) 0.38 / 0.35, 32x64 (BK 64, two wave groups along K) 0.368 /
+// 0.34, 96x32 0.46 / 0.50 (no int4 variant; its three
 // co-resident workgroups per CU share the matrix cores, so a slice of each
 // is charged in full: fitted on 1500x1536x384, where the 768 tiles are three
 // per CU exactly); t_fill (pipeline fill, epilogue, launch)
 // ~3.5 us; t_reduce (the second launch that sums the splits' partials)
 // ~3.6 us plus the partials' traffic, splits * M * N * 8 bytes at ~6 TB/s.
 void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
-    static const double t_one[] = {2.05, 1.09, 0.61, 4.05, 1.21, 0.62, 0.40, 0.38, 0.46};
-    static const double t_many[] = {2.05, 1.09, 0.56, 4.05, 1.21, 0.62, 0.33, 0.35, 0.50};
+    static const double t_one[] = {2.05, 1.09, 0.61, 4.05, 1.21, 0.62, 0.40, 0.38, 0.46, 0.368};
+    static const double t_many[] = {2.05, 1.09, 0.56, 4.05, 1.21, 0.62, 0.33, 0.35, 0.50, 0.34};
+    static_assert(sizeof(t_one) == sizeof(t_many), "one cost pair per tile config");
     static const int splits[] = {1, 2, 3, 4, 6, 8};
     constexpr double kFill = 3.5, kReduce = 3.6, kBytesPerUs = 6.0e6;
     const int cus = device_cus();
@@ -461,6 +463,7 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
     const int forced_split = env_int("TML_GEMM_SPLIT", 0);
     double best_t = 1e300;
     for (int c = 0; c < gemm_dma_num_cfgs(); ++c) {
+        if (c >= (int)(sizeof(t_one) / sizeof(t_one[0]))) break;  // no cost model for this config
         if ((forced_tile >= 0 && c != forced_tile) || !gemm_dma_cfg_ok(c, fmt)) continue;
         int bm = 0, bn = 0, bk = 32;
         gemm_dma_tile(c, &bm, &bn, &bk);
@@ -501,7 +504,7 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
     // split of a tile sums them); on MI355X that measured ~2 us slower per
     // headline step than the extra launch (the agent-scope round trip of the
     // last split costs more than a reduce kernel in a graph), so it is off.
-    p->fused = p->nsplit > 1 && env_int("TML_GEMM_FUSED", 0) != 0;
+    p->fused = p->nsplit > 1 && env_int("TML_GEMM_FUSED", 0) != 0 && gemm_dma_cfg_fusable(p->cfg);
 }
 
 bool aligned(const void *p, size_t n) { return ((uintptr_t)p % n) == 0; }

@@ -163,6 +163,7 @@ bool gemm_dma_supported(const MatmulArgs &a);
 int gemm_dma_num_cfgs();
 bool gemm_dma_cfg_ok(int cfg, int fmt);  // the tile config has a kernel for B format fmt
 void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk);
+bool gemm_dma_cfg_fusable(int cfg);  // the tile config can combine K splits in the kernel
 Status launch_gemm_f32_dma(const MatmulArgs &a, const GemmPlan &p, const Workspace &ws, hipStream_t s);
 void gemm_dma_workspace_need(const MatmulArgs &a, const GemmPlan &p, size_t *partial_floats, size_t *counters);
 Status launch_gemv(const MatmulArgs &a, const Workspace &ws, hipStream_t s);
