@@ -456,21 +456,26 @@ struct TPlan {
 //    one wave per group up to two waves' worth of chunks, else the whole
 //    workgroup, fewer rows per wave for M > 2; once the weight streams tens
 //    of MB (bandwidth-bound, e.g. a vocabulary projection), short rows
-//    (<= 48 chunks) go to 16-lane groups, which waste no lanes and reduce
-//    with DPP alone.
-//  * CW: the most outputs per group (<= 4) that still gives one workgroup
-//    per CU, with CW * MR <= 16 dot products per lane.
+//    (<= 96 chunks) go to 16-lane groups, which waste no lanes and reduce
+//    with DPP alone (the 80-chunk Q8_0 vocabulary rows would leave 48 of
+//    the 128 lane slots of two 64-lane batches idle).
+//  * CW: two outputs per group (four for long rows of weights streaming
+//    tens of MB), fewer if that leaves a CU without a workgroup, with
+//    CW * MR <= 16 dot products per lane.  At decoder sizes two beat four
+//    by 2-11 % (e.g. Q4_0 1280x5120 M = 1: 3.99 against 4.34 us, F16 M = 8:
+//    9.06 against 10.32 us) and one, by 2-35 %.
 //  * JB = 1: one chunk per lane per batch; the batch loop keeps two in
 //    flight (larger batches cost registers and occupancy).
 TPlan plan_t(int fmt, int64_t M, int64_t N, int64_t nchunk, int cus) {
     TPlan p;
     const int mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
     const double weight_bytes = (double)N * (double)nchunk * 16.0;
-    if (weight_bytes > 32.0e6 && nchunk <= 48) p.lk = 16;
+    const bool big = weight_bytes > 32.0e6;
+    if (big && nchunk <= 96) p.lk = 16;
     else if (nchunk <= 128 || mr > 2) p.lk = 64;
     else p.lk = 256;
     const int groups = kThreads / p.lk;
-    p.cw = 4;
+    p.cw = (big && p.lk != 16) ? 4 : 2;
     while (p.cw > 1 && (N + (int64_t)groups * p.cw - 1) / ((int64_t)groups * p.cw) < cus) p.cw /= 2;
     while (p.cw > 1 && p.cw * mr > 16) p.cw /= 2;
     p.jb = 1;
@@ -631,8 +636,10 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     const bool use_lds = mr * t_elems(fmt) > 64 || lds_mode == 1 ||
                          (lds_mode < 0 && ((fmt == TML_FMT_Q4_0 && mr == 2) || (fmt == TML_FMT_F16 && mr == 8)));
     if (use_lds) {
-        // CW outputs per wave: the most (<= 4) that still gives a workgroup per CU
-        int cw = 4;
+        // CW outputs per wave: two (four for Q4_0 at M = 3-4: 6.53 against
+        // 7.51 us at 1280x5120; two elsewhere, e.g. Q8_0 M = 8: 5.73 against
+        // 6.11 us), fewer if that leaves a CU without a workgroup
+        int cw = (fmt == TML_FMT_Q4_0 && mr == 4) ? 4 : 2;
         while (cw > 1 && (N + 4LL * cw - 1) / (4LL * cw) < cus) cw /= 2;
         const int forced_cw = env_int("TML_GEMVT_CW", 0);
         if (forced_cw == 1 || forced_cw == 2 || forced_cw == 4) cw = forced_cw;
