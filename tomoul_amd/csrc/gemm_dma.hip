@@ -61,6 +61,21 @@ struct DmaArgs {
 };
 
 #define TML_GPTR(p) ((__attribute__((address_space(1))) void *)(p))
+
+// Buffer resource word 3 for raw (untyped, unswizzled) loads on gfx9 parts:
+// DATA_FORMAT = 32 bits.  A lane offset at or past the resource's byte count
+// reads zeros; kBufOutOfRange is such an offset for every resource here.
+constexpr int kBufDword3 = 0x00020000;
+constexpr unsigned kBufOutOfRange = 0x80000000u;
+
+// 16 bytes at base + off (a buffer of nbytes) into this lane's slot of the
+// 1 KiB LDS block at lds.  The resource is built from uniform values, so it
+// lives in SGPRs and the compiler keeps it out of the loop.
+__device__ __forceinline__ void buffer_copy16(const void *base, unsigned nbytes, unsigned off, void *lds) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0,
+                                                                       (int)nbytes, kBufDword3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, 0);
+}
 #define TML_LPTR(p) ((__attribute__((address_space(3))) void *)(p))
 
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
@@ -186,46 +201,51 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     const int m0 = tile_m * BM;
     const int n0 = tile_n * BN;
 
-    // ---- per-lane copy sources (fixed part), see the layout notes above
-    int a_row[BLKS_A / NW], a_col[BLKS_A / NW];
+    // ---- per-lane copy sources, see the layout notes above.  A and B are
+    // read through buffer resources (base + byte count in SGPRs) with a
+    // 32-bit per-lane byte offset fixed for the whole loop; each slice adds
+    // one uniform step to it (one v_add per copy).  The hardware returns
+    // zeros for offsets at or past the byte count, which covers A rows >= M
+    // and B k-rows >= K without a select.  The host keeps every offset
+    // below 2^31 (gemm_dma_supported).  Per-slice 64-bit address arithmetic
+    // and zero-block selects measured 2-5 us per headline GEMM.
+    const unsigned a_bytes = (unsigned)a.M * (unsigned)a.K * 4u, b_bytes = (unsigned)a.K * (unsigned)a.ldb;
+    unsigned a_off0[BLKS_A / NW];  // byte offset of the lane's A chunk at k0 = 0
+    int a_col[BLKS_A / NW];
 #pragma unroll
     for (int i = 0; i < BLKS_A / NW; ++i) {
         const int blk = wave + i * NW;
         const int row = blk * ROWS_A + lane / SLOTS_A;
         const int q = (lane % SLOTS_A) ^ (row % 8);
-        a_row[i] = m0 + row;
         a_col[i] = q * 4;
+        a_off0[i] = ((unsigned)(m0 + row) * (unsigned)a.K + (unsigned)a_col[i]) * 4u;
     }
     const bool extra_b = (BLKS_B % NW) != 0 && wave < BLKS_B % NW;
-    int b_row[BPW], b_colb[BPW];  // k-row in the slice, byte offset of the 16-byte chunk in the tile row
+    unsigned b_off0[BPW];  // byte offset of the lane's B chunk at k0 = 0
 #pragma unroll
     for (int i = 0; i < BPW; ++i) {
         const int blk = wave + i * NW;
         const int krow = blk * ROWS_B + lane / SLOTS_B;
         const int q = (lane % SLOTS_B) ^ (((krow >> 2) & 1) * XS);
-        b_row[i] = krow;
-        b_colb[i] = q * 16;
+        // columns past N (N is a whole number of 16-byte chunks) read bytes
+        // of the next k-row: they only feed outputs the epilogue drops
+        b_off0[i] = (unsigned)krow * (unsigned)a.ldb + (unsigned)(n0 * BNUM / BDEN) + (unsigned)(q * 16);
     }
-    const long long n0b = (long long)n0 * BNUM / BDEN;
     const bool scale_wave = KS && wave == NW - 1;
     auto issue = [&](float *as, float *bs, float *ss, int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BLKS_A / NW; ++i) {
-            const int gk = k0 + a_col[i];
-            const bool in = a_row[i] < a.M && gk < a.K;
-            const float *src = in ? a.A + (size_t)a_row[i] * a.K + gk : a.zero;
-            __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(as + (wave + i * NW) * 256), 16, 0, 0);
+            // k >= K inside a row would read the next row: point it past
+            // the end instead, so the padded product is 0 * 0, never 0 * inf
+            const unsigned off = a_col[i] < a.K - k0 ? a_off0[i] + (unsigned)k0 * 4u : kBufOutOfRange;
+            buffer_copy16(a.A, a_bytes, off, as + (wave + i * NW) * 256);
         }
+        const unsigned kstep = (unsigned)k0 * (unsigned)a.ldb;
 #pragma unroll
         for (int i = 0; i < BPW; ++i) {
             const int blk = wave + i * NW;
-            if (BLKS_B % NW == 0 || blk < BLKS_B) {  // uniform per wave
-                const int gk = k0 + b_row[i];
-                const bool in = gk < a.K && n0 + b_colb[i] * BDEN / BNUM < a.N;
-                const void *src = in ? (const void *)((const uint8_t *)a.B + (size_t)gk * a.ldb + n0b + b_colb[i])
-                                     : (const void *)a.zero;
-                __builtin_amdgcn_global_load_lds(TML_GPTR(src), TML_LPTR(bs + blk * 256), 16, 0, 0);
-            }
+            if (BLKS_B % NW == 0 || blk < BLKS_B)  // uniform per wave
+                buffer_copy16(a.B, b_bytes, b_off0[i] + kstep, bs + blk * 256);
         }
         if constexpr (KS) {
             if (scale_wave) {
@@ -691,6 +711,13 @@ bool gemm_dma_supported(const MatmulArgs &m) {
             break;
         default: return false;
     }
+    // The copies address A and B with 32-bit byte offsets below 2^31
+    // (buffer resources, see gemm_dma_kernel): the largest offset a tile
+    // can form is below (M + 256) * K * 4 for A and (K + 64) * (bytes per B
+    // row) for B.
+    const uint64_t lim = (uint64_t)1 << 31;
+    if ((uint64_t)(m.M + 256) * (uint64_t)m.K * 4u >= lim || (uint64_t)(m.K + 64) * weight_row_bytes(m.fmt, m.N) >= lim)
+        return false;
     return m.K % 4 == 0 && m.N % nmul == 0 && ((uintptr_t)m.A % 16) == 0 && ((uintptr_t)m.B % 16) == 0;
 }
 

@@ -441,19 +441,22 @@ int device_cus() {
 // and each costs t_many.  So
 //   t = ceil(units / CUs) * slices_per_split * (BK / 32) * t_slice(tile, one / many)
 //       + t_fill + (splits > 1 ? t_reduce : 0)
-// with per 32-deep slice costs measured on MI355X (us, one / several per CU):
-// 128x128 2.05, 128x64 1.09, 64x64 0.61 / 0.56, 256x128 4.05,
-// 128x64 (BK 64) 1.21, 64x64 (BK 64) 0.62, 32x64 0.40 / 0.33,
-// 32x64 (BK 64) 0.38 / 0.35, 32x64 (BK 64, two wave groups along K) 0.368 /
-// 0.34, 96x32 0.46 / 0.50 (no int4 variant; its three
-// co-resident workgroups per CU share the matrix cores, so a slice of each
-// is charged in full: fitted on 1500x1536x384, where the 768 tiles are three
-// per CU exactly); t_fill (pipeline fill, epilogue, launch)
-// ~3.5 us; t_reduce (the second launch that sums the splits' partials)
-// ~3.6 us plus the partials' traffic, splits * M * N * 8 bytes at ~6 TB/s.
+// with t_fill (pipeline fill, epilogue, launch) ~3.5 us and t_reduce (the
+// second launch that sums the splits' partials) ~3.6 us plus the partials'
+// traffic, splits * M * N * 8 bytes at ~6 TB/s.  The per 32-deep slice costs
+// (us, one / several per CU) were fitted on MI355X to a sweep of every tile
+// x split (1, 2, 4 over twelve shapes -- the XLM-R layer, the Whisper
+// large-v3-turbo and tiny encoder linears, the sentence-transformer
+// linears, 128x4096x1024 -- and 3, 6, 8 over the six that split) so that
+// the model's pick is the measured best on eleven of them and 0.4 us off on
+// the twelfth: 128x128 1.975 / 1.998, 128x64 0.974 / 0.854, 64x64 0.528 /
+// 0.504, 256x128 4.05 (not refitted: it spills), 128x64 (BK 64) 1.06 /
+// 1.147, 64x64 (BK 64) 0.54 / 0.672, 32x64 0.308 / 0.24, 32x64 (BK 64)
+// 0.308 / 0.293, 96x32 0.354 / 0.383 (no int4 variant), 32x64 (BK 64, two
+// wave groups along K) 0.226 / 0.282.
 void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
-    static const double t_one[] = {2.05, 1.09, 0.61, 4.05, 1.21, 0.62, 0.40, 0.38, 0.46, 0.368};
-    static const double t_many[] = {2.05, 1.09, 0.56, 4.05, 1.21, 0.62, 0.33, 0.35, 0.50, 0.34};
+    static const double t_one[] = {1.975, 0.974, 0.528, 4.05, 1.06, 0.54, 0.308, 0.308, 0.354, 0.226};
+    static const double t_many[] = {1.998, 0.854, 0.504, 4.05, 1.147, 0.672, 0.24, 0.293, 0.383, 0.282};
     static_assert(sizeof(t_one) == sizeof(t_many), "one cost pair per tile config");
     static const int splits[] = {1, 2, 3, 4, 6, 8};
     constexpr double kFill = 3.5, kReduce = 3.6, kBytesPerUs = 6.0e6;
