@@ -580,6 +580,42 @@ def test_prepared_plan_variants(orc, lk, cw, jb):
                 os.environ[key] = v
 
 
+@pytest.mark.parametrize("lk", [16, 64, 256])
+@pytest.mark.parametrize("cw", [1, 2, 4])
+@pytest.mark.parametrize("jb", [1, 2])
+def test_prepared_buffer_loads(orc, lk, cw, jb):
+    # K a whole number of chunks takes the buffer-resource loads (chunks past
+    # the row read unchecked and their sums are dropped); they must give the
+    # checked loads' result bit for bit, with partial last batches (40, 80,
+    # 320 chunks over 16-, 64- and 256-lane groups), several superchunks
+    # (K = 3072: 3 of int8) and an inf in the activation row after row 0,
+    # which the dropped sums of row 0 must not pick up.
+    keys = ("TML_GEMVT_LK", "TML_GEMVT_CW", "TML_GEMVT_JB", "TML_GEMVT_BUF")
+    saved = {key: os.environ.get(key) for key in keys}
+    os.environ.update({"TML_GEMVT_LK": str(lk), "TML_GEMVT_CW": str(cw), "TML_GEMVT_JB": str(jb)})
+    try:
+        for (k, n) in [(1280, 200), (3072, 72)]:
+            w = rnd(191, k, n, 0.02)
+            for m in (1, 2):
+                a = rnd(192 + m, m, k)
+                if m == 2:
+                    a[1, :7] = np.inf
+                for fmt, b, scale, ref, tol in _prepared_cases(orc, w, k, n, a):
+                    got = {}
+                    for buf in ("1", "0"):
+                        os.environ["TML_GEMVT_BUF"] = buf
+                        got[buf] = _run_prepared(fmt, b, scale, k, n, m, a)
+                    np.testing.assert_array_equal(got["1"], got["0"])
+                    assert np.all(np.isfinite(got["1"][0])), (fmt, k, m)
+                    assert rel_err(got["1"][:1], ref[:1]) <= tol, (fmt, k, m)
+    finally:
+        for key, v in saved.items():
+            if v is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = v
+
+
 @pytest.mark.parametrize("cw", [1, 2, 4])
 def test_prepared_lds_kernel(orc, cw):
     # The LDS-staged prepared kernel (forced for every row count and format)
