@@ -503,7 +503,8 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
     """Decoder GEMVs for kernel traces / counters: Q8_0 1024x4096 at M = 1
     and 8, Q4_0 1280x5120 and 5120x1280 at M = 1 and 4, each on its prepared
     copy and in the [K,N] layout, `launches` times over 16 distinct weight
-    copies (eager launches, one kernel per call)."""
+    copies (eager launches, one kernel per call); then the Q8_0 and Q4_0
+    vocabulary projections (1280 x 51866, M = 1) on 3 / 4 prepared copies."""
     for fmt, K, N, M in ((_abi.FMT_Q8_0, 1024, 4096, 1), (_abi.FMT_Q8_0, 1024, 4096, 8),
                          (_abi.FMT_Q4_0, 1280, 5120, 1), (_abi.FMT_Q4_0, 1280, 5120, 4),
                          (_abi.FMT_Q4_0, 5120, 1280, 1), (_abi.FMT_Q4_0, 5120, 1280, 4)):
@@ -527,6 +528,28 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
         for h_ in hs:
             _abi.prepared_free(h_)
         log(f"profile-gemv: fmt {fmt} {K}x{N}: {launches} prepared + {launches} [K,N] launches")
+    # the vocabulary projection (1280 x 51866) at M = 1 on prepared copies
+    for fmt, ncopy in ((_abi.FMT_Q8_0, 3), (_abi.FMT_Q4_0, 4)):
+        K, N = 1280, 51866
+        w = torch.from_numpy(synth.normal_matrix(2004, K, N, 0.02)).to(dev)
+        nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+        q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        sc = torch.empty(1, dtype=torch.float32, device=dev)
+        _abi.quantize_dev(fmt, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
+        torch.cuda.synchronize()
+        copies = q.repeat(ncopy).view(ncopy, nbytes)
+        del w
+        hs = [_abi.prepare_dev(fmt, K, N, copies[i].data_ptr(), float(sc.item()), sptr) for i in range(ncopy)]
+        x = torch.from_numpy(synth.normal_matrix(1001, 1, K)).to(dev)
+        y = torch.empty((1, N), dtype=torch.float32, device=dev)
+        for i in range(launches):
+            _abi.gemm_prepared(hs[i % ncopy], 1, x.data_ptr(), y.data_ptr(), stream=sptr)
+        torch.cuda.synchronize()
+        for h_ in hs:
+            _abi.prepared_free(h_)
+        del copies
+        torch.cuda.empty_cache()
+        log(f"profile-gemv: fmt {fmt} vocab {K}x{N}: {launches} prepared launches")
     print(json.dumps({"profile_gemv": True}), flush=True)
 
 
