@@ -54,7 +54,26 @@ struct GemmKArgs {
     int act;             // TML_ACT_* after the bias
     const float *res;    // [M,N] residual added after the bias, or nullptr
     long long tail0;     // tml_act_tail0(M * N)
+    unsigned a_bytes = 0, b_bytes = 0;  // M*K*4 and the bytes of B: buffer-resource sizes (vector path)
 };
+
+// Vector-path loads go through buffer resources: the base and byte count
+// are uniform (SGPRs), the lane's byte offset is one 32-bit VGPR, and
+// offsets at or past the byte count read zeros.  This replaces a 64-bit
+// address and a zero-block select per load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, unsigned nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)nbytes, 0x00020000);
+}
+__device__ __forceinline__ uintx4 buf_load_b128(const void *base, unsigned nbytes, unsigned off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(buf_rsrc(base, nbytes), off, 0, 0);
+}
+__device__ __forceinline__ uintx2 buf_load_b64(const void *base, unsigned nbytes, unsigned off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(base, nbytes), off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load_b32(const void *base, unsigned nbytes, unsigned off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(base, nbytes), off, 0, 0);
+}
+constexpr unsigned kBufOutOfRange = 0x80000000u;
 
 // ---------------------------------------------------------------- B formats
 // Elements of B moved per global load ("chunk") in the vector path.
@@ -79,11 +98,27 @@ __device__ __forceinline__ float sext4(uint32_t word, int nib) {
     return (float)((int32_t)(word << (28 - 4 * nib)) >> 28);
 }
 
-// Vector-path chunk load at (k, n); n % EPC == 0.  Branch-free: an out-of-
-// range chunk reads the zero block (its address is selected, not its value), so the
-// compiler keeps every load of a slice in flight together.
+// Vector-path chunk load at (k, n); n % EPC == 0.  Branch-free, so the
+// compiler keeps every load of a slice in flight together.  Through the
+// buffer resource (all formats but Q8_K): k >= K lies past the end of B and
+// reads zeros; a chunk at n >= N reads bytes of the next k-row, which only
+// feed output columns the epilogue drops.  Q8_K (whose block-scale lookup
+// must stay inside the scales) selects the zero block instead.
 template <int FMT>
 __device__ __forceinline__ void load_b_vec(const GemmKArgs &a, int k, int n, BRaw &r) {
+    if constexpr (FMT != TML_FMT_Q8_K) {
+        const unsigned e = (unsigned)k * (unsigned)a.N + (unsigned)n;  // element index
+        if constexpr (FMT == TML_FMT_F32 || FMT == TML_FMT_F16) {
+            const uintx4 v = buf_load_b128(a.B, a.b_bytes, e * (FMT == TML_FMT_F32 ? 4u : 2u));
+            r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3];
+        } else if constexpr (FMT == TML_FMT_Q8_0) {
+            const uintx2 v = buf_load_b64(a.B, a.b_bytes, e);
+            r.w[0] = v[0]; r.w[1] = v[1];
+        } else {  // Q4_0: 8 nibbles = 4 bytes starting at byte e/2 (e % 8 == 0)
+            r.w[0] = buf_load_b32(a.B, a.b_bytes, e / 2);
+        }
+        return;
+    }
     const bool in = (k < a.K) && (n < a.N);
     const size_t e = (size_t)(in ? k : 0) * a.N + (in ? n : 0);
     if constexpr (FMT == TML_FMT_F32 || FMT == TML_FMT_F16) {
@@ -204,9 +239,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_mfma_kernel(GemmKArgs a) {
                 const int row = c / (BK / 4), kq = (c % (BK / 4)) * 4;
                 const int gm = m0 + row, gk = k0 + kq;
                 if constexpr (VEC) {
-                    const bool in = gm < a.M && gk < a.K;
-                    st.a[i] = *(const floatx4 *)(in ? (const void *)(a.A + (size_t)gm * a.K + gk)
-                                                    : a.zero);
+                    // rows >= M lie past the end of A; k >= K inside a row
+                    // would read the next row, so it points past the end too
+                    const unsigned off = gk < a.K ? ((unsigned)gm * (unsigned)a.K + (unsigned)gk) * 4u : kBufOutOfRange;
+                    st.a[i] = __builtin_bit_cast(floatx4, buf_load_b128(a.A, a.a_bytes, off));
                 } else {
                     float t[4];
 #pragma unroll
@@ -526,6 +562,14 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
     const size_t bbytes = (FMT == TML_FMT_F32 || FMT == TML_FMT_F16) ? 16 : (FMT == TML_FMT_Q4_0 ? 4 : 8);
     bool vec = (m.K % 4 == 0) && aligned(m.A, 16) && (m.N % EPC == 0) && aligned(m.B, bbytes);
     if (FMT == TML_FMT_Q8_K) vec = vec && (m.block % 8 == 0);
+    // the vector path's buffer offsets stay below 2^31: rows up to M + 256
+    // of A, k-rows up to K + 64 of B
+    const uint64_t brow = (FMT == TML_FMT_F32) ? (uint64_t)m.N * 4 : (FMT == TML_FMT_F16) ? (uint64_t)m.N * 2
+                        : (FMT == TML_FMT_Q4_0) ? (uint64_t)m.N / 2 : (uint64_t)m.N;
+    const uint64_t lim = (uint64_t)1 << 31;
+    vec = vec && (uint64_t)(m.M + 256) * (uint64_t)m.K * 4u < lim && (uint64_t)(m.K + 64) * brow < lim;
+    ka.a_bytes = (unsigned)((uint64_t)m.M * (uint64_t)m.K * 4u);
+    ka.b_bytes = (unsigned)((uint64_t)m.K * brow);
     if (!vec) cfg = 3;  // the generic path is instantiated for one tile shape
     const int bm = kCfgs[cfg].bm, bn = kCfgs[cfg].bn;
     ka.tiles_m = (int)((m.M + bm - 1) / bm);
