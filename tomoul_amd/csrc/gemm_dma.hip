@@ -276,21 +276,35 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     int a_off[TM];            // float offset of the lane's A row (chunk added per read)
 #pragma unroll
     for (int i = 0; i < TM; ++i) a_off[i] = (wm0 + i * 16 + lrow) * BK;
-    int b_off[TN];            // swizzled byte offset of the lane's B element within a k-row
+    // Narrow B with an even number of 16-column fragments pairs them:
+    // fragments 2p and 2p + 1 take the even and odd columns of the wave's
+    // p-th 32-column group, so lane lrow feeds the adjacent columns
+    // wn0 + 32p + 2 lrow and + 1, which one LDS read returns (2 bytes of
+    // int8, 4 of f16, 1 of int4) instead of two.  The epilogue maps
+    // fragment j back to its columns (bcol).
+    constexpr bool PAIR = FMT != TML_FMT_F32 && TN % 2 == 0;
+    constexpr int NRD = PAIR ? TN / 2 : TN;  // B reads per (k, lane)
+    auto bcol = [&](int j) __attribute__((always_inline)) {
+        return PAIR ? wn0 + 32 * (j / 2) + 2 * lrow + (j % 2) : wn0 + j * 16 + lrow;
+    };
+    int b_off[NRD];           // swizzled byte offset of the lane's B element(s) within a k-row
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int nb = (wn0 + j * 16 + lrow) * BNUM / BDEN;
+    for (int j = 0; j < NRD; ++j) {
+        const int nb = (PAIR ? wn0 + 32 * j + 2 * lrow : wn0 + j * 16 + lrow) * BNUM / BDEN;
         b_off[j] = (((nb >> 4) ^ ((g & 1) * XS)) << 4) | (nb & 15);
     }
-    const int nib = (lrow & 1) * 4;  // int4: odd columns sit in the high nibble (N and n0 are even)
+    const int nib = (lrow & 1) * 4;  // int4 unpaired: odd columns sit in the high nibble (N and n0 are even)
     const int aswz = lrow & 7;
     auto read_frag = [&](Frag &f, const float *as, const float *bs, const float *ss, int chunk)
                          __attribute__((always_inline)) {
         const int q = chunk * 4 + g;
         if constexpr (KS) {
-            // fragment j's 16 columns lie in scale block (wn0 + j * 16) / 32
+            // fragment j's 16 columns lie in one scale block of 32
 #pragma unroll
-            for (int j = 0; j < TN; ++j) f.sc[j] = *(const floatx4 *)&ss[((wn0 + j * 16) / 32) * BK + chunk * 16 + g * 4];
+            for (int j = 0; j < TN; ++j) {
+                const int blk = (PAIR ? wn0 + 32 * (j / 2) : wn0 + j * 16) / 32;
+                f.sc[j] = *(const floatx4 *)&ss[blk * BK + chunk * 16 + g * 4];
+            }
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) f.a[i] = *(const floatx4 *)&as[a_off[i] + ((q ^ aswz) << 2)];
@@ -298,10 +312,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         for (int s = 0; s < 4; ++s) {
             const int k = chunk * 16 + g * 4 + s;
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
+            for (int j = 0; j < NRD; ++j) {
                 const uint8_t *bp = (const uint8_t *)bs + k * BNB + b_off[j];
                 if constexpr (FMT == TML_FMT_F32) f.b[j][s] = *(const float *)bp;
-                else if constexpr (FMT == TML_FMT_F16) f.braw[j][s] = *(const uint16_t *)bp;
+                else if constexpr (PAIR) {
+                    // both columns' raw bits; split in widen()
+                    if constexpr (FMT == TML_FMT_F16) f.braw[j][s] = *(const uint32_t *)bp;
+                    else if constexpr (FMT == TML_FMT_Q4_0) f.braw[j][s] = *bp;
+                    else f.braw[j][s] = *(const uint16_t *)bp;
+                } else if constexpr (FMT == TML_FMT_F16) f.braw[j][s] = *(const uint16_t *)bp;
                 else if constexpr (FMT == TML_FMT_Q8_0 || FMT == TML_FMT_Q8_K)
                     f.braw[j][s] = (uint32_t)(int32_t)*(const int8_t *)bp;
                 else f.braw[j][s] = *bp;
@@ -309,7 +328,32 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         }
     };
     auto widen = [&](Frag &f) __attribute__((always_inline)) {
-        if constexpr (FMT != TML_FMT_F32) {
+        if constexpr (PAIR) {
+#pragma unroll
+            for (int p = 0; p < NRD; ++p)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const uint32_t r = f.braw[p][s];
+                    float lo, hi;  // the even and the odd column
+                    if constexpr (FMT == TML_FMT_F16) {
+                        lo = tml_half_bits(r & 0xFFFFu);
+                        hi = tml_half_bits(r >> 16);
+                    } else if constexpr (FMT == TML_FMT_Q4_0) {
+                        lo = (float)((int32_t)(r << 28) >> 28);
+                        hi = (float)((int32_t)(r << 24) >> 28);
+                    } else {
+                        lo = (float)((int32_t)(r << 24) >> 24);
+                        hi = (float)((int32_t)(r << 16) >> 24);
+                    }
+                    if constexpr (FMT == TML_FMT_Q8_K) {
+                        // reference dequantization: f32(q) * scale, rounded per element
+                        lo *= f.sc[2 * p][s];
+                        hi *= f.sc[2 * p + 1][s];
+                    }
+                    f.b[2 * p][s] = lo;
+                    f.b[2 * p + 1][s] = hi;
+                }
+        } else if constexpr (FMT != TML_FMT_F32) {
 #pragma unroll
             for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -518,7 +562,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const int col = n0 + wn0 + j * 16 + lrow;
+                const int col = n0 + bcol(j);
                 if (col >= a.N) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -534,9 +578,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn0 + j * 16 + lrow;
+            const int col = n0 + bcol(j);
             if (col >= a.N) continue;
-            const float bcol = a.bias ? a.bias[col] : 0.0f;
+            const float biasc = a.bias ? a.bias[col] : 0.0f;
             const float acol = a.colscale ? a.alpha * a.colscale[col] : a.alpha;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -545,7 +589,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                     float *cp = a.C + (size_t)row * a.N + col;
                     float v = acol * acc[i][j][r];
                     if (a.beta != 0.0f) v += a.beta * *cp;
-                    if (a.bias) v += bcol;
+                    if (a.bias) v += biasc;
                     const long long flat = (long long)row * a.N + col;
                     if (a.res) v += a.res[flat];
                     *cp = tml_apply_act(v, a.act, flat, a.tail0);

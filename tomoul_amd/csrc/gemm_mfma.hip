@@ -584,24 +584,25 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
 
 GemmPlan plan_gemm(const MatmulArgs &m) {
     GemmPlan p;
-    // f32 B takes the direct-copy kernel whenever its rows allow it.  F16,
-    // Q8_0 and Q4_0 B take it from M = 1024 on: measured on MI355X, it is
-    // 14-18 % faster than the register-staged kernel at Whisper's 1500-row
-    // shapes with N = 3840, level at M = 1024-2048 with N = 4096-5120, and
-    // 4-11 % slower at M <= 512 (where the register-staged kernel widens B
-    // once per tile instead of once per fragment read).  Narrow formats,
-    // Q8_K included, also take it whenever the register-staged kernel's best
-    // tiling leaves most CUs idle (it has no K split): at 256x768x3072 Q8_0
-    // the direct-copy kernel with its split takes 23.1 us against 45.1, at
-    // 512x384x1536 16.3 against 24.8, at 256x768x768 10.9 against 14.5 (96
-    // register tiles each), while with 192 register tiles it is 2-9 % slower
-    // at K <= 768 (256x3072x768, 512x1536x384) and faster at long K (Q8_K
-    // 2048x768x3072: 100.6 against 120.3 us).
-    // Q8_K widens each element with its block scale on the fragment read,
-    // which costs the direct-copy kernel its margin at large M
-    // (1500x3840x1280: 154 against 145 us), so for Q8_K only the idle-CU rule
-    // applies.  TML_GEMM_DMA_Q=1 / 0 forces it on / off for the narrow
-    // formats; TML_GEMM_DMA=0 turns it off.
+    // f32 B takes the direct-copy kernel whenever its rows allow it.  For
+    // the narrow formats both kernels read B through buffer resources and
+    // the direct-copy kernel reads two adjacent columns per LDS access;
+    // measured on MI355X (us, register-staged / direct-copy):
+    //   Q8_0 128x4096x1024 16.8 / 17.2, 512x4096x1024 41.4 / 46.0,
+    //        1024x4096x1024 77.0 / 77.3, 1500x3840x1280 130.5 / 138.1;
+    //   Q4_0 128x5120x1280 33.4 / 28.0, 512x5120x1280 73.1 / 76-79,
+    //        1500x3840x1280 162.4 / 140.8;
+    //   F16  512x4096x1024 41.5 / 43.2, 1500x3840x1280 143.3 / 132.2;
+    //   Q8_K 1500x3840x1280 150.4 / 148.6.
+    // So F16 and Q4_0 take the direct-copy kernel from M = 1024 on, Q4_0 also
+    // at M <= 128 (where the register-staged kernel widens each B element of
+    // a tile for few rows of A); Q8_0 and Q8_K keep the register-staged
+    // kernel.  Every narrow format also takes it whenever the register-staged
+    // kernel's best tiling leaves most CUs idle (it has no K split): at
+    // 256x768x3072 Q8_0 the direct-copy kernel with its split takes 23.1 us
+    // against 45.1, at 512x384x1536 16.3 against 24.8, at 256x768x768 10.9
+    // against 14.5 (96 register tiles each).  TML_GEMM_DMA_Q=1 / 0 forces it
+    // on / off for the narrow formats; TML_GEMM_DMA=0 turns it off.
     const int dma_q = env_int("TML_GEMM_DMA_Q", -1);
     bool few_tiles = false;
     if (m.fmt != TML_FMT_F32) {
@@ -610,8 +611,9 @@ GemmPlan plan_gemm(const MatmulArgs &m) {
         const int64_t tiles = ((m.M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((m.N + kCfgs[c].bn - 1) / kCfgs[c].bn);
         few_tiles = tiles < cus / 2 || (tiles < cus && m.K >= 2048);
     }
-    const bool large_m = m.M >= 1024 && m.fmt != TML_FMT_Q8_K;
-    const bool narrow_ok = m.fmt == TML_FMT_F32 || dma_q == 1 || (dma_q < 0 && (large_m || few_tiles));
+    const bool by_m = (m.fmt == TML_FMT_F16 && m.M >= 1024) ||
+                      (m.fmt == TML_FMT_Q4_0 && (m.M >= 1024 || m.M <= 128));
+    const bool narrow_ok = m.fmt == TML_FMT_F32 || dma_q == 1 || (dma_q < 0 && (by_m || few_tiles));
     if (narrow_ok && env_int("TML_GEMM_DMA", 1) != 0 && gemm_dma_supported(m) && m.K > 0) {
         p.dma = true;
         pick_dma(m.M, m.N, m.K, m.fmt, &p);
