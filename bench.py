@@ -232,7 +232,8 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": traffic_per_step(),
                 "algorithmic_bytes": int(sum(4 * (M * K + K * N + M * N) for (_, M, N, K) in XLMR_SHAPES)),
-                "kernel": "gemm_dma_kernel<f32 B> (tiles 128x64, 32x64; + splitk_reduce_kernel), v_mfma_f32_16x16x4_f32",
+                "kernel": "gemm_dma_kernel<f32 B> (32x64 tiles; BK 32 for QKV and FFN-up, BK 64 with two wave "
+                          "groups along K for out and FFN-down), v_mfma_f32_16x16x4_f32",
                 "per_shape": per_shape, "per_shape_sum_tflops": round(tot_fl / tot_ms / 1e9, 2),
                 "per_shape_note": "each shape timed as 20 back-to-back launches (L2 warm)"}
     log(f"roofline: {json.dumps(roofline)}")
