@@ -3,12 +3,15 @@
 //
 //   C[M,N] = alpha * A[M,K] . B[K,N] + beta * C + bias[N]
 //
-// Data path.  Each BK = 32 deep slice of the A and B tiles is copied from
-// HBM/L2 straight into LDS with global_load_lds_dwordx4 (no staging through
-// VGPRs, no ds_write instructions).  Three LDS stages: while the waves run the
-// MFMAs of slice t, the copies of slices t+1 and t+2 are in flight.  A wave's
-// copy instruction fills 1 KiB of LDS in lane order, so the tiles are stored
-// unpadded and bank conflicts are avoided with XOR swizzles instead:
+// Data path.  Each BK-deep slice (32 or 64) of the A and B tiles is copied
+// from HBM/L2 straight into LDS with buffer_load_dwordx4 ... lds (no staging
+// through VGPRs, no ds_write instructions), each operand through a buffer
+// resource: a lane's 32-bit offset is fixed for the loop plus one uniform
+// step per slice, and offsets past the operand read zeros.  Three LDS stages:
+// while the waves run the MFMAs of slice t, the copies of slices t+1 and t+2
+// are in flight.  A wave's copy instruction fills 1 KiB of LDS in lane
+// order, so the tiles are stored unpadded and bank conflicts are avoided with
+// XOR swizzles instead:
 //   A stage [BM][BK]: 16-byte chunk q of row r sits in slot q ^ (r % 8), so the
 //     per-lane 16-byte fragment reads of 8 consecutive rows hit 8 distinct
 //     bank groups;
@@ -22,7 +25,9 @@
 // (vmcnt(0)) and serialise the pipeline.
 //
 // Compute: v_mfma_f32_16x16x4_f32, fp32 accumulation; lane l feeds A[l%16][kk]
-// and B[kk][l%16] with kk = l/16 and holds D[4*(l/16)+r][l%16] in register r;
+// and B[kk][l%16] with kk = l/16 and holds D[4*(l/16)+r][l%16] in register r
+// (for narrow B the 16 columns of a fragment are every other column of a
+// 32-column group, see PAIR below);
 // within a 16-deep chunk, step s feeds the physical k = 4*kk + s.  Fragment
 // reads run one chunk ahead of the MFMAs and are issued between the two
 // halves of the current chunk's MFMAs; the last chunk of a slice is
