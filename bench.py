@@ -64,6 +64,9 @@ def parse():
                    help="only warm up and run the timed headline steps (for rocprofv3 runs)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run a plain 256 MiB device copy 5 times (scale for FETCH_SIZE / WRITE_SIZE)")
+    p.add_argument("--config5-only", action="store_true",
+                   help="only the config-5 sweep (Whisper encoder linears), for kernel traces and counters")
+    p.add_argument("--config5-layers", type=int, default=32, help="layers of the config-5 sweep")
     p.add_argument("--profile-gemv", action="store_true",
                    help="only run the decoder GEMVs (configs 3/4, M = 1) 50 times per path, eagerly, for rocprofv3")
     return p.parse_args()
@@ -148,6 +151,10 @@ def main():
 
     if args.profile_gemv:
         profile_gemv(torch, dev, sptr, _abi, synth)
+        return
+
+    if args.config5_only:
+        print(json.dumps({"config5": bench_config5(torch, dev, sptr, _abi, layers=args.config5_layers)}), flush=True)
         return
 
     if args.calibrate_copy:
@@ -263,7 +270,7 @@ def main():
         result["gemv"] = bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np)
         result["qgemm"] = bench_qgemm(torch, dev, sptr, timer, _abi, synth, np)
         result["config1"] = bench_config1(torch, dev, sptr, timer, _abi, synth, np)
-        result["config5"] = bench_config5(torch, dev, sptr, _abi)
+        result["config5"] = bench_config5(torch, dev, sptr, _abi, layers=args.config5_layers)
         result["sentence_transformer"] = bench_sentence_transformer(torch, dev, sptr, timer, _abi, synth)
 
     if not args.no_cpu_baseline:
