@@ -558,6 +558,22 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
         del copies
         torch.cuda.empty_cache()
         log(f"profile-gemv: fmt {fmt} vocab {K}x{N}: {launches} prepared launches")
+    # the f32 token embedding [51866 x 1280] used in place (rows-prepared), M = 1
+    K, N, ncopy = 1280, 51866, 3
+    e = torch.from_numpy(synth.normal_matrix(2004, N, K, 0.02)).to(dev)
+    copies = e.reshape(1, N * K).repeat(ncopy, 1)
+    del e
+    hs = [_abi.prepare_rows_dev(_abi.FMT_F32, K, N, copies[i].data_ptr(), 4 * K, 1.0, sptr) for i in range(ncopy)]
+    x = torch.from_numpy(synth.normal_matrix(1001, 1, K)).to(dev)
+    y = torch.empty((1, N), dtype=torch.float32, device=dev)
+    for i in range(launches):
+        _abi.gemm_prepared(hs[i % ncopy], 1, x.data_ptr(), y.data_ptr(), stream=sptr)
+    torch.cuda.synchronize()
+    for h_ in hs:
+        _abi.prepared_free(h_)
+    del copies
+    torch.cuda.empty_cache()
+    log(f"profile-gemv: f32 embedding rows {N}x{K} in place: {launches} launches")
     print(json.dumps({"profile_gemv": True}), flush=True)
 
 
