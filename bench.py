@@ -67,6 +67,8 @@ def parse():
     p.add_argument("--config5-only", action="store_true",
                    help="only the config-5 sweep (Whisper encoder linears), for kernel traces and counters")
     p.add_argument("--config5-layers", type=int, default=32, help="layers of the config-5 sweep")
+    p.add_argument("--config1-only", action="store_true",
+                   help="only config 1 (Whisper-tiny MLP + bias, 20 launches per replay), for kernel traces")
     p.add_argument("--profile-gemv", action="store_true",
                    help="only run the decoder GEMVs (configs 3/4, M = 1) 50 times per path, eagerly, for rocprofv3")
     return p.parse_args()
@@ -151,6 +153,10 @@ def main():
 
     if args.profile_gemv:
         profile_gemv(torch, dev, sptr, _abi, synth)
+        return
+
+    if args.config1_only:
+        print(json.dumps({"config1": bench_config1(torch, dev, sptr, Timer(torch), _abi, synth, np)}), flush=True)
         return
 
     if args.config5_only:
