@@ -156,3 +156,60 @@ def test_tied_vocab_projection_end_to_end(orc, tmp_path):
     got = logits.cpu().numpy()
     assert rel_err(got, ref) <= 1e-4
     assert int(np.argmax(got)) == int(np.argmax(ref))
+
+
+# ------------------------------------- files written by the reference's exporter
+EXPORTER = {0: "exporter_f32.tl", 1: "exporter_q8_0.tl", 2: "exporter_q4_0.tl", 3: "exporter_q8_k.tl",
+            4: "exporter_f16.tl"}
+
+
+@pytest.mark.parametrize("fmt", sorted(EXPORTER))
+def test_exporter_files_to_hbm_and_matmul(orc, fmt):
+    # tests/golden/tl/exporter_*.tl hold bytes tools/tl_format.py wrote
+    # (tests/golden/make_tl_fixtures.py).  Every payload goes to HBM byte for
+    # byte and dequantizes as the oracle says; the [64, 32] weight "w" then
+    # multiplies through the C ABI exactly as the reference's matmul of that
+    # in-memory tensor (dequantize-then-f32-accumulate).
+    import torch
+    path = os.path.join(GOLD, EXPORTER[fmt])
+    data = open(path, "rb").read()
+    ld = tl.ModelLoader(path)
+    for e in orc.tl_parse(data)["tensors"]:
+        name, shp = e[0], e[1]
+        n = int(np.prod(shp))
+        parts = orc.tl_payload(data, e, fmt)
+        nbytes = {0: 4 * n, 4: 2 * n, 1: n, 2: (n + 1) // 2, 3: n}[fmt]
+        buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        sc = torch.empty(max((n + 31) // 32, 1), dtype=torch.float32, device="cuda")
+        scale = ld.readDev(name, fmt, buf.data_ptr(), sc.data_ptr() if fmt == 3 else None)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(buf.cpu().numpy(), np.frombuffer(parts["data"].tobytes(), dtype=np.uint8))
+        if fmt in (1, 2):
+            assert np.float32(scale) == np.float32(parts["scale"])
+        if fmt == 3:
+            np.testing.assert_array_equal(sc.cpu().numpy()[: parts["scales"].size], parts["scales"])
+        got = ld.getTensorDequantized(name).numpy().reshape(-1)
+        np.testing.assert_array_equal(got.view(np.uint32), orc.tl_dequantize(fmt, parts, n).view(np.uint32))
+    e = [t for t in orc.tl_parse(data)["tensors"] if t[0] == "w"][0]
+    parts = orc.tl_payload(data, e, fmt)
+    K, N = e[1]
+    for M in (1, 5, 100):
+        x = synth.normal_matrix(1001 + M, M, K)
+        c = np.zeros((M, N), dtype=np.float32)
+        if fmt == 0:
+            _abi.sgemm(M, N, K, x, parts["data"].reshape(K, N), c)
+            ref = orc.matmul(x, parts["data"].reshape(K, N))
+        elif fmt == 1:
+            _abi.sgemm_q8(M, N, K, x, parts["data"], parts["scale"], c)
+            ref = orc.matmul_q8(x, parts["data"].reshape(K, N), parts["scale"])
+        elif fmt == 2:
+            _abi.sgemm_q4(M, N, K, x, parts["data"], parts["scale"], c)
+            ref = orc.matmul_q4(x, parts["data"], K, N, parts["scale"])
+        elif fmt == 3:
+            _abi.sgemm_q8k(M, N, K, x, parts["data"], parts["scales"], 32, c)
+            ref = orc.matmul_q8k(x, parts["data"].reshape(K, N), parts["scales"])
+        else:
+            _abi.sgemm_f16(M, N, K, x, parts["data"], c)
+            ref = orc.matmul_f16(x, parts["data"].reshape(K, N))
+        tol = 1e-4 if fmt in (0, 4) else 1e-3
+        assert rel_err(c, ref) <= tol, (fmt, M, rel_err(c, ref))
