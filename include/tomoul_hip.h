@@ -199,7 +199,15 @@ int tml_hip_weight_release(const void *host);
  * block     Q8_K block size (ignored otherwise).
  * bias      device pointer to N floats, or NULL.
  * stream    hipStream_t to launch on (NULL = the null stream).
- * All pointers are device pointers.  Asynchronous: returns after the launch. */
+ * All pointers are device pointers.  Asynchronous: returns after the launch.
+ *
+ * Workspace and HIP graphs: a problem whose plan splits K uses the device's
+ * split-K workspace, which the library grows (hipMalloc) the first time a
+ * call needs more than earlier calls did.  Growth is refused with
+ * TML_ERR_INVALID_ARG while `stream` is being captured, so run every call
+ * once eagerly before capturing it.  A grown workspace never frees the old
+ * one before tml_hip_shutdown: a graph captured earlier stays valid however
+ * the workspace grows afterwards. */
 int tml_hip_gemm_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
                      const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
                      void *stream);

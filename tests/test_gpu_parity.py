@@ -522,9 +522,11 @@ def _dev(a):
 def _prepared_cases(orc, w, k, n, a):
     q, s = orc.quantize_q8(w)
     p, s4 = orc.quantize_q4(w)
+    h = orc.to_f16(w)
     return [(_abi.FMT_F32, w, 1.0, orc.matmul(a, w), FP32_TOL),
             (_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s), Q_TOL),
-            (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4), Q_TOL)]
+            (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4), Q_TOL),
+            (_abi.FMT_F16, h, 1.0, orc.matmul_f16(a, h.reshape(k, n)), FP32_TOL)]
 
 
 def _run_prepared(fmt, b, scale, k, n, m, a, bias=None, c0=None, alpha=1.0, beta=0.0):
@@ -542,9 +544,9 @@ def _run_prepared(fmt, b, scale, k, n, m, a, bias=None, c0=None, alpha=1.0, beta
         _abi.prepared_free(h)
 
 
-@pytest.mark.parametrize("k,n", [(1024, 4096), (1280, 5120), (5120, 96), (333, 640), (77, 45), (1, 3),
-                                 (2100, 130), (9000, 40)])
-@pytest.mark.parametrize("m", [1, 2, 3, 5, 9])
+@pytest.mark.parametrize("k,n", [(1024, 4096), (1280, 5120), (5120, 1280), (5120, 96), (333, 640), (77, 45),
+                                 (1, 3), (2100, 130), (9000, 40)])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9])
 def test_prepared_vs_oracle(orc, k, n, m):
     # The prepared kernels cover M <= 8 (registers for small M x E, LDS-staged
     # activations beyond); M = 9 runs the [K,N] GEMM on the weight the copy
@@ -627,11 +629,9 @@ def test_prepared_lds_kernel(orc, cw):
     try:
         for (k, n) in [(5000, 130), (77, 45), (1280, 600)]:
             w = rnd(181, k, n, 0.02)
-            h = orc.to_f16(w)
             for m in (1, 2, 3, 5, 8):
                 a = rnd(182 + m, m, k)
-                cases = _prepared_cases(orc, w, k, n, a) + [(_abi.FMT_F16, h, 1.0, orc.matmul_f16(a, h), FP32_TOL)]
-                for fmt, b, scale, ref, tol in cases:
+                for fmt, b, scale, ref, tol in _prepared_cases(orc, w, k, n, a):
                     assert rel_err(_run_prepared(fmt, b, scale, k, n, m, a), ref) <= tol, (k, n, m, fmt)
     finally:
         for key, v in saved.items():

@@ -138,18 +138,38 @@ def test_prepared_cols(orc, env, fmt, lds):
 def test_registered_cols_weight(orc):
     # Host-pointer calls on a registered per-channel weight build a prepared
     # copy with the column scales; new scales for the same weight rebuild it.
+    # The result equals the prepared kernel's bit for bit (tml_hip_prepare_ex_dev
+    # on the same bytes and scales) and differs from the [K,N] kernel's,
+    # which sums in another order: the prepared copy is what ran.
+    import torch
     fmt = _abi.FMT_Q8_0_PC
     k, n = 640, 384
     w = _weights(241, k, n)
     q, s = _quant(orc, fmt, w)
     q = np.ascontiguousarray(q)
     a = rnd(242, 1, k)
+    expect = []
+    for scales in (s, s * 2.0):
+        sc = np.ascontiguousarray(scales, dtype=np.float32)
+        kn = np.zeros((1, n), np.float32)
+        _abi.gemm(fmt, 1, n, k, a, q, kn, scales=sc)  # unregistered: the [K,N] kernel
+        B, S, A = (torch.from_numpy(v).cuda() for v in (q.reshape(-1).view(np.uint8), sc, a))
+        C = torch.zeros((1, n), dtype=torch.float32, device="cuda")
+        h = _abi.prepare_ex_dev(fmt, k, n, B.data_ptr(), scales_ptr=S.data_ptr())
+        try:
+            _abi.gemm_prepared(h, 1, A.data_ptr(), C.data_ptr())
+            torch.cuda.synchronize()
+        finally:
+            _abi.prepared_free(h)
+        expect.append((sc, kn, C.cpu().numpy()))
     _abi.weight_register(q)
     try:
-        for scales in (s, s * 2.0):
+        for sc, kn, prep in expect:
             got = np.zeros((1, n), np.float32)
-            _abi.gemm(fmt, 1, n, k, a, q, got, scales=np.ascontiguousarray(scales, dtype=np.float32))
-            assert rel_err(got, orc.matmul_cols(a, fmt, q, scales, k, n)) <= Q_TOL
+            _abi.gemm(fmt, 1, n, k, a, q, got, scales=sc)
+            np.testing.assert_array_equal(got, prep)
+            assert not np.array_equal(got, kn)
+            assert rel_err(got, orc.matmul_cols(a, fmt, q, sc, k, n)) <= Q_TOL
     finally:
         _abi.weight_release(q)
 

@@ -237,3 +237,21 @@ def test_oracle_dequantize_matches_definitions(orc):
     h = orc.to_f16(w)
     np.testing.assert_array_equal(orc.tl_dequantize(4, {"data": h}, 77), orc.from_f16(h))
     assert qz.BLOCK_SIZE == 32
+
+
+def test_shape_product_that_wraps_is_corrupted(orc):
+    # A crafted rank-4 shape of 2^16 x 2^16 x 2^16 x 2^16 elements: the
+    # product wraps 2^64 to 0, which would match an empty payload.  The
+    # getters compare the element count against what the payload can hold
+    # and report CorruptedFile.
+    import struct as st
+    for fmt, payload in ((0, b""), (1, st.pack("<f", 1.0)), (2, st.pack("<f", 1.0))):
+        head = b"TOUL" + st.pack("<II", 1, 1) + bytes([fmt, 0, 0, 0])
+        table = st.pack("<I", 1) + b"w" + st.pack("<I", 4) + st.pack("<4I", *[1 << 16] * 4)
+        start = len(head) + len(table) + 16
+        data = head + table + st.pack("<QQ", start, len(payload)) + payload
+        ld = tl.ModelLoader.initFromBytes(data)
+        assert ld.getTensorInfo("w").shape == (1 << 16,) * 4
+        getter = {0: ld.getTensor, 1: ld.getQuantizedTensorQ8, 2: ld.getQuantizedTensorQ4}[fmt]
+        with pytest.raises(tl.LoadError.CorruptedFile):
+            getter("w")

@@ -26,6 +26,8 @@
 // 8 XCDs (each with its own L2); ids are remapped so that consecutive tiles
 // run on one XCD, then grouped GROUP_M tile-rows at a time so neighbouring
 // workgroups share A rows and B columns in that XCD's L2.
+#include <cstdlib>
+
 #include "tml_internal.hpp"
 
 namespace tml {
@@ -628,12 +630,43 @@ void gemm_workspace_need(const MatmulArgs &m, size_t *partial_floats, size_t *co
     if (p.dma && p.nsplit > 1) gemm_dma_workspace_need(m, p, partial_floats, counters);
 }
 
+// The planner's overrides (experiments and tests: TML_GEMM_DMA_TILE,
+// TML_GEMM_SPLIT, TML_GEMM_TILE, TML_GEMM_DMA_Q, TML_GEMM_DMA, TML_GEMM_FUSED,
+// TML_GEMM_XCDPART, TML_GEMM_XCD, TML_GEMM_GROUPM) are honoured only up to
+// the problem sizes the GPU tests run them at, M*N*K <= 512*1024*4096.  A
+// calibration sweep that forced tile x split plans at the Whisper encoder
+// shapes (M*N*K ~ 1e10) once ended in a GPU memory fault whose cause was not
+// found in these kernels (their address arithmetic over that whole sweep is
+// checked on the CPU, tests/test_cpu_emu.py), so forced plans above that size
+// are refused rather than run untested.  Default plans are unaffected.
+// (The CPU build of tests/cpu_emu raises the limit at compile time to check
+// the kernels' addresses under every forced plan at full size.)
+#ifndef TML_FORCED_PLAN_MAX_MNK
+#define TML_FORCED_PLAN_MAX_MNK (512ull * 1024ull * 4096ull)
+#endif
+constexpr uint64_t kForcedPlanMaxMNK = TML_FORCED_PLAN_MAX_MNK;
+
+bool plan_forced() {
+    static const char *const keys[] = {"TML_GEMM_DMA_TILE", "TML_GEMM_SPLIT", "TML_GEMM_TILE",  "TML_GEMM_DMA_Q",
+                                       "TML_GEMM_DMA",      "TML_GEMM_FUSED", "TML_GEMM_XCDPART", "TML_GEMM_XCD",
+                                       "TML_GEMM_GROUPM"};
+    for (const char *k : keys) {
+        const char *v = std::getenv(k);
+        if (v != nullptr && *v != '\0') return true;
+    }
+    return false;
+}
+
 Status launch_gemm_mfma(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     // Index math in the kernels is 32-bit for dimensions and 64-bit for
     // element offsets; grids are 1-D.
     const int64_t lim = (int64_t)1 << 30;
     if (m.M >= lim || m.N >= lim || m.K >= lim)
         return Status::Err(TML_ERR_INVALID_SHAPE, "GEMM dimension exceeds 2^30");
+    if (plan_forced() && (uint64_t)m.M * (uint64_t)m.N * (uint64_t)m.K > kForcedPlanMaxMNK)
+        return Status::Err(TML_ERR_INVALID_ARG,
+                           "forced GEMM plans (TML_GEMM_* overrides) are refused above M*N*K = 512*1024*4096, "
+                           "the largest size the tests run them at");
     const GemmPlan p = plan_gemm(m);
     if (p.dma) return launch_gemm_f32_dma(m, p, ws, s);
     const int cus = device_cus();

@@ -9,6 +9,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <string>
 #include <unordered_map>
 
 #include "tml_internal.hpp"
@@ -88,12 +89,39 @@ struct Registered {
     Prepared *prep = nullptr;  // made on the first decoder call that uses this weight
 };
 
+// A device allocation that only grows and never frees a buffer a launch
+// may still reference: the split-K workspace of the asynchronous "_dev"
+// entry points.  Their launches may sit in a queue or in a captured HIP
+// graph that is replayed later, so a grown buffer replaces the old one in
+// new launches only; the old one is released by tml_hip_shutdown.
+struct GrowBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    std::vector<void *> retired;
+    Status ensure(size_t n) {
+        if (n <= bytes) return Status::Ok();
+        void *q = nullptr;
+        TML_HIP_TRY(hipMalloc(&q, n));
+        if (p) retired.push_back(p);
+        p = q;
+        bytes = n;
+        return Status::Ok();
+    }
+    void release() {
+        for (void *r : retired) (void)hipFree(r);
+        retired.clear();
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+};
+
 struct DeviceCtx {
     int device = -1;
     hipStream_t stream = nullptr;
-    DevBuf a, b, c, bias, res, scales, qtmp;  // staging of the host-pointer API
-    DevBuf tl_raw, tl_scales, tr;            // .tl payload staging, transpose temporary
-    DevBuf ws, counters;                 // split-K workspace (gemv, gemm)
+    DevBuf a, b, c, bias, res, scales;   // staging of the host-pointer API (synchronous calls)
+    GrowBuf qtmp, tl_raw, tl_scales, tr;  // quantizer partials, .tl payload staging, transpose temporary
+    GrowBuf ws, counters;                // split-K workspace (gemv, gemm)
     DevBuf zero;                         // kZeroBlockBytes of zeros
     std::unordered_map<const void *, Registered> weights;
 };
@@ -136,18 +164,34 @@ Status current_ctx(DeviceCtx **out) {
     return Status::Ok();
 }
 
+// Split-K workspace (partial sums and arrival counters) this problem needs.
+void workspace_need(const MatmulArgs &m, size_t *partial_floats, size_t *counters) {
+    *partial_floats = 0;
+    *counters = 0;
+    if (m.M <= kGemvMaxM) gemv_workspace_need(m, partial_floats, counters);
+    else gemm_workspace_need(m, partial_floats, counters);
+}
+
 // Grow the split-K workspace to what this problem needs; new counters are
-// zeroed (kernels leave them zero when they finish).
+// zeroed on `s` before the launch that needs them (kernels leave them zero
+// when they finish).  Growing allocates, so it is refused while `s` is being
+// captured into a graph: run every captured call once eagerly first.
 Status ensure_workspace(DeviceCtx *c, const MatmulArgs &m, hipStream_t s, Workspace *ws) {
     size_t pf = 0, nc = 0;
-    if (m.M <= kGemvMaxM) gemv_workspace_need(m, &pf, &nc);
-    else gemm_workspace_need(m, &pf, &nc);
+    workspace_need(m, &pf, &nc);
     if (pf > 0) {
+        const bool grow_ws = pf * sizeof(float) > c->ws.bytes;
+        const bool grow_ctr = nc * sizeof(unsigned) > c->counters.bytes;
+        if (grow_ws || grow_ctr) {
+            hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+            TML_HIP_TRY(hipStreamIsCapturing(s, &cap));
+            if (cap != hipStreamCaptureStatusNone)
+                return Status::Err(TML_ERR_INVALID_ARG,
+                                   "the split-K workspace must grow during stream capture: run this call once "
+                                   "eagerly (outside capture) before capturing it");
+        }
         TML_TRY(c->ws.ensure(pf * sizeof(float)));
-        if (c->counters.bytes < nc * sizeof(unsigned)) {
-            // The old counters may still be in use by queued kernels on
-            // another stream; finish all work on the device before growing.
-            TML_HIP_TRY(hipDeviceSynchronize());
+        if (grow_ctr) {
             TML_TRY(c->counters.ensure(nc * sizeof(unsigned)));
             TML_HIP_TRY(hipMemsetAsync(c->counters.p, 0, c->counters.bytes, s));
         }
@@ -183,34 +227,54 @@ size_t weight_bytes(int fmt, int64_t K, int64_t N) {
 
 bool valid_act(int act) { return act == TML_ACT_NONE || act == TML_ACT_GELU_ERF || act == TML_ACT_GELU_TANH; }
 
-Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B,
-                float scale, const float *scales, int64_t block, const float *bias, float *C, float alpha,
-                float beta, hipStream_t s, int act = TML_ACT_NONE, const float *res = nullptr) {
+// Validates a device-pointer matmul and fills its MatmulArgs (zero block
+// and workspace excepted).  *empty: nothing to compute (M == 0 or N == 0).
+Status matmul_args(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                   const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
+                   int act, const float *res, MatmulArgs *m, bool *empty) {
+    *empty = false;
     if (!valid_fmt(fmt)) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown weight format");
     if (!valid_act(act)) return Status::Err(TML_ERR_INVALID_ARG, "unknown activation");
     if (M < 0 || N < 0 || K < 0) return Status::Err(TML_ERR_INVALID_SHAPE, "negative matrix dimension");
-    if (M == 0 || N == 0) return Status::Ok();
+    if (M == 0 || N == 0) {
+        *empty = true;
+        return Status::Ok();
+    }
     if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr)))
         return Status::Err(TML_ERR_INVALID_ARG, "null matrix pointer");
     if (fmt == TML_FMT_Q8_K && (block <= 0 || (K > 0 && scales == nullptr)))
         return Status::Err(TML_ERR_INVALID_ARG, "Q8_K needs scales and a positive block size");
     if (per_channel(fmt) && scales == nullptr)
         return Status::Err(TML_ERR_INVALID_ARG, "per-channel formats need their N column scales");
-    MatmulArgs m;
-    m.M = M; m.N = N; m.K = K;
-    m.A = A; m.B = B; m.block = fmt == TML_FMT_Q8_K ? block : 1;
-    m.scales = fmt == TML_FMT_Q8_K ? scales : nullptr;
-    m.colscale = per_channel(fmt) ? scales : nullptr;
-    m.bias = bias; m.C = C; m.beta = beta; m.fmt = data_fmt(fmt);
-    m.alpha_eff = (fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0) ? alpha * scale : alpha;
-    m.zero = c->zero.p;
-    m.act = act;
-    m.res = res;
-    Workspace ws;
-    TML_TRY(ensure_workspace(c, m, s, &ws));
-    if (M <= kGemvMaxM) return launch_gemv(m, ws, s);
+    m->M = M; m->N = N; m->K = K;
+    m->A = A; m->B = B; m->block = fmt == TML_FMT_Q8_K ? block : 1;
+    m->scales = fmt == TML_FMT_Q8_K ? scales : nullptr;
+    m->colscale = per_channel(fmt) ? scales : nullptr;
+    m->bias = bias; m->C = C; m->beta = beta; m->fmt = data_fmt(fmt);
+    m->alpha_eff = (fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0) ? alpha * scale : alpha;
+    m->act = act;
+    m->res = res;
+    return Status::Ok();
+}
+
+Status launch_matmul(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
+    if (m.M <= kGemvMaxM) return launch_gemv(m, ws, s);
     return launch_gemm_mfma(m, ws, s);
 }
+
+Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B,
+                float scale, const float *scales, int64_t block, const float *bias, float *C, float alpha,
+                float beta, hipStream_t s, int act = TML_ACT_NONE, const float *res = nullptr) {
+    MatmulArgs m;
+    bool empty = false;
+    TML_TRY(matmul_args(fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, act, res, &m, &empty));
+    if (empty) return Status::Ok();
+    m.zero = c->zero.p;
+    Workspace ws;
+    TML_TRY(ensure_workspace(c, m, s, &ws));
+    return launch_matmul(m, ws, s);
+}
+
 
 bool preparable_fmt(int fmt) {
     return fmt == TML_FMT_F32 || fmt == TML_FMT_F16 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0 || per_channel(fmt);
@@ -341,7 +405,8 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
     // A registered weight used at a decoder row count gets (once) and then
     // uses its prepared, K-contiguous copy.
     Registered *reg = nullptr;
-    if (preparable_fmt(fmt) && prepared_gemv_supported(fmt, M, K) && prepared_gemv_preferred(fmt, M)) {
+    if (preparable_fmt(fmt) && prepared_gemv_supported(data_fmt(fmt), M, K) &&
+        prepared_gemv_preferred(data_fmt(fmt), M)) {
         auto it = c->weights.find(B);
         if (it != c->weights.end() && it->second.bytes >= weight_bytes(fmt, K, N)) reg = &it->second;
     }
@@ -391,6 +456,17 @@ Status quantize_dev(DeviceCtx *c, int fmt, int64_t n, const float *w, void *q, f
     }
     TML_TRY(c->qtmp.ensure(quantize_tmp_floats(fmt, n) * sizeof(float) + 16));
     return launch_quantize(fmt, n, w, q, scales, (float *)c->qtmp.p, s);
+}
+
+Status tl_check_getter(int getter) {
+    if (getter < TML_FMT_F32 || getter > TML_FMT_F16) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown getter format");
+    return Status::Ok();
+}
+Status tl_need(const TlParts &p, const void *data, const float *scales, const float *scale) {
+    if ((p.data_bytes > 0 && data == nullptr) || (p.nscales > 0 && scales == nullptr) ||
+        ((p.fmt == TML_FMT_Q8_0 || p.fmt == TML_FMT_Q4_0) && scale == nullptr))
+        return Status::Err(TML_ERR_INVALID_ARG, "null destination");
+    return Status::Ok();
 }
 
 }  // namespace
@@ -815,18 +891,6 @@ int tml_tl_info(tml_tl_t f, const char *name, int64_t *dims, int cap, int *ndim,
     return report(Status::Ok());
 }
 
-namespace {
-Status tl_check_getter(int getter) {
-    if (getter < TML_FMT_F32 || getter > TML_FMT_F16) return Status::Err(TML_ERR_INVALID_FORMAT, "unknown getter format");
-    return Status::Ok();
-}
-Status tl_need(const TlParts &p, const void *data, const float *scales, const float *scale) {
-    if ((p.data_bytes > 0 && data == nullptr) || (p.nscales > 0 && scales == nullptr) ||
-        ((p.fmt == TML_FMT_Q8_0 || p.fmt == TML_FMT_Q4_0) && scale == nullptr))
-        return Status::Err(TML_ERR_INVALID_ARG, "null destination");
-    return Status::Ok();
-}
-}  // namespace
 
 int tml_tl_read(tml_tl_t f, const char *name, int getter, void *data, float *scales, float *scale) {
     if (f == nullptr) return report(Status::Err(TML_ERR_INVALID_ARG, "null file"));

@@ -73,9 +73,15 @@ Status parse(TlFile *f) {
     return Status::Ok();
 }
 
-int64_t numel_of(const TlTensor &t) {
+// Product of the dims, or -1 when it exceeds `cap` (the most elements a
+// payload of the file's size could hold) -- a crafted shape whose product
+// wraps around 2^64 must not pass the payload-size check.
+int64_t numel_of(const TlTensor &t, uint64_t cap) {
     uint64_t e = 1;
-    for (int64_t d : t.shape) e *= (uint64_t)d;
+    for (int64_t d : t.shape) {
+        if (d != 0 && e > cap / (uint64_t)d) return -1;
+        e *= (uint64_t)d;
+    }
     return (int64_t)e;
 }
 
@@ -143,7 +149,9 @@ Status tl_parts(const TlFile *f, const char *name, int getter, bool by_file_form
     if (t == nullptr) return Status::Err(TML_ERR_TENSOR_NOT_FOUND, std::string("no tensor named ") + (name ? name : ""));
     if (t->offset > f->size || t->size > f->size - t->offset)
         return Status::Err(TML_ERR_CORRUPTED_FILE, "tensor data runs past the end of the file");
-    const int64_t n = numel_of(*t);
+    // No format stores more than two elements per payload byte.
+    const int64_t n = numel_of(*t, 2 * t->size);
+    if (n < 0) return Status::Err(TML_ERR_CORRUPTED_FILE, "tensor shape holds more elements than its payload");
     const uint8_t *src = f->data + t->offset;
     *p = TlParts{};
     p->fmt = fmt;

@@ -172,6 +172,12 @@ class ModelLoader:
         info = self.getTensorInfo(name)
         if info is None:
             raise TensorNotFound(f"no tensor named {name}")
+        # No format stores more than two elements per payload byte: a shape
+        # claiming more (e.g. one whose product wraps 2^64 in a native
+        # reader) is CorruptedFile before any buffer is sized from it, the
+        # rule the native getters apply.
+        if _numel(info.shape) > 2 * info.data_size:
+            raise CorruptedFile("tensor shape holds more elements than its payload")
         return info.shape
 
     def _read(self, name: str, getter: int, data: np.ndarray, scales: np.ndarray | None) -> float:
@@ -183,9 +189,8 @@ class ModelLoader:
 
     # ----------------------------------------------------------- getters
     def getTensor(self, name: str) -> Tensor:  # noqa: N802
+        self._shape(name)
         info = self.getTensorInfo(name)
-        if info is None:
-            raise TensorNotFound(f"no tensor named {name}")
         data = np.empty(_numel(info.shape), dtype=np.float32)
         self._read(name, QuantFormat.f32, data, None)
         return Tensor.from_numpy(data.reshape(info.shape) if info.shape else data)
