@@ -2,25 +2,33 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Workload (XLM-RoBERTa-large layer at seq=512, fp32):
-one "step" is the four linear layers of one encoder layer, back to back on
-one stream, operands resident in HBM:
-    QKV      X[512x1024] . W[1024x3072]
-    out      X[512x1024] . W[1024x1024]
-    FFN-up   X[512x1024] . W[1024x4096]
-    FFN-down H[512x4096] . W[4096x1024]
-Inputs: SplitMix64/Box-Muller, X,H ~ N(0,1) (seed 1001), W ~ N(0, 0.02)
-(seed 2002 + index).  `value` = 2*M*N*K summed over the step / step time.
+Headline workload: BASELINE config 5, the largest single-GPU configuration --
+the Whisper large-v3-turbo encoder linears at 1500 frames, fp32, as one
+32-layer sweep with each layer's own weights (2.3 GB of weights per sweep,
+nine times the 256 MB Infinity Cache).  One "step" is one sweep, on one
+stream, operands resident in HBM:
+    QKV      X[1500x1280] . W[1280x3840]   (the fused q, k, v projections)
+    FFN-up   X[1500x1280] . W[1280x5120]
+    FFN-down H[1500x5120] . W[5120x1280]
+for each of 32 layers: 96 GEMMs, 1.730 TFLOP.
+Inputs (host generator of tomoul_amd/synth.py, SplitMix64 -> Box-Muller):
+X ~ N(0,1) seed 1001, H ~ N(0,1) seed 1002, layer l's three weights
+~ N(0, 0.02) drawn in that order from one stream of seed 2002 + l.
+`value` = TFLOP per sweep x K / wall time of the K timed sweeps.
 
 The same JSON line also carries:
+  batches       the K timed sweeps as 5 consecutive batches (HIP events on
+                the stream the sweeps run on), each batch's TFLOP/s and
+                their median;
   roofline      the GEMM kernel against the fp32 MFMA peak (157.3 TFLOP/s),
-                from HIP events around each launch on the launch stream;
-  gemv          quantized decoder GEMVs (configs 3 and 4 at M <= 8) in GB/s
-                against 8 TB/s, rotating over >= 1 GB of distinct weight
-                copies so neither L2 nor the 256 MB Infinity Cache serves them;
-  qgemm, config1  the other configs' large-M products;
+                from HIP events over the timed region on the launch stream;
+  config5_q     the same sweep with Q8_0 and Q4_0 weights;
+  config2       the XLM-R-large layer linears at seq 512 (configs[1]);
+  config1, qgemm, gemv, sentence_transformer   the other configs;
+  host_pointer  the drop-in's host-pointer calls (PCIe transfers included);
   cpu_baseline  the reference's CPU path (the oracle's restatement of the
-                ops.zig fallback, test infrastructure) on the same workload.
+                ops.zig fallback and quantization.zig loops, test
+                infrastructure) on a bounded sample of the same workloads.
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -37,7 +45,13 @@ sys.path.insert(0, ROOT)
 FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
 
-XLMR_SHAPES = [  # (name, M, N, K)
+ENC_SHAPES = [  # config 5, per layer: (name, M, N, K)
+    ("qkv", 1500, 3840, 1280),
+    ("ffn_up", 1500, 5120, 1280),
+    ("ffn_down", 1500, 1280, 5120),
+]
+ENC_LAYERS = 32
+XLMR_SHAPES = [  # config 2: (name, M, N, K)
     ("qkv", 512, 3072, 1024),
     ("out", 512, 1024, 1024),
     ("ffn_up", 512, 4096, 1024),
@@ -52,26 +66,58 @@ def log(*a):
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=20, help="timed sweeps (one sweep = 32 layers x 3 GEMMs)")
+    p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--settle", type=float, default=1.0,
-                   help="seconds of untimed replays of the captured steps after the warm-up steps, so the "
+                   help="seconds of untimed replays of the captured sweep after the warm-up steps, so the "
                         "timed region runs at steady clocks")
+    p.add_argument("--layers", type=int, default=ENC_LAYERS, help="layers per sweep (32 = the config)")
+    p.add_argument("--gen-workers", type=int, default=min(16, os.cpu_count() or 1),
+                   help="processes drawing the config-5 weights on the host (0: in this process, for "
+                        "rocprofv3 runs)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true", help="only the headline workload")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the 1-thread CPU baseline sample")
     p.add_argument("--profile-step", action="store_true",
-                   help="only warm up and run the timed headline steps (for rocprofv3 runs)")
+                   help="only warm up and run the timed headline sweeps (for rocprofv3 runs)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run a plain 256 MiB device copy 5 times (scale for FETCH_SIZE / WRITE_SIZE)")
-    p.add_argument("--config5-only", action="store_true",
-                   help="only the config-5 sweep (Whisper encoder linears), for kernel traces and counters")
-    p.add_argument("--config5-layers", type=int, default=32, help="layers of the config-5 sweep")
+    p.add_argument("--config2-only", action="store_true",
+                   help="only the XLM-R layer step (config 2), for kernel traces")
     p.add_argument("--config1-only", action="store_true",
                    help="only config 1 (Whisper-tiny MLP + bias, 20 launches per replay), for kernel traces")
     p.add_argument("--profile-gemv", action="store_true",
                    help="only run the decoder GEMVs (configs 3/4, M = 1) 50 times per path, eagerly, for rocprofv3")
     return p.parse_args()
+
+
+# ------------------------------------------------------------ host inputs
+def _layer_weights(layer: int):
+    """Layer `layer`'s three config-5 weights: one N(0, 0.02) stream of seed
+    2002 + layer, drawn in the order QKV, FFN-up, FFN-down."""
+    from tomoul_amd import synth
+    out, off = [], 0
+    for (_, M, N, K) in ENC_SHAPES:
+        out.append(synth.normal(2002 + layer, K * N, 0.0, 0.02, offset=off).reshape(K, N))
+        off += K * N
+    return out
+
+
+def encoder_weights(layers: int, workers: int):
+    """All layers' weights, drawn before the GPU is used: by `workers` child
+    processes (spawned: fresh interpreters that never touch the GPU), or in
+    this process when workers == 0 -- for runs under rocprofv3, whose
+    preloaded library would follow every child."""
+    if workers <= 0:
+        out = []
+        for li in range(layers):
+            out.append(_layer_weights(li))
+            if li % 8 == 7:
+                log(f"config-5 weights: {li + 1} of {layers} layers drawn")
+        return out
+    import multiprocessing as mp
+    with mp.get_context("spawn").Pool(max(1, min(workers, layers))) as pool:
+        return pool.map(_layer_weights, range(layers))
 
 
 class Timer:
@@ -119,9 +165,20 @@ def main():
         sys.exit(2)
 
     import numpy as np
+
+    from tomoul_amd import synth
+
+    headline = not (args.config1_only or args.config2_only or args.profile_gemv or args.calibrate_copy)
+    if headline:
+        t0 = time.perf_counter()
+        host_w = encoder_weights(args.layers, args.gen_workers)
+        host_x = synth.normal_matrix(1001, 1500, 1280)
+        host_h = synth.normal_matrix(1002, 1500, 5120)
+        log(f"config-5 inputs drawn on the host in {time.perf_counter() - t0:.1f} s")
+
     import torch
 
-    from tomoul_amd import _abi, synth
+    from tomoul_amd import _abi
 
     _abi.init()
     dev = torch.device("cuda:0")
@@ -130,39 +187,15 @@ def main():
     timer = Timer(torch)
     log(f"device: {_abi.device_name()}")
 
-    def to_dev(a):
-        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-
-    # ---------------------------------------------------------------- headline
-    x = to_dev(synth.normal_matrix(1001, 512, 1024))
-    h = to_dev(synth.normal_matrix(1001, 512, 4096))
-    ws = [to_dev(synth.normal_matrix(2002 + i, K, N, 0.02)) for i, (_, M, N, K) in enumerate(XLMR_SHAPES)]
-    outs = [torch.empty((M, N), dtype=torch.float32, device=dev) for (_, M, N, K) in XLMR_SHAPES]
-    ins = [x, x, x, h]
-    launches = []
-    for i, (name, M, N, K) in enumerate(XLMR_SHAPES):
-        a_p, b_p, c_p = ins[i].data_ptr(), ws[i].data_ptr(), outs[i].data_ptr()
-        launches.append((name, M, N, K,
-                         lambda st, M=M, N=N, K=K, a_p=a_p, b_p=b_p, c_p=c_p:
-                         _abi.gemm_dev(_abi.FMT_F32, M, N, K, a_p, b_p, c_p, stream=st)))
-    step_flops = sum(2.0 * M * N * K for (_, M, N, K) in XLMR_SHAPES)
-
-    def step(st=sptr):
-        for (_, _, _, _, fn) in launches:
-            fn(st)
-
     if args.profile_gemv:
         profile_gemv(torch, dev, sptr, _abi, synth)
         return
-
     if args.config1_only:
         print(json.dumps({"config1": bench_config1(torch, dev, sptr, Timer(torch), _abi, synth, np)}), flush=True)
         return
-
-    if args.config5_only:
-        print(json.dumps({"config5": bench_config5(torch, dev, sptr, _abi, layers=args.config5_layers)}), flush=True)
+    if args.config2_only:
+        print(json.dumps({"config2": bench_config2(torch, dev, sptr, timer, _abi, synth, args)}), flush=True)
         return
-
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -172,83 +205,108 @@ def main():
         print(json.dumps({"calibrate_copy_bytes": 256 << 20, "copies": 5}), flush=True)
         return
 
-    # The K timed steps are captured as one HIP graph (4 GEMM launches per
-    # step, plus a split-K reduce where the plan splits K) and replayed once,
-    # so the steps run back to back as a model's layers would; replaying a
-    # one-step graph K times would add a graph launch (several us) per step.
+    # ---------------------------------------------------------------- headline
+    L = args.layers
+    x = torch.from_numpy(host_x).to(dev)
+    h = torch.from_numpy(host_h).to(dev)
+    wdev = [[torch.from_numpy(w).to(dev) for w in layer] for layer in host_w]
+    outs = [torch.empty((M, N), dtype=torch.float32, device=dev) for (_, M, N, K) in ENC_SHAPES]
+    sweep_flops = L * sum(2.0 * M * N * K for (_, M, N, K) in ENC_SHAPES)
+
+    def sweep(st=sptr, layers=None):
+        for li in (range(L) if layers is None else layers):
+            for i, (_, M, N, K) in enumerate(ENC_SHAPES):
+                a = x if K == 1280 else h
+                _abi.gemm_dev(_abi.FMT_F32, M, N, K, a.data_ptr(), wdev[li][i].data_ptr(), outs[i].data_ptr(),
+                              stream=st)
+
     for _ in range(args.warmup):
-        step()
+        sweep()
     torch.cuda.synchronize()
+    # correctness guard: the first and last layers against a float64 product
+    # of the same device operands
+    max_rel = 0.0
+    for li in sorted({0, L - 1}):
+        sweep(layers=[li])
+        torch.cuda.synchronize()
+        for i, (_, M, N, K) in enumerate(ENC_SHAPES):
+            a = x if K == 1280 else h
+            ref = a.double() @ wdev[li][i].double()
+            max_rel = max(max_rel, float((outs[i].double() - ref).abs().max() / ref.abs().max()))
+            del ref
+    torch.cuda.empty_cache()
+    log(f"headline max rel err vs f64: {max_rel:.3e}")
+
+    # One sweep (96 launches, plus a split-K reduce where the plan splits K)
+    # captured as one HIP graph; the timed region replays it K times in 5
+    # consecutive batches with HIP events at the batch boundaries on the
+    # stream the graph runs on.  MI355X lowers its clocks whenever the GPU
+    # idles, so untimed replays run for --settle seconds first.
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
-        step(side.cuda_stream)
+        sweep(side.cuda_stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
-        for _ in range(args.steps):
-            step(side.cuda_stream)
+        sweep(side.cuda_stream)
     torch.cuda.synchronize()
-    graph.replay()  # warm replay (first replay uploads the graph)
-    torch.cuda.synchronize()
-    # correctness guard against a float64 torch product on the GPU
-    max_rel = 0.0
-    for i, (name, M, N, K) in enumerate(XLMR_SHAPES):
-        ref = (ins[i].double() @ ws[i].double())
-        max_rel = max(max_rel, float((outs[i].double() - ref).abs().max() / ref.abs().max()))
-    log(f"headline max rel err vs f64: {max_rel:.3e}")
-
-    # Settle: MI355X raises its clocks over the first stretch of sustained
-    # load and lowers them again when the GPU idles (the correctness guard
-    # above idles it for a few hundred ms); a timed region that starts cold
-    # measures that ramp (140-145 us per step against 131 us at steady
-    # clocks), not the kernels.  Untimed replays of the same K-step graph run
-    # until --settle seconds have passed, immediately before the timed
-    # replay; their count is reported as extra_warmup_steps.
-    extra_warmup = args.steps
+    extra_warmup = 0
     t_settle = time.perf_counter()
-    while time.perf_counter() - t_settle < args.settle:
+    while time.perf_counter() - t_settle < args.settle or extra_warmup == 0:
         graph.replay()
         torch.cuda.synchronize()
-        extra_warmup += args.steps
+        extra_warmup += 1
+    K = max(1, args.steps)
+    nb = min(5, K)
+    bounds = [round(K * b / nb) for b in range(nb + 1)]
     cur = torch.cuda.current_stream(dev)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(nb + 1)]
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ev0.record(cur)
-    graph.replay()
-    ev1.record(cur)
+    evs[0].record(cur)
+    for b in range(nb):
+        for _ in range(bounds[b + 1] - bounds[b]):
+            graph.replay()
+        evs[b + 1].record(cur)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    ev_ms = ev0.elapsed_time(ev1)
-    ms_per_step = wall_ms / args.steps
-    value = step_flops / (ms_per_step * 1e-3) / 1e12
-    log(f"headline: {ms_per_step * 1e3:.1f} us/step wall, {ev_ms / args.steps * 1e3:.1f} us/step events, "
-        f"{value:.2f} TFLOP/s")
+    ev_ms = evs[0].elapsed_time(evs[-1])
+    batch = []
+    for b in range(nb):
+        ms_b = evs[b].elapsed_time(evs[b + 1])
+        n_b = bounds[b + 1] - bounds[b]
+        batch.append({"sweeps": n_b, "ms": round(ms_b, 4), "TFLOP/s": round(sweep_flops * n_b / ms_b / 1e9, 2)})
+    med = sorted(bb["TFLOP/s"] for bb in batch)[nb // 2]
+    ms_per_step = wall_ms / K
+    value = sweep_flops / (ms_per_step * 1e-3) / 1e12
+    log(f"headline: {ms_per_step:.3f} ms/sweep wall, {ev_ms / K:.3f} ms/sweep events, {value:.2f} TFLOP/s, "
+        f"batches {[bb['TFLOP/s'] for bb in batch]}")
     if args.profile_step:
         print(json.dumps({"profile_step": True, "ms_per_step": ms_per_step, "tflops": value}), flush=True)
         return
 
-    # Per-launch durations of the GEMM kernels: 20 back-to-back launches of
-    # each shape in one graph, HIP events around 5 replays on the stream the
-    # graph runs on.
+    # Per-shape launch durations: the 32 layers' launches of one shape in one
+    # graph (each layer its own weights, as in the sweep), 5 replays.
     per_shape = {}
-    tot_fl, tot_ms = 0.0, 0.0
-    for (name, M, N, K, fn) in launches:
-        ms = timer.time_ms(lambda st, fn=fn: [fn(st) for _ in range(20)], 5, per_replay=20)
-        fl = 2.0 * M * N * K
-        per_shape[name] = {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2), "tflops": round(fl / ms / 1e9, 2)}
-        tot_fl += fl
-        tot_ms += ms
-    # achieved: the step's algorithmic flops over its HIP-event duration in
-    # the timed region (every GEMM launch of the step, split-K reduces
-    # included; the GEMMs start with a cold L2, unlike the per-shape repeats).
-    achieved = step_flops / (ev_ms / args.steps) / 1e9
+    for i, (name, M, N, K_) in enumerate(ENC_SHAPES):
+        a = x if K_ == 1280 else h
+
+        def one_shape(st, i=i, a=a, M=M, N=N, K_=K_):
+            for li in range(L):
+                _abi.gemm_dev(_abi.FMT_F32, M, N, K_, a.data_ptr(), wdev[li][i].data_ptr(), outs[i].data_ptr(),
+                              stream=st)
+
+        ms = timer.time_ms(one_shape, 5, per_replay=L)
+        per_shape[name] = {"M": M, "N": N, "K": K_, "us": round(ms * 1e3, 2),
+                           "tflops": round(2.0 * M * N * K_ / ms / 1e9, 2)}
+    achieved = sweep_flops / (ev_ms / K) / 1e9
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": traffic_per_step(),
-                "algorithmic_bytes": int(sum(4 * (M * K + K * N + M * N) for (_, M, N, K) in XLMR_SHAPES)),
-                "kernel": "gemm_dma_kernel<f32 B> (32x64 tiles; BK 32 for QKV and FFN-up, BK 64 with two wave "
-                          "groups along K for out and FFN-down), v_mfma_f32_16x16x4_f32",
-                "per_shape": per_shape, "per_shape_sum_tflops": round(tot_fl / tot_ms / 1e9, 2),
-                "per_shape_note": "each shape timed as 20 back-to-back launches (L2 warm)"}
+                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": traffic_per_sweep(),
+                "algorithmic_bytes": int(L * sum(4 * (M * K_ + K_ * N + M * N) for (_, M, N, K_) in ENC_SHAPES)),
+                "kernel": "gemm_dma_kernel<f32 B> (128x64 tiles, 8 waves, BK 32, three LDS stages; FFN-down K "
+                          "split 2 + splitk_reduce_kernel), v_mfma_f32_16x16x4_f32",
+                "per_unit": "2*M*N*K flop per GEMM launch; 96 launches per sweep",
+                "per_shape": per_shape}
     log(f"roofline: {json.dumps(roofline)}")
 
     result = {
@@ -256,7 +314,7 @@ def main():
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": K,
         "warmup": args.warmup,
         "extra_warmup_steps": extra_warmup,
         "ms_per_step": round(ms_per_step, 5),
@@ -264,37 +322,185 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (SplitMix64/Box-Muller, X~N(0,1), W~N(0,0.02))",
-        "config": {"workload": "XLM-R-large layer linears, seq=512, fp32: 512x1024.1024x3072, "
-                               "512x1024.1024x1024, 512x1024.1024x4096, 512x4096.4096x1024",
+        "data": "synthetic (SplitMix64/Box-Muller: X~N(0,1) seed 1001, H~N(0,1) seed 1002, "
+                "W~N(0,0.02) seed 2002+layer)",
+        "config": {"workload": f"config 5: Whisper large-v3-turbo encoder linears, fp32, {L}-layer sweep "
+                               f"(1500x1280.1280x3840, 1500x1280.1280x5120, 1500x5120.5120x1280 per layer, "
+                               f"own weights per layer)",
                    "parallelism": "single GPU"},
         "max_rel_err_vs_f64": max_rel,
+        "batches": {"n": nb, "per_batch": batch, "median_TFLOP/s": med},
         "roofline": roofline,
     }
 
     if not args.no_extras:
+        result["config5_q"] = bench_config5_quant(torch, dev, sptr, _abi, wdev, x, h, outs, L)
+    del wdev
+    torch.cuda.empty_cache()
+    if not args.no_extras:
+        result["config2"] = bench_config2(torch, dev, sptr, timer, _abi, synth, args)
         result["gemv"] = bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np)
         result["qgemm"] = bench_qgemm(torch, dev, sptr, timer, _abi, synth, np)
         result["config1"] = bench_config1(torch, dev, sptr, timer, _abi, synth, np)
-        result["config5"] = bench_config5(torch, dev, sptr, _abi, layers=args.config5_layers)
         result["sentence_transformer"] = bench_sentence_transformer(torch, dev, sptr, timer, _abi, synth)
+        result["host_pointer"] = bench_host_pointer(_abi, synth, np)
 
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, host_w, host_x, host_h,
+                                              quantized=not args.no_extras)
+        if not args.no_extras:
+            attach_cpu_quantized(result)
 
     print(json.dumps(result), flush=True)
 
 
-def traffic_per_step():
-    """HBM bytes per headline step from the committed rocprofv3 PMC summary
+def traffic_per_sweep():
+    """HBM bytes per headline sweep from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a plain copy kernel),
     or None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "gemm_xlmr_traffic.json")
+    path = os.path.join(ROOT, "profiles", "gemm_whisper_encoder_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_step")
+            return json.load(f).get("hbm_bytes_per_sweep")
     except (OSError, ValueError):
         return None
+
+
+def bench_config5_quant(torch, dev, sptr, _abi, wdev, x, h, outs, layers):
+    """Config 5 with Q8_0 and Q4_0 weights: the headline's fp32 weights
+    quantized on the device by the reference quantizer (per tensor), then
+    the same sweep (graph of 96 launches, replays timed with HIP events)."""
+    res = {}
+    flops = layers * sum(2.0 * M * N * K for (_, M, N, K) in ENC_SHAPES)
+    for fmt, name in ((_abi.FMT_Q8_0, "q8_0"), (_abi.FMT_Q4_0, "q4_0")):
+        rows, keep = [], []
+        for li in range(layers):
+            row = []
+            for i, (_, M, N, K) in enumerate(ENC_SHAPES):
+                nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+                q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+                sc = torch.empty(1, dtype=torch.float32, device=dev)
+                _abi.quantize_dev(fmt, K * N, wdev[li][i].data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
+                keep.append((q, sc))
+                row.append((q.data_ptr(), sc))
+            rows.append(row)
+        torch.cuda.synchronize()
+        rows = [[(p, float(s.item())) for (p, s) in row] for row in rows]
+
+        def sweep(st, rows=rows, fmt=fmt):
+            for row in rows:
+                for i, (_, M, N, K) in enumerate(ENC_SHAPES):
+                    a = x if K == 1280 else h
+                    p, sc = row[i]
+                    _abi.gemm_dev(fmt, M, N, K, a.data_ptr(), p, outs[i].data_ptr(), scale=sc, stream=st)
+
+        ms = Timer(torch, settle_s=0.5).time_ms(sweep, 5)
+        tf = flops / (ms * 1e-3) / 1e12
+        wbytes = layers * sum((K * N if fmt == _abi.FMT_Q8_0 else K * N // 2) for (_, M, N, K) in ENC_SHAPES)
+        res[name] = {"ms_per_sweep": round(ms, 3), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4),
+                     "weight_bytes": wbytes}
+        log(f"config5 {name}: {layers} layers, {ms:.2f} ms/sweep, {tf:.1f} TFLOP/s")
+        del keep, rows
+        torch.cuda.empty_cache()
+    res["flops_per_sweep"] = flops
+    res["layers"] = layers
+    return res
+
+
+def bench_config2(torch, dev, sptr, timer, _abi, synth, args):
+    """Config 2: the four XLM-R-large layer linears at seq 512 in fp32 (QKV,
+    out, FFN-up, FFN-down), one step = the four back to back, K steps
+    captured as one graph and replayed; plus each shape as 20 back-to-back
+    launches."""
+    x = torch.from_numpy(synth.normal_matrix(1001, 512, 1024)).to(dev)
+    hh = torch.from_numpy(synth.normal_matrix(1001, 512, 4096)).to(dev)
+    ws = [torch.from_numpy(synth.normal_matrix(2002 + i, K, N, 0.02)).to(dev)
+          for i, (_, M, N, K) in enumerate(XLMR_SHAPES)]
+    outs = [torch.empty((M, N), dtype=torch.float32, device=dev) for (_, M, N, K) in XLMR_SHAPES]
+    ins = [x, x, x, hh]
+    step_flops = sum(2.0 * M * N * K for (_, M, N, K) in XLMR_SHAPES)
+    launches = []
+    for i, (name, M, N, K) in enumerate(XLMR_SHAPES):
+        a_p, b_p, c_p = ins[i].data_ptr(), ws[i].data_ptr(), outs[i].data_ptr()
+        launches.append((name, M, N, K, lambda st, M=M, N=N, K=K, a_p=a_p, b_p=b_p, c_p=c_p:
+                         _abi.gemm_dev(_abi.FMT_F32, M, N, K, a_p, b_p, c_p, stream=st)))
+    steps = 200
+    ms = timer.time_ms(lambda st: [fn(st) for _ in range(steps) for (_, _, _, _, fn) in launches], 3,
+                       per_replay=steps)
+    max_rel = 0.0
+    for i, (name, M, N, K) in enumerate(XLMR_SHAPES):
+        ref = ins[i].double() @ ws[i].double()
+        max_rel = max(max_rel, float((outs[i].double() - ref).abs().max() / ref.abs().max()))
+    per_shape = {}
+    for (name, M, N, K, fn) in launches:
+        ms_s = timer.time_ms(lambda st, fn=fn: [fn(st) for _ in range(20)], 5, per_replay=20)
+        per_shape[name] = {"M": M, "N": N, "K": K, "us": round(ms_s * 1e3, 2),
+                           "tflops": round(2.0 * M * N * K / ms_s / 1e9, 2)}
+    tf = step_flops / ms / 1e9
+    log(f"config2 (XLM-R layer, seq 512): {ms * 1e3:.1f} us/step, {tf:.2f} TFLOP/s, max rel err {max_rel:.2e}")
+    return {"us_per_step": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4),
+            "max_rel_err_vs_f64": max_rel, "steps_per_graph": steps, "per_shape": per_shape,
+            "per_shape_note": "each shape timed as 20 back-to-back launches (L2 warm)"}
+
+
+def bench_host_pointer(_abi, synth, np):
+    """The drop-in as the Zig shim calls it (src/core/ops.zig:266-275): host
+    slices in and out, every call synchronous.  A registered weight stays
+    resident (tml_hip_weight_register), so a call moves A up and C down over
+    PCIe; an unregistered one uploads B too.  Per call, averaged over 10
+    calls after 2 warm-up calls."""
+    res = {}
+
+    def timed(fn, n=10):
+        for _ in range(2):
+            fn()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        return (time.perf_counter() - t0) / n * 1e3
+
+    # config 2 step through tml_hip_sgemm (registered weights)
+    xs = synth.normal_matrix(1001, 512, 1024)
+    hs = synth.normal_matrix(1001, 512, 4096)
+    wts = [synth.normal_matrix(2002 + i, K, N, 0.02) for i, (_, M, N, K) in enumerate(XLMR_SHAPES)]
+    cs = [np.zeros((M, N), np.float32) for (_, M, N, K) in XLMR_SHAPES]
+    ins = [xs, xs, xs, hs]
+    step_flops = sum(2.0 * M * N * K for (_, M, N, K) in XLMR_SHAPES)
+
+    def step():
+        for i, (_, M, N, K) in enumerate(XLMR_SHAPES):
+            _abi.sgemm(M, N, K, ins[i], wts[i], cs[i])
+
+    ms_unreg = timed(step, 5)
+    for w in wts:
+        _abi.weight_register(w)
+    try:
+        ms_reg = timed(step)
+    finally:
+        for w in wts:
+            _abi.weight_release(w)
+    pcie = sum(4 * (M * K + M * N) for (_, M, N, K) in XLMR_SHAPES)
+    res["config2_sgemm"] = {
+        "registered": {"ms_per_step": round(ms_reg, 3), "TFLOP/s": round(step_flops / ms_reg / 1e9, 2),
+                       "pcie_bytes_per_step": pcie},
+        "unregistered": {"ms_per_step": round(ms_unreg, 3), "TFLOP/s": round(step_flops / ms_unreg / 1e9, 2),
+                         "pcie_bytes_per_step": pcie + sum(4 * K * N for (_, M, N, K) in XLMR_SHAPES)}}
+    log(f"host-pointer config2 step: {ms_reg:.2f} ms registered, {ms_unreg:.2f} ms unregistered")
+    # config 1 through tml_hip_sgemm_bias (registered weight)
+    a = synth.normal_matrix(1001, 1500, 384)
+    w = synth.normal_matrix(2002, 384, 1536, 0.02)
+    b = synth.normal(3003, 1536, 0.0, 0.02)
+    c = np.zeros((1500, 1536), np.float32)
+    _abi.weight_register(w)
+    try:
+        ms1 = timed(lambda: _abi.sgemm_bias(1500, 1536, 384, a, w, b, c))
+    finally:
+        _abi.weight_release(w)
+    res["config1_sgemm_bias"] = {"registered": {"ms_per_call": round(ms1, 3),
+                                                "TFLOP/s": round(2.0 * 1500 * 1536 * 384 / ms1 / 1e9, 2),
+                                                "pcie_bytes_per_call": 4 * (1500 * 384 + 1500 * 1536 + 1536)}}
+    log(f"host-pointer config1 sgemm_bias: {ms1:.3f} ms per call")
+    return res
 
 
 def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
@@ -306,12 +512,19 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
     M -- and "kn" -- the weight in the reference's [K,N] layout, per call.
     Algorithmic bytes per launch = weight bytes + scale bytes (4, or 4*N for
     the per-column formats) + 4*M*K + 4*M*N.
-    Each timed pass walks >= 1 GB of distinct weight copies, so neither L2
-    nor the 256 MB Infinity Cache serves them."""
+    Each timed pass walks >= 1 GiB of distinct weight copies, so neither L2
+    nor the 256 MB Infinity Cache serves them.  Beside each: the floor for
+    the same weight bytes over the same rotation (torch's device copy of
+    them; torch's read-only row reduction is listed too and is slower) and
+    the GEMV's time as a fraction of it ("frac_of_floor" = floor / GEMV
+    time)."""
     out = {}
     rot_bytes = 1 << 30
 
-    def run(fmt, K, N, Ms, seed, label, max_copies=256):
+    def copies_for(nbytes):
+        return max(2, -(-rot_bytes // nbytes))  # >= 1 GiB of distinct copies
+
+    def run(fmt, K, N, Ms, seed, label):
         w = synth.normal_matrix(seed, K, N, 0.02)
         wt = torch.from_numpy(w).to(dev)
         cols = fmt in (_abi.FMT_Q8_0_PC, _abi.FMT_Q4_0_PC)
@@ -326,7 +539,7 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
         torch.cuda.synchronize()
         scale = 1.0 if cols else float(sc.item())
         sc_ptr = sc.data_ptr() if cols else None
-        ncopy = min(max_copies, max(2, rot_bytes // wbytes))
+        ncopy = copies_for(wbytes)
         copies = q.repeat(ncopy).view(ncopy, wbytes)
         del wt
         ptrs = [copies[i].data_ptr() for i in range(ncopy)]
@@ -348,11 +561,15 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
                 for h in handles:
                     _abi.gemm_prepared(h, M, x.data_ptr(), y.data_ptr(), stream=st)
 
+            floor_us = read_floor(wbytes)
+            entry["floor_us"] = floor_us
             for name, fn in (("prepared", prep), ("kn", kn)):
                 ms = timer.time_ms(fn, 3, per_replay=ncopy)
                 gbs = alg / (ms * 1e-3) / 1e9
-                entry[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
-                log(f"gemv {label} M={M} {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+                entry[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                               "frac_of_floor": round(floor_us / (ms * 1e3), 4)}
+                log(f"gemv {label} M={M} {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s "
+                    f"({floor_us / (ms * 1e3):.2f} of the copy floor)")
             res[f"M{M}"] = entry
         for h in handles:
             _abi.prepared_free(h)
@@ -391,12 +608,44 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
         torch.cuda.empty_cache()
         return res
 
+    floors = {}
+
+    def read_floor(nbytes):
+        # Floors for a launch that streams `nbytes` of weights, over the same
+        # >= 1 GiB rotation of distinct buffers the GEMVs use: torch's own
+        # fastest memory operation at that size, a device copy of the same
+        # bytes (nbytes read and nbytes written: no slower a floor than a
+        # pure read would be), and torch's read-only row reduction
+        # (nbytes read, 1/256 of it written).  Returns the copy time.
+        if nbytes in floors:
+            return floors[nbytes]["copy_us"]
+        nb4 = -(-nbytes // 1024) * 256  # floats, a multiple of 256
+        ncopy = copies_for(4 * nb4)
+        src = torch.ones((ncopy, nb4), dtype=torch.float32, device=dev)
+        dst = torch.empty((ncopy, nb4), dtype=torch.float32, device=dev)
+
+        def cp(st):
+            for i in range(ncopy):
+                dst[i].copy_(src[i])
+
+        def rd(st):
+            for i in range(ncopy):
+                torch.sum(src[i].view(-1, 256), dim=1, out=dst[i, : nb4 // 256])
+
+        ms_c = timer.time_ms(cp, 3, per_replay=ncopy)
+        ms_r = timer.time_ms(rd, 3, per_replay=ncopy)
+        del src, dst
+        torch.cuda.empty_cache()
+        floors[nbytes] = {"copy_us": round(ms_c * 1e3, 3), "row_sum_us": round(ms_r * 1e3, 3)}
+        log(f"floors for {nbytes} B: torch copy {ms_c * 1e3:.2f} us, torch row sum {ms_r * 1e3:.2f} us")
+        return floors[nbytes]["copy_us"]
+
     def copy_floor(nbytes):
         # Context for the decoder shapes: torch's own device copy moving
         # 2 * nbytes per launch (nbytes read, nbytes written), rotating over
         # >= 1 GB like the GEMVs.  A launch that moves a few MB costs this
         # much on MI355X whatever it computes.
-        ncopy = min(256, max(2, rot_bytes // nbytes))
+        ncopy = copies_for(nbytes)
         src = torch.empty((ncopy, nbytes), dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
 
@@ -421,9 +670,11 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
     # and the same for the int4 pair's first shape (Q4_0_PC)
     out["q8pc_1024x4096"] = run(_abi.FMT_Q8_0_PC, 1024, 4096, [1, 8], 2002, "q8pc 1024x4096")
     out["q4pc_1280x5120"] = run(_abi.FMT_Q4_0_PC, 1280, 5120, [1, 4], 2002, "q4pc 1280x5120")
-    out["f32_vocab_rows_51866x1280"] = run_rows_f32(51866, 1280, [1, 4], 2004, "f32 vocab rows 51866x1280", 4)
-    out["q8_vocab_1280x51866"] = run(_abi.FMT_Q8_0, 1280, 51866, [1], 2004, "q8 vocab 1280x51866", 12)
-    out["q4_vocab_1280x51866"] = run(_abi.FMT_Q4_0, 1280, 51866, [1], 2004, "q4 vocab 1280x51866", 24)
+    out["f32_vocab_rows_51866x1280"] = run_rows_f32(51866, 1280, [1, 4], 2004, "f32 vocab rows 51866x1280",
+                                                    copies_for(4 * 51866 * 1280))
+    out["q8_vocab_1280x51866"] = run(_abi.FMT_Q8_0, 1280, 51866, [1], 2004, "q8 vocab 1280x51866")
+    out["q4_vocab_1280x51866"] = run(_abi.FMT_Q4_0, 1280, 51866, [1], 2004, "q4 vocab 1280x51866")
+    out["floors_by_weight_bytes"] = {str(k): v for k, v in floors.items()}
     return out
 
 
@@ -583,124 +834,112 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
     print(json.dumps({"profile_gemv": True}), flush=True)
 
 
-def bench_config5(torch, dev, sptr, _abi, layers: int = 32):
-    """Config 5: the Whisper large-v3-turbo encoder linears at 1500 frames --
-    X[1500x1280] . W[1280x3840] (fused QKV), X . W[1280x5120] (FFN up),
-    H[1500x5120] . W[5120x1280] (FFN down) -- for each of `layers` layers with
-    their own weights, back to back, in fp32 and as Q8_0 / Q4_0 weights
-    (quantized on the device by the reference quantizer).  Weights are drawn
-    on the GPU (seeded N(0, 0.02)); X, H ~ N(0, 1).  The fp32 sweep streams
-    2.3 GB of weights, more than the 256 MB Infinity Cache."""
-    shapes = [(1500, 3840, 1280), (1500, 5120, 1280), (1500, 1280, 5120)]
-    flops = layers * sum(2.0 * M * N * K for (M, N, K) in shapes)
-    g = torch.Generator(device=dev)
-    g.manual_seed(1001)
-    x = torch.randn(1500, 1280, generator=g, device=dev)
-    h = torch.randn(1500, 5120, generator=g, device=dev)
-    outs = [torch.empty(M, N, device=dev) for (M, N, K) in shapes]
+def cpu_baseline(budget_s: float, host_w, host_x, host_h, quantized: bool = True):
+    """The reference's CPU path on a bounded sample of the headline workload:
+    the oracle's restatement of the register-blocked ops.zig:277-414 fallback
+    (the reference's fp32 path without zblas), single-threaded as in the
+    reference, over whole config-5 layers (three GEMMs, 54 GFLOP each) until
+    about `budget_s` seconds are spent; then the same loops row-parallel with
+    the reference's matmulParallel cap of 4 threads (src/core/context.zig:285)
+    and with every host thread.  With `quantized`, also the reference's
+    weight-only loops (quantization.zig:240-311 Q8_0, :829-957 Q4_0) at the
+    config-3 and config-4 shapes."""
+    from oracle import oracle as orc
+
+    orc.lib()
+    layer_flops = sum(2.0 * M * N * K for (_, M, N, K) in ENC_SHAPES)
+
+    def run_layer(li, nt):
+        for i, (_, M, N, K) in enumerate(ENC_SHAPES):
+            a = host_x if K == 1280 else host_h
+            if nt == 1:
+                orc.matmul(a, host_w[li][i])
+            else:
+                orc.matmul_mt(a, host_w[li][i], nt)
+
+    def sample(nt, budget):
+        n, t = 0, 0.0
+        while (t < budget or n == 0) and n < len(host_w):
+            t0 = time.perf_counter()
+            run_layer(n, nt)
+            t += time.perf_counter() - t0
+            n += 1
+        return n, t
+
+    n1, t1 = sample(1, budget_s)
+    tf = layer_flops * n1 / t1 / 1e12
+    log(f"cpu baseline: {n1} config-5 layers in {t1:.1f} s, {tf * 1e3:.2f} GFLOP/s (1 thread)")
+    threaded = {}
+    for nt in sorted({4, max(1, orc.max_threads())}):
+        n, t = sample(nt, budget_s / 4)
+        threaded[f"{nt}_threads"] = {"value": round(layer_flops * n / t / 1e12, 6), "layers": n,
+                                     "seconds": round(t, 2)}
+        log(f"cpu baseline, {nt} threads: {n} layers in {t:.1f} s, {layer_flops * n / t / 1e9:.2f} GFLOP/s")
+    out = {"value": round(tf, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+           "sample": f"{n1} of the {len(host_w)} config-5 layers (3 GEMMs, {layer_flops / 1e9:.1f} GFLOP each, the "
+                     f"headline's own inputs) with the oracle's restatement of the ops.zig:277-414 fallback, "
+                     f"1 thread, -O3 AVX2, {t1:.1f} s; zblas (the reference default) is not vendored and "
+                     f"cannot be timed, OpenBLAS is not installed",
+           "host_cpus": os.cpu_count(), "threaded": threaded}
+    if quantized:
+        out["quantized"] = cpu_quantized(orc)
+    return out
+
+
+def cpu_quantized(orc):
+    """The reference's weight-only loops at configs 3 and 4, on the oracle's
+    restatement (i, k, j order, f32(q) * scale per element): Q8_0 W[1024x4096]
+    at M in {1, 8, 128, 512}; Q4_0 W[1280x5120] and W[5120x1280] at M in
+    {1, 4, 8}.  1 thread (the reference's Q4_0 loop is always
+    single-threaded) and 4 threads (rows split; the reference's cap).  Each
+    timed for at least 0.2 s."""
+    from tomoul_amd import synth
+
+    def tm(fn):
+        n, t = 0, 0.0
+        while t < 0.2:
+            t0 = time.perf_counter()
+            fn()
+            t += time.perf_counter() - t0
+            n += 1
+        return round(t / n * 1e6, 1)
+
     res = {}
-    for fmt, name in ((_abi.FMT_F32, "fp32"), (_abi.FMT_Q8_0, "q8_0"), (_abi.FMT_Q4_0, "q4_0")):
-        weights = []  # per layer: [(ptr, scale)] and the tensors that own them
-        keep = []
-        for layer in range(layers):
-            g.manual_seed(2002 + layer)
-            row = []
-            for (M, N, K) in shapes:
-                w = torch.randn(K, N, generator=g, device=dev) * 0.02
-                if fmt == _abi.FMT_F32:
-                    keep.append(w)
-                    row.append((w.data_ptr(), 1.0))
-                    continue
-                nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
-                q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-                sc = torch.empty(1, dtype=torch.float32, device=dev)
-                _abi.quantize_dev(fmt, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
-                keep.append((q, sc))
-                row.append((q.data_ptr(), sc))
-                del w
-            weights.append(row)
-        torch.cuda.synchronize()
-        weights = [[(p, s if isinstance(s, float) else float(s.item())) for (p, s) in row] for row in weights]
-
-        def sweep():
-            for row in weights:
-                for i, (M, N, K) in enumerate(shapes):
-                    a = x if K == 1280 else h
-                    p, sc = row[i]
-                    _abi.gemm_dev(fmt, M, N, K, a.data_ptr(), p, outs[i].data_ptr(), scale=sc, stream=sptr)
-
-        # warm-up: workspaces, then sweeps until the clocks have settled
-        t_end = time.perf_counter() + 0.3
-        sweep()
-        torch.cuda.synchronize()
-        while time.perf_counter() < t_end:
-            sweep()
-            torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 3
-        e0.record()
-        for _ in range(reps):
-            sweep()
-        e1.record()
-        e1.synchronize()
-        ms = e0.elapsed_time(e1) / reps
-        tf = flops / (ms * 1e-3) / 1e12
-        wbytes = sum((K * N * 4 if fmt == _abi.FMT_F32 else (K * N if fmt == _abi.FMT_Q8_0 else K * N // 2))
-                     for (M, N, K) in shapes) * layers
-        res[name] = {"ms_per_sweep": round(ms, 3), "TFLOP/s": round(tf, 2), "frac": round(tf / FP32_PEAK_TFLOPS, 4),
-                     "weight_bytes": wbytes}
-        log(f"config5 {name}: {layers} layers, {ms:.2f} ms/sweep, {tf:.1f} TFLOP/s")
-        del keep, weights
-        torch.cuda.empty_cache()
-    res["flops_per_sweep"] = flops
-    res["layers"] = layers
+    w = synth.normal_matrix(2002, 1024, 4096, 0.02)
+    q, s = orc.quantize_q8(w)
+    q = q.reshape(1024, 4096)
+    for M in (1, 8, 128, 512):
+        a = synth.normal_matrix(1001, M, 1024)
+        res[f"q8_1024x4096_M{M}"] = {"1_thread_us": tm(lambda: orc.matmul_q8(a, q, s)),
+                                     "4_threads_us": tm(lambda: orc.matmul_q8_mt(a, q, s, 4))}
+    for (K, N, seed) in ((1280, 5120, 2002), (5120, 1280, 2003)):
+        w = synth.normal_matrix(seed, K, N, 0.02)
+        p, s4 = orc.quantize_q4(w)
+        for M in (1, 4, 8):
+            a = synth.normal_matrix(1001, M, K)
+            res[f"q4_{K}x{N}_M{M}"] = {"1_thread_us": tm(lambda: orc.matmul_q4(a, p, K, N, s4)),
+                                       "4_threads_us": tm(lambda: orc.matmul_q4_mt(a, p, K, N, s4, 4))}
+    for k, v in res.items():
+        log(f"cpu baseline {k}: {v['1_thread_us']:.0f} us (1 thread), {v['4_threads_us']:.0f} us (4 threads)")
     return res
 
 
-def cpu_baseline(budget_s: float):
-    """The reference's fp32 CPU path (oracle restatement of the register-
-    blocked ops.zig fallback, single-threaded as in the reference) on the
-    headline step; repeated until about `budget_s` seconds are spent."""
-    from oracle import oracle as orc
-    from tomoul_amd import synth
-
-    xs = synth.normal_matrix(1001, 512, 1024)
-    hs = synth.normal_matrix(1001, 512, 4096)
-    wts = [synth.normal_matrix(2002 + i, K, N, 0.02) for i, (_, M, N, K) in enumerate(XLMR_SHAPES)]
-    ins = [xs, xs, xs, hs]
-    step_flops = sum(2.0 * M * N * K for (_, M, N, K) in XLMR_SHAPES)
-    orc.lib()
-    steps, t_tot = 0, 0.0
-    while t_tot < budget_s and steps < 50:
-        t0 = time.perf_counter()
-        for i in range(4):
-            orc.matmul(ins[i], wts[i])
-        t_tot += time.perf_counter() - t0
-        steps += 1
-    tf = step_flops * steps / t_tot / 1e12
-    log(f"cpu baseline: {steps} steps in {t_tot:.1f} s, {tf * 1e3:.2f} GFLOP/s (1 thread)")
-    # The same loops row-parallel (rows are independent, results bitwise
-    # unchanged) with the reference's matmulParallel cap of 4 threads
-    # (src/core/context.zig:285) and with every host thread the oracle's
-    # OpenMP runtime offers; a few steps each, reported beside the baseline.
-    threaded = {}
-    for nt in sorted({4, max(1, orc.max_threads())}):
-        n_mt, t_mt = 0, 0.0
-        while t_mt < budget_s / 4 and n_mt < 50:
-            t0 = time.perf_counter()
-            for i in range(4):
-                orc.matmul_mt(ins[i], wts[i], nt)
-            t_mt += time.perf_counter() - t0
-            n_mt += 1
-        threaded[f"{nt}_threads"] = {"value": round(step_flops * n_mt / t_mt / 1e12, 6), "steps": n_mt,
-                                     "seconds": round(t_mt, 2)}
-        log(f"cpu baseline, {nt} threads: {n_mt} steps in {t_mt:.1f} s, "
-            f"{step_flops * n_mt / t_mt / 1e9:.2f} GFLOP/s")
-    return {"value": round(tf, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{steps} full headline steps (4 GEMMs, {step_flops / 1e9:.2f} GFLOP each) with the "
-                      f"oracle's restatement of the ops.zig:277-414 fallback, 1 thread, -O3 AVX2, "
-                      f"{t_tot:.1f} s; zblas (the reference default) is not vendored and cannot be timed",
-            "host_cpus": os.cpu_count(), "threaded": threaded}
+def attach_cpu_quantized(result):
+    """Puts each quantized CPU figure beside the GPU entry of the same shape."""
+    cq = result.get("cpu_baseline", {}).get("quantized", {})
+    for key, v in cq.items():
+        name, m = key.rsplit("_M", 1)
+        M = int(m)
+        if name.startswith("q8_") and M >= 128:
+            e = result.get("qgemm", {}).get(f"q8_M{M}")
+            gpu_us = e and e.get("us")
+        else:
+            e = result.get("gemv", {}).get(name, {}).get(f"M{M}")
+            gpu_us = e and e.get("prepared", {}).get("us")
+        if e is not None:
+            e["cpu"] = dict(v)
+            if gpu_us:
+                e["cpu"]["gpu_speedup_vs_1_thread"] = round(v["1_thread_us"] / gpu_us, 1)
 
 
 if __name__ == "__main__":
