@@ -221,6 +221,26 @@ int tml_hip_gemm_ex_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A
                         const float *scales, int64_t block, const float *bias, const float *residual, int act,
                         float *C, float alpha, float beta, void *stream);
 
+/* Allocation-free form of tml_hip_gemm_ex_dev.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments, same kernels and plans, same results bit for
+ * bit; the split-K scratch (partial sums, arrival counters and the zero
+ * block the kernels read out-of-range lanes from) is a static device array of
+ * TML_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load until the
+ * process ends, instead of the library's growable workspace.  The call makes
+ * no hipMalloc / hipFree.  Set-up -- looking up this GPU's address of the
+ * array and clearing its counters -- happens in tml_hip_init (or on the first
+ * call on a device, which must then not be under stream capture).
+ * A problem whose plan needs more scratch than the array holds is refused
+ * with TML_ERR_INVALID_SHAPE before any launch.  All calls on one GPU share
+ * its array: calls that overlap on one GPU (several streams, several host
+ * threads) race; issue them on one stream. */
+#define TML_NOALLOC_SCRATCH_BYTES (16u << 20)
+int tml_hip_gemm_ex_dev_noalloc(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                                const float *scales, int64_t block, const float *bias, const float *residual, int act,
+                                float *C, float alpha, float beta, void *stream);
+
 /* On-device quantizers, bit-identical to the reference's Zig quantizers
  * (quantizeQ8 quantization.zig:98-129, quantizeQ8K :406-446, quantizeQ4
  * :721-754) and its f32 -> f16 converter toF16 (:1907-1917, IEEE round to

@@ -59,6 +59,9 @@ pub extern "c" fn tml_hip_weight_release(host: *const anyopaque) c_int;
 // ----------------------------------------------- device-pointer API
 pub extern "c" fn tml_hip_gemm_dev(fmt: c_int, M: i64, N: i64, K: i64, A: [*]const f32, B: *const anyopaque, scale: f32, scales: ?[*]const f32, block: i64, bias: ?[*]const f32, C: [*]f32, alpha: f32, beta: f32, stream: ?*anyopaque) c_int;
 pub extern "c" fn tml_hip_gemm_ex_dev(fmt: c_int, M: i64, N: i64, K: i64, A: [*]const f32, B: *const anyopaque, scale: f32, scales: ?[*]const f32, block: i64, bias: ?[*]const f32, residual: ?[*]const f32, act: c_int, C: [*]f32, alpha: f32, beta: f32, stream: ?*anyopaque) c_int;
+/// The allocation-free form of tml_hip_gemm_ex_dev (static split-K scratch of
+/// TML_NOALLOC_SCRATCH_BYTES per GPU; for code under graph capture).
+pub extern "c" fn tml_hip_gemm_ex_dev_noalloc(fmt: c_int, M: i64, N: i64, K: i64, A: [*]const f32, B: *const anyopaque, scale: f32, scales: ?[*]const f32, block: i64, bias: ?[*]const f32, residual: ?[*]const f32, act: c_int, C: [*]f32, alpha: f32, beta: f32, stream: ?*anyopaque) c_int;
 pub extern "c" fn tml_hip_quantize_dev(fmt: c_int, n: i64, w: [*]const f32, q: *anyopaque, scales: ?[*]f32, stream: ?*anyopaque) c_int;
 pub extern "c" fn tml_hip_quantize_cols_dev(fmt: c_int, K: i64, N: i64, w: [*]const f32, q: *anyopaque, scales: [*]f32, stream: ?*anyopaque) c_int;
 pub extern "c" fn tml_hip_quantize_cols(fmt: c_int, K: i64, N: i64, w: [*]const f32, q: *anyopaque, scales: [*]f32) c_int;

@@ -12,7 +12,7 @@
 //          host     tml_hip_gemm_act (host-pointer path, staging and copies)
 //          quant    tml_hip_quantize_dev over K*N elements (cols: tml_hip_quantize_cols_dev)
 //          treq     tml_hip_transpose_requant_dev of a [K, N] tensor
-//          noalloc  tml_hip_gemm_ex_dev_noalloc (when the library exports it)
+//          noalloc  tml_hip_gemm_ex_dev_noalloc
 //          tlfile   the .tl file named by the flags field: open it, list it, and
 //                   read every tensor with every getter to host memory, to the
 //                   device and dequantized (errors are expected for most)
@@ -21,8 +21,6 @@
 //          harness must report it)
 //   NAME=VALUE  environment for this case only (the library's tuning overrides)
 // Output: "ok <line>" or "err <code> <message> <line>" per case; exit 0.
-#include <dlfcn.h>
-
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -144,11 +142,7 @@ int run_case(const std::string &op, int fmt, int64_t M, int64_t N, int64_t K, co
         if (op == "gemm") {
             rc = tml_hip_gemm_ex_dev(fmt, M, N, K, A, B, 0.01f, S, 32, bias, res, act, C, 1.0f, beta, nullptr);
         } else if (op == "noalloc") {
-            typedef int (*fn_t)(int, int64_t, int64_t, int64_t, const float *, const void *, float, const float *,
-                                int64_t, const float *, const float *, int, float *, float, float, void *);
-            fn_t f = (fn_t)dlsym(RTLD_DEFAULT, "tml_hip_gemm_ex_dev_noalloc");
-            if (f == nullptr) return 1;
-            rc = f(fmt, M, N, K, A, B, 0.01f, S, 32, bias, res, act, C, 1.0f, beta, nullptr);
+            rc = tml_hip_gemm_ex_dev_noalloc(fmt, M, N, K, A, B, 0.01f, S, 32, bias, res, act, C, 1.0f, beta, nullptr);
         } else if (op == "prep" || op == "rows") {
             tml_prepared_t h = nullptr;
             if (op == "prep") {

@@ -235,3 +235,18 @@ def test_tl_parser_on_corrupted_files(emu, tmp_path):
     for g in files:
         if os.path.dirname(g) == os.path.join(HERE, "golden", "tl"):
             assert f"tlfile 0 0 0 0 {g}" in ok, g
+
+
+def test_noalloc_entry_point(emu):
+    # tml_hip_gemm_ex_dev_noalloc: its static scratch (partials, counters,
+    # zero block) serves the split-K GEMM, the split [K,N] GEMV and plain
+    # plans inside bounds; a plan needing more than the array is refused.
+    ok_cases = ["noalloc 0 256 512 4096 br TML_GEMM_SPLIT=4", "noalloc 0 96 256 2048 bt TML_GEMM_SPLIT=4",
+                "noalloc 1 4 1024 8192 b", "noalloc 1 3 512 4096 br", "noalloc 0 300 260 516 be",
+                "noalloc 17 6 1000 3000 b", "noalloc 2 8 640 5120 b", "noalloc 3 5 384 1536 b",
+                "noalloc 0 128 256 2048 b TML_GEMM_SPLIT=4 TML_GEMM_DMA_TILE=2 TML_GEMM_FUSED=1"]
+    outs, fails = run_cases(emu, ok_cases, workers=3)
+    assert not fails, fails
+    assert len(_ok_lines(outs)) == len(ok_cases), _err_lines(outs)
+    outs, fails = run_cases(emu, ["noalloc 0 512 1024 4096 - TML_GEMM_SPLIT=8"], workers=1)
+    assert not fails and len(_err_lines(outs)) == 1 and "static scratch" in _err_lines(outs)[0]

@@ -69,6 +69,8 @@ SIGNATURES = {
     "tml_hip_gemm_ex_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp,
                                            ctypes.c_int, _vp, _f, _f, _vp]),
     "tml_hip_gemm_prepared_ex": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, ctypes.c_int, _vp, _f, _f, _vp]),
+    "tml_hip_gemm_ex_dev_noalloc": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _i64, _vp, _vp, _f, _vp, _i64, _vp, _vp,
+                                                   ctypes.c_int, _vp, _f, _f, _vp]),
     "tml_hip_quantize_cols_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _vp, _vp, _vp]),
     "tml_hip_quantize_cols": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _vp, _vp]),
     "tml_hip_prepare_ex_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _f, _vp, _vp, ctypes.POINTER(_vp)]),
@@ -224,6 +226,15 @@ def gemm_ex_dev(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr:
                 stream: int | None = None) -> None:
     check(lib().tml_hip_gemm_ex_dev(fmt, m, n, k, a_ptr, b_ptr, scale, scales_ptr, block, bias_ptr, residual_ptr,
                                     act, c_ptr, alpha, beta, stream))
+
+
+def gemm_ex_dev_noalloc(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int, c_ptr: int, *,
+                        act: int = ACT_NONE, residual_ptr: int | None = None, scale: float = 1.0,
+                        scales_ptr: int | None = None, block: int = 32, bias_ptr: int | None = None,
+                        alpha: float = 1.0, beta: float = 0.0, stream: int | None = None) -> None:
+    """tml_hip_gemm_ex_dev_noalloc: gemm_ex_dev with the static split-K scratch (no device allocation)."""
+    check(lib().tml_hip_gemm_ex_dev_noalloc(fmt, m, n, k, a_ptr, b_ptr, scale, scales_ptr, block, bias_ptr,
+                                            residual_ptr, act, c_ptr, alpha, beta, stream))
 
 
 def quantize_dev(fmt: int, n: int, w_ptr: int, q_ptr: int, scales_ptr: int, stream: int | None = None) -> None:

@@ -5,6 +5,8 @@
 //   M >  8            -> gemm_mfma.hip (LDS-tiled fp32 MFMA, compute-bound)
 // The host-pointer entry points wrap the device-pointer one: upload operands
 // (or reuse a registered weight), launch, download C, synchronise.
+// tml_hip_gemm_ex_dev_noalloc is the device-pointer entry point for callers
+// that cannot allocate: its split-K scratch is a static device array.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -129,6 +131,8 @@ struct DeviceCtx {
 std::mutex g_mu;
 std::unordered_map<int, DeviceCtx *> g_ctx;
 
+Status scratch_setup(hipStream_t s, void **base);
+
 Status current_ctx(DeviceCtx **out) {
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
@@ -152,6 +156,10 @@ Status current_ctx(DeviceCtx **out) {
     if (zs.ok()) {
         e = hipMemset(c->zero.p, 0, kZeroBlockBytes);
         if (e != hipSuccess) zs = hip_status(e, "hipMemset");
+    }
+    if (zs.ok()) {
+        void *base = nullptr;
+        zs = scratch_setup(c->stream, &base);
     }
     if (!zs.ok()) {
         (void)hipStreamDestroy(c->stream);
@@ -275,6 +283,91 @@ Status gemm_dev(DeviceCtx *c, int fmt, int64_t M, int64_t N, int64_t K, const fl
     return launch_matmul(m, ws, s);
 }
 
+// ---------------------------------------------- allocation-free scratch
+// The split-K scratch of tml_hip_gemm_ex_dev_noalloc: a static device array
+// (each GPU holds its own copy, at its own address, for the life of the
+// process), never allocated or freed by the library.  Layout:
+//   [0, 256)                 zero block (kernels point out-of-range loads here; never written)
+//   [256, 256 + 64 KiB)      arrival counters, zero between launches
+//   [kScratchPartialOff, end) split-K partial sums
+// Host code uses the address hipGetSymbolAddress returns for the current
+// device, never the array's name.
+constexpr size_t kScratchBytes = TML_NOALLOC_SCRATCH_BYTES;
+constexpr size_t kScratchCounters = 16384;
+constexpr size_t kScratchPartialOff = 256 + kScratchCounters * sizeof(unsigned);
+static_assert(kScratchPartialOff % 256 == 0 && kScratchPartialOff < kScratchBytes, "scratch layout");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+struct ScratchSlot {
+    void *base = nullptr;  // this device's address of `scratch`
+    bool ready = false;
+};
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[kMaxScratchDevices];
+
+__global__ void zero_words_kernel(unsigned *p, unsigned long long n) {
+    const unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// Once per device, with that device current: look up the device's address
+// of `scratch` and clear its zero block and counters (a fill kernel on `s`,
+// waited for).  Allocates nothing.  Refused while `s` is being captured.
+Status scratch_setup(hipStream_t s, void **base) {
+    int dev = 0;
+    TML_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return Status::Err(TML_ERR_NO_DEVICE, "device id beyond the static scratch table");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    ScratchSlot &sl = g_scratch[dev];
+    if (!sl.ready) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        TML_HIP_TRY(hipStreamIsCapturing(s, &cap));
+        if (cap != hipStreamCaptureStatusNone)
+            return Status::Err(TML_ERR_INVALID_ARG,
+                               "the static scratch of this device is not set up: call tml_hip_init on the device "
+                               "(or make one call outside stream capture) first");
+        void *p = nullptr;
+        TML_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        const unsigned long long words = kScratchPartialOff / sizeof(unsigned);
+        zero_words_kernel<<<dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s>>>((unsigned *)p, words);
+        TML_HIP_TRY(hipGetLastError());
+        TML_HIP_TRY(hipStreamSynchronize(s));
+        sl.base = p;
+        sl.ready = true;
+    }
+    *base = sl.base;
+    return Status::Ok();
+}
+
+Status gemm_dev_noalloc(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B, float scale,
+                        const float *scales, int64_t block, const float *bias, float *C, float alpha, float beta,
+                        hipStream_t s, int act, const float *res) {
+    MatmulArgs m;
+    bool empty = false;
+    TML_TRY(matmul_args(fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, act, res, &m, &empty));
+    if (empty) return Status::Ok();
+    void *base = nullptr;
+    TML_TRY(scratch_setup(s, &base));
+    size_t pf = 0, nc = 0;
+    workspace_need(m, &pf, &nc);
+    const size_t cap_floats = (kScratchBytes - kScratchPartialOff) / sizeof(float);
+    if (pf > cap_floats || nc > kScratchCounters)
+        return Status::Err(TML_ERR_INVALID_SHAPE,
+                           "this problem's split-K plan needs " + std::to_string(pf * sizeof(float)) +
+                               " bytes of partial sums and " + std::to_string(nc) +
+                               " counters; the static scratch holds " + std::to_string(cap_floats * sizeof(float)) +
+                               " bytes and " + std::to_string(kScratchCounters) +
+                               " counters (TML_NOALLOC_SCRATCH_BYTES): use tml_hip_gemm_ex_dev");
+    m.zero = base;
+    Workspace ws;
+    ws.partials = (float *)((unsigned char *)base + kScratchPartialOff);
+    ws.partial_floats = cap_floats;
+    ws.counters = (unsigned *)((unsigned char *)base + 256);
+    ws.counter_count = kScratchCounters;
+    return launch_matmul(m, ws, s);
+}
 
 bool preparable_fmt(int fmt) {
     return fmt == TML_FMT_F32 || fmt == TML_FMT_F16 || fmt == TML_FMT_Q8_0 || fmt == TML_FMT_Q4_0 || per_channel(fmt);
@@ -659,6 +752,13 @@ int tml_hip_gemm_ex_dev(int fmt, int64_t M, int64_t N, int64_t K, const float *A
     if (!s.ok()) return report(s);
     return report(gemm_dev(c, fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta, (hipStream_t)stream,
                            act, residual));
+}
+
+int tml_hip_gemm_ex_dev_noalloc(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *B,
+                                float scale, const float *scales, int64_t block, const float *bias,
+                                const float *residual, int act, float *C, float alpha, float beta, void *stream) {
+    return report(gemm_dev_noalloc(fmt, M, N, K, A, B, scale, scales, block, bias, C, alpha, beta,
+                                   (hipStream_t)stream, act, residual));
 }
 
 int tml_hip_prepare_dev(int fmt, int64_t K, int64_t N, const void *B, float scale, void *stream,
