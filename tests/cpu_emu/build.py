@@ -46,10 +46,18 @@ def _kernel_start(text: str, end: int) -> int:
     i = end - 1
     while i >= 0 and text[i].isspace():
         i -= 1
-    if text[i] == ">":  # template-id: match the angle brackets backwards
-        depth = 0
+    if text[i] == ">":  # template-id: match the angle brackets backwards,
+        depth = 0       # skipping parenthesised template arguments whole
         while i >= 0:
-            if text[i] == ">":
+            if text[i] == ")":
+                par = 0
+                while i >= 0:
+                    par += text[i] == ")"
+                    par -= text[i] == "("
+                    if par == 0:
+                        break
+                    i -= 1
+            elif text[i] == ">":
                 depth += 1
             elif text[i] == "<":
                 depth -= 1

@@ -8,8 +8,9 @@
 // thread after another, with the real index arithmetic of the source.  Every
 // global-memory access is a host access to an allocation of exactly the
 // size the runtime asked hipMalloc for, so ASan reports any access outside
-// it; LDS arrays are static arrays, so an access outside one is reported as
-// well.  Buffer loads implement the hardware's range check (a dword at or
+// it; LDS arrays are static arrays and a launch's dynamic LDS is a heap
+// block of the size the launch asked for, so an access outside either is
+// reported as well.  Buffer loads implement the hardware's range check (a dword at or
 // past the resource's byte count reads zero, no access is made) and
 // report -- as an error -- a resource whose byte count exceeds the
 // allocation it points into.  LDS-DMA copies write lane `l`'s bytes at
@@ -32,6 +33,7 @@
 #include <cstring>
 #include <map>
 #include <type_traits>
+#include <vector>
 
 #define __global__
 #define __device__
@@ -162,15 +164,27 @@ inline hipError_t hipGetSymbolAddress(void **p, const void *sym) {
 }
 
 // ------------------------------------------------------------- launches
+// Dynamic LDS of the running launch: a heap block of exactly the bytes the
+// launch asked for, so an access past it is an ASan report.
+inline std::vector<char> *&tml_emu_dyn_buf() {
+    static std::vector<char> *b = nullptr;
+    return b;
+}
+inline void *tml_emu_dyn_lds() { return tml_emu_dyn_buf() ? tml_emu_dyn_buf()->data() : nullptr; }
+#define TML_DYNAMIC_LDS(T, v) T *const v = (T *)tml_emu_dyn_lds()
+
 template <typename... P>
 struct tml_emu_launcher {
     void (*k)(P...);
     dim3 g, b;
+    size_t shmem;
     template <typename... A>
     void operator()(A &&...args) const {
         ++tml_emu_launches;
         gridDim = g;
         blockDim = b;
+        std::vector<char> dyn(shmem);
+        tml_emu_dyn_buf() = shmem ? &dyn : nullptr;
         for (unsigned bz = 0; bz < g.z; ++bz)
             for (unsigned by = 0; by < g.y; ++by)
                 for (unsigned bx = 0; bx < g.x; ++bx) {
@@ -182,11 +196,12 @@ struct tml_emu_launcher {
                                 k(args...);
                             }
                 }
+        tml_emu_dyn_buf() = nullptr;
     }
 };
 template <typename... P>
-tml_emu_launcher<P...> tml_emu_launch(void (*k)(P...), dim3 g, dim3 b, size_t = 0, hipStream_t = nullptr) {
-    return {k, g, b};
+tml_emu_launcher<P...> tml_emu_launch(void (*k)(P...), dim3 g, dim3 b, size_t shmem = 0, hipStream_t = nullptr) {
+    return {k, g, b, shmem};
 }
 
 // ------------------------------------------------------------- device side
@@ -234,11 +249,18 @@ typedef uint32_t tml_emu_u32x2 __attribute__((ext_vector_type(2)));
 inline void __builtin_amdgcn_s_waitcnt(int) {}
 inline void __builtin_amdgcn_s_barrier() {}
 inline void __builtin_amdgcn_sched_barrier(int) {}
+inline void __builtin_amdgcn_wave_barrier() {}
+inline void __builtin_amdgcn_fence(int, const char *) {}
 template <typename T>
 inline T __builtin_amdgcn_readfirstlane(T v) {
     return v;
 }
 inline tml_emu_f32x4 __builtin_amdgcn_mfma_f32_16x16x4f32(float, float, tml_emu_f32x4 c, int, int, int) { return c; }
+typedef __bf16 tml_emu_bf16x8 __attribute__((ext_vector_type(8)));
+inline tml_emu_f32x4 __builtin_amdgcn_mfma_f32_16x16x32_bf16(tml_emu_bf16x8, tml_emu_bf16x8, tml_emu_f32x4 c, int, int,
+                                                            int) {
+    return c;
+}
 inline int __builtin_amdgcn_update_dpp(int, int src, int, int, int, bool) { return src; }
 inline int __builtin_amdgcn_ds_swizzle(int v, int) { return v; }
 

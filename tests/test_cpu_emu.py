@@ -101,6 +101,17 @@ def _default_cases():
             if fmt != Q8_K:
                 cs.append(f"prep {fmt} {M} 1000 {1030 if fmt not in (Q4_0, Q4_0_PC) else 1028} br")
                 cs.append(f"prep {fmt} {M} 130 4096 bt")
+        if fmt in (Q8_0, Q4_0, Q8_0_PC, Q4_0_PC):
+            # the matrix-core decoder GEMV: each workgroup width, chunk batch
+            # and staged row count, partial column tiles and partial rounds
+            for M in (2, 3, 5, 8):
+                cs.append(f"prep {fmt} {M} 4100 256 b")
+                cs.append(f"prep {fmt} {M} 2050 1280 br")
+                for nw in (1, 3, 5, 10, 16):
+                    for it in (1, 2, 4):
+                        for t in (1, 2):
+                            cs.append(f"prep {fmt} {M} 40 2080 b TML_GEMVTM_NW={nw} TML_GEMVTM_IT={it} "
+                                      f"TML_GEMVTM_T={t}")
         if fmt in (F32, F16, Q8_0, Q4_0):
             cs.append(f"rows {fmt} 3 777 260 b")
             cs.append(f"rows {fmt} 13 300 384 b")

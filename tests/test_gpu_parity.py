@@ -641,6 +641,63 @@ def test_prepared_lds_kernel(orc, cw):
                 os.environ[key] = v
 
 
+@pytest.mark.parametrize("nw,it,t", [(1, 1, 1), (3, 2, 2), (10, 1, 1), (10, 2, 2), (16, 4, 1), (5, 4, 2), (16, 1, 2)])
+def test_prepared_matrix_core_plans(orc, nw, it, t):
+    # The matrix-core decoder GEMV (Q8_0 / Q4_0, M >= 2) under forced plans:
+    # 1-16 waves, runs of 4 / 8 / 16 chunks, one or two 16-column tiles, on
+    # several superchunks (K = 4160: 4 of int8 plus a partial one, 2 of int4
+    # plus 2 chunks) and ragged N, with bias, beta and a residual-free
+    # epilogue.  The bound is 2e-5, not the 1e-3 of the quantized paths: the
+    # bf16 hi + lo split of an activation leaves 2^-17 of it, while a dropped
+    # lo term, a misplaced k or a swapped row costs 1e-3 or more.
+    keys = ("TML_GEMVTM", "TML_GEMVTM_NW", "TML_GEMVTM_IT", "TML_GEMVTM_T")
+    saved = {key: os.environ.get(key) for key in keys}
+    os.environ.update({"TML_GEMVTM": "2", "TML_GEMVTM_NW": str(nw), "TML_GEMVTM_IT": str(it),
+                       "TML_GEMVTM_T": str(t)})
+    try:
+        for (k, n) in [(4160, 70), (1280, 600)]:
+            w = rnd(201, k, n, 0.02)
+            q, s = orc.quantize_q8(w)
+            p, s4 = orc.quantize_q4(w)
+            bias = synth.normal(203, n, 0.0, 0.02)
+            for m in (2, 3, 5, 8):
+                a, c0 = rnd(204 + m, m, k), rnd(214 + m, m, n)
+                for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
+                                           (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
+                    got = _run_prepared(fmt, b, scale, k, n, m, a, bias=bias, c0=c0, alpha=0.75, beta=0.5)
+                    err = rel_err(got, 0.75 * ref + 0.5 * c0 + bias)
+                    assert err <= 2e-5, (k, n, m, fmt, err)
+    finally:
+        for key, v in saved.items():
+            if v is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = v
+
+
+@pytest.mark.parametrize("m", [3, 8])
+def test_prepared_matrix_core_inf(orc, m):
+    # Infinite and NaN activations through the matrix-core GEMV: each output
+    # is inf, -inf or nan exactly where the reference's fp32 product is, and
+    # the other rows are untouched.
+    k, n = 1280, 300
+    w = rnd(221, k, n, 0.02)
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    a = rnd(222, m, k)
+    a[1, 5] = np.inf
+    a[1, 700] = -np.inf
+    a[2, 9] = np.nan
+    for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
+                               (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
+        got = _run_prepared(fmt, b, scale, k, n, m, a)
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+        np.testing.assert_array_equal(np.isposinf(got), np.isposinf(ref))
+        np.testing.assert_array_equal(np.isneginf(got), np.isneginf(ref))
+        fin = np.isfinite(ref)
+        assert np.all(fin[0]) and rel_err(got[fin], ref[fin]) <= 2e-5, fmt
+
+
 def test_prepared_alpha_beta_and_inf(orc):
     k, n, m = 300, 200, 2
     w, a, c0 = rnd(161, k, n, 0.02), rnd(162, m, k), rnd(163, m, n)

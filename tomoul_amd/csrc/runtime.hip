@@ -422,7 +422,7 @@ Status gemm_prepared(DeviceCtx *c, const Prepared *p, int64_t M, const float *A,
     const float alpha_eff = (p->fmt == TML_FMT_Q8_0 || p->fmt == TML_FMT_Q4_0) ? alpha * p->scale : alpha;
     const long long tail0 = tml_act_tail0((long long)M * p->N);
     const int dfmt = data_fmt(p->fmt);
-    if (prepared_gemv_supported(dfmt, M, p->K) && (p->B == nullptr || prepared_gemv_preferred(dfmt, M)))
+    if (prepared_gemv_supported(dfmt, M, p->K) && (p->B == nullptr || prepared_gemv_preferred(dfmt, M, p->K)))
         return launch_gemv_t(dfmt, M, p->N, p->K, A, p->Bt, p->ldt, bias, res, C, alpha_eff, beta, c->zero.p, act,
                              tail0, p->colscale, s);
     if (p->B != nullptr)
@@ -499,7 +499,7 @@ Status host_gemm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const
     // uses its prepared, K-contiguous copy.
     Registered *reg = nullptr;
     if (preparable_fmt(fmt) && prepared_gemv_supported(data_fmt(fmt), M, K) &&
-        prepared_gemv_preferred(data_fmt(fmt), M)) {
+        prepared_gemv_preferred(data_fmt(fmt), M, K)) {
         auto it = c->weights.find(B);
         if (it != c->weights.end() && it->second.bytes >= weight_bytes(fmt, K, N)) reg = &it->second;
     }

@@ -10,6 +10,11 @@
 
 #include "../../include/tomoul_hip.h"
 
+// A kernel's dynamically sized LDS array (the launch's shared-memory bytes).
+#ifndef TML_DYNAMIC_LDS
+#define TML_DYNAMIC_LDS(T, v) extern __shared__ T v[]
+#endif
+
 namespace tml {
 
 // Status carrying a TML_ERR_* code and a message; ok() when code == TML_OK.
@@ -185,9 +190,15 @@ constexpr int64_t kGemvMaxM = 8;
 constexpr int64_t kPreparedGemvMaxM = 8;  // every prepared format
 int64_t prepared_row_bytes(int fmt, int64_t K);
 bool prepared_gemv_supported(int fmt, int64_t M, int64_t K);
-// Whether the prepared kernels are the faster choice at M rows when the
-// [K,N] weight is also at hand.
-bool prepared_gemv_preferred(int fmt, int64_t M);
+// Whether the prepared kernels are the faster choice at M rows (K deep)
+// when the [K,N] weight is also at hand.
+bool prepared_gemv_preferred(int fmt, int64_t M, int64_t K);
+// Matrix-core decoder GEMV on a prepared Q8_0 / Q4_0 weight (gemv_tm.hip):
+// M = 2..8, K a whole number of chunks (16 int8 / 32 int4 elements).
+bool gemv_tm_supported(int fmt, int64_t M, int64_t K);
+Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
+                      const float *bias, const float *res, float *C, float alpha_eff, float beta, int act,
+                      long long tail0, const float *colscale, hipStream_t s);
 // Bytes of one row of K elements of fmt in the reference's packing (Q4_0:
 // two per byte), before the 16-byte padding of a prepared row.
 inline int64_t packed_row_bytes(int fmt, int64_t K) {
