@@ -111,7 +111,7 @@ def _default_cases():
                     for it in (1, 2, 4):
                         for t in (1, 2):
                             cs.append(f"prep {fmt} {M} 40 2080 b TML_GEMVTM_NW={nw} TML_GEMVTM_IT={it} "
-                                      f"TML_GEMVTM_T={t}")
+                                      f"TML_GEMVTM_T={t} TML_GEMVTM_PF={(nw + it + t) % 2}")
         if fmt in (F32, F16, Q8_0, Q4_0):
             cs.append(f"rows {fmt} 3 777 260 b")
             cs.append(f"rows {fmt} 13 300 384 b")

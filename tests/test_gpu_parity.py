@@ -660,7 +660,7 @@ def test_prepared_matrix_core_plans(orc, nw, it, t):
             q, s = orc.quantize_q8(w)
             p, s4 = orc.quantize_q4(w)
             bias = synth.normal(203, n, 0.0, 0.02)
-            for m in (2, 3, 5, 8):
+            for m in (1, 2, 3, 5, 8):
                 a, c0 = rnd(204 + m, m, k), rnd(214 + m, m, n)
                 for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
                                            (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
@@ -673,6 +673,22 @@ def test_prepared_matrix_core_plans(orc, nw, it, t):
                 os.environ.pop(key, None)
             else:
                 os.environ[key] = v
+
+
+def test_prepared_matrix_core_vocabulary(orc):
+    # Q4_0 at M = 1 on a vocabulary-sized N takes the matrix-core kernel by
+    # default (two waves a workgroup, eight or more workgroups a CU); Q8_0
+    # there and Q4_0 on a layer-sized N stay on the VALU kernels.
+    k = 256
+    for n in (33000, 5000):
+        w = rnd(231, k, n, 0.02)
+        q, s = orc.quantize_q8(w)
+        p, s4 = orc.quantize_q4(w)
+        a = rnd(232, 1, k)
+        for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
+                                   (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
+            got = _run_prepared(fmt, b, scale, k, n, 1, a)
+            assert rel_err(got, ref) <= 2e-5, (n, fmt)
 
 
 @pytest.mark.parametrize("m", [3, 8])

@@ -622,8 +622,9 @@ int64_t prepared_gemv_max_m(int fmt) {
 // and 5120x1280 Q4_0): the prepared kernels beat the [K,N] GEMV everywhere
 // except Q4_0 at M > 4 (15.0 / 19.7 us against 10.4 / 14.3 us), where the
 // staged activations of eight rows outweigh the halved weight bytes.
-// The matrix-core kernel (gemv_tm.hip) serves Q8_0 / Q4_0 at M >= 2 when K
-// is a whole number of chunks, Q4_0 above M = 4 included.
+// The matrix-core kernel (gemv_tm.hip) serves Q8_0 / Q4_0 at M >= 3 (and
+// M = 2 on short Q4_0 rows) when K is a whole number of chunks, Q4_0 above
+// M = 4 included.
 bool prepared_gemv_preferred(int fmt, int64_t M, int64_t K) {
     return gemv_tm_supported(fmt, M, K) || !(fmt == TML_FMT_Q4_0 && M > 4);
 }
@@ -675,10 +676,11 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
         return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV dimension exceeds 2^30");
     if (ldt < prepared_row_bytes(fmt, K) || ldt % 16 != 0 || ((uintptr_t)Bt % 16) != 0)
         return Status::Err(TML_ERR_INVALID_ARG, "prepared weight layout");
-    // Q8_0 / Q4_0 at M >= 2 on the matrix cores (gemv_tm.hip) where its
+    // Q8_0 / Q4_0 on the matrix cores (gemv_tm.hip) where it is the faster
+    // kernel (M >= 3, short Q4_0 rows at M = 2, Q4_0 vocabularies at M = 1) and its
     // operands fit its buffer offsets.
-    if (gemv_tm_supported(fmt, M, K) && ((uintptr_t)A % 16) == 0 && N * ldt < ((int64_t)1 << 31) &&
-        M * K * 4 < ((int64_t)1 << 31))
+    if ((gemv_tm_supported(fmt, M, K) || (M == 1 && gemv_tm_m1_preferred(fmt, N, K))) && ((uintptr_t)A % 16) == 0 &&
+        N * ldt < ((int64_t)1 << 31) && M * K * 4 < ((int64_t)1 << 31))
         return launch_gemv_tm(fmt, M, N, K, A, Bt, ldt, bias, res, C, alpha_eff, beta, act, tail0, colscale, s);
     GemvTArgs ka;
     ka.M = (int)M; ka.N = (int)N; ka.K = (int)K;

@@ -149,7 +149,7 @@ __device__ __forceinline__ uintx4 tm_weights(const uintx4 &w, int st) {
     return b;
 }
 
-template <int FMT, int IT, int MR, int T>
+template <int FMT, int IT, int MR, int T, bool PF>
 __global__ __launch_bounds__(1024) void gemv_tm_kernel(GemvTmArgs a) {
     constexpr int E = FMT == TML_FMT_Q8_0 ? 16 : 32;  // elements per 16-byte chunk
     constexpr int NQ = E / 4;                          // element groups (float4) per chunk
@@ -187,9 +187,8 @@ __global__ __launch_bounds__(1024) void gemv_tm_kernel(GemvTmArgs a) {
     for (int tl = 0; tl < T; ++tl) acc[tl] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
     // A round: wave w owns the run of R chunks r0 + w R + [0, R); lane group
     // g of sub-round it takes chunk 4 it + g of the run.
-    for (int r0 = 0; r0 < a.nchunk; r0 += nw * R) {
+    auto load_round = [&](int r0, uintx4 (&w)[IT][T], floatx4 (&x)[TASKS]) __attribute__((always_inline)) {
         const int base = r0 + wave * R;
-        uintx4 w[IT][T];
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int ch = base + 4 * it + g;
@@ -203,7 +202,6 @@ __global__ __launch_bounds__(1024) void gemv_tm_kernel(GemvTmArgs a) {
         // chunks, whose element groups q are adjacent float4s of the
         // activation row (the layout's chunk interleave), so each load
         // instruction reads runs of 16 R contiguous bytes.
-        floatx4 x[TASKS];
 #pragma unroll
         for (int t = 0; t < TASKS; ++t) {
             const int j = lane + 64 * t;
@@ -214,6 +212,8 @@ __global__ __launch_bounds__(1024) void gemv_tm_kernel(GemvTmArgs a) {
             x[t] = __builtin_bit_cast(floatx4,
                                       tm_load16(a.A, a.xbytes, in ? 4u * ((unsigned)m * (unsigned)a.K + k) : kOutOfRange));
         }
+    };
+    auto compute_round = [&](const uintx4 (&w)[IT][T], const floatx4 (&x)[TASKS]) __attribute__((always_inline)) {
         // Split and stage: k-set q / 2, dwords 2 (q & 1) and 2 (q & 1) + 1 of
         // row m (the B order below), the lo part in row m + MR.
 #pragma unroll
@@ -253,6 +253,30 @@ __global__ __launch_bounds__(1024) void gemv_tm_kernel(GemvTmArgs a) {
         }
         // every lane's reads done before the next round's writes
         __builtin_amdgcn_wave_barrier();
+    };
+
+    const int step = nw * R;
+    uintx4 wa[IT][T];
+    floatx4 xa[TASKS];
+    if constexpr (PF) {
+        // Two rounds in flight: the next round's loads are issued before
+        // this round's arithmetic, so a wave's memory latency overlaps its
+        // own work, not only other waves'.
+        uintx4 wb[IT][T];
+        floatx4 xb[TASKS];
+        load_round(0, wa, xa);
+        for (int r0 = 0; r0 < a.nchunk; r0 += 2 * step) {
+            if (r0 + step < a.nchunk) load_round(r0 + step, wb, xb);
+            compute_round(wa, xa);
+            if (r0 + step >= a.nchunk) break;
+            if (r0 + 2 * step < a.nchunk) load_round(r0 + 2 * step, wa, xa);
+            compute_round(wb, xb);
+        }
+    } else {
+        for (int r0 = 0; r0 < a.nchunk; r0 += step) {
+            load_round(r0, wa, xa);
+            compute_round(wa, xa);
+        }
     }
 
     // Lane (c, g) holds D[4 g + r][c] of each tile: rows of A, columns of B
@@ -306,27 +330,40 @@ constexpr size_t tm_lds_bytes(int nw, int tiles) {
     return (size_t)nw * tm_stage<FMT, MR, IT>().wave * 4 + (size_t)(nw - 1) * tiles * 64 * sizeof(floatx4);
 }
 
-template <int FMT, int IT, int T>
-void launch_tm_mr(const GemvTmArgs &ka, unsigned grid, hipStream_t s) {
+template <int FMT, int IT, int MR, int T>
+void launch_tm_pf(const GemvTmArgs &ka, bool pf, unsigned grid, hipStream_t s) {
     const dim3 block((unsigned)ka.nw * 64);
-    if (ka.M <= 2) gemv_tm_kernel<FMT, IT, 2, T><<<dim3(grid), block, tm_lds_bytes<FMT, 2, IT>(ka.nw, T), s>>>(ka);
-    else if (ka.M <= 4) gemv_tm_kernel<FMT, IT, 4, T><<<dim3(grid), block, tm_lds_bytes<FMT, 4, IT>(ka.nw, T), s>>>(ka);
-    else gemv_tm_kernel<FMT, IT, 8, T><<<dim3(grid), block, tm_lds_bytes<FMT, 8, IT>(ka.nw, T), s>>>(ka);
+    const size_t lds = tm_lds_bytes<FMT, MR, IT>(ka.nw, T);
+    // runs of 16 chunks hold too many registers for two rounds in flight
+    if constexpr (IT < 4) {
+        if (pf) {
+            gemv_tm_kernel<FMT, IT, MR, T, true><<<dim3(grid), block, lds, s>>>(ka);
+            return;
+        }
+    }
+    gemv_tm_kernel<FMT, IT, MR, T, false><<<dim3(grid), block, lds, s>>>(ka);
+}
+
+template <int FMT, int IT, int T>
+void launch_tm_mr(const GemvTmArgs &ka, bool pf, unsigned grid, hipStream_t s) {
+    if (ka.M <= 2) launch_tm_pf<FMT, IT, 2, T>(ka, pf, grid, s);
+    else if (ka.M <= 4) launch_tm_pf<FMT, IT, 4, T>(ka, pf, grid, s);
+    else launch_tm_pf<FMT, IT, 8, T>(ka, pf, grid, s);
 }
 
 template <int FMT, int T>
-void launch_tm_it(const GemvTmArgs &ka, int it, unsigned grid, hipStream_t s) {
+void launch_tm_it(const GemvTmArgs &ka, int it, bool pf, unsigned grid, hipStream_t s) {
     switch (it) {
-        case 1: launch_tm_mr<FMT, 1, T>(ka, grid, s); break;
-        case 2: launch_tm_mr<FMT, 2, T>(ka, grid, s); break;
-        default: launch_tm_mr<FMT, 4, T>(ka, grid, s); break;
+        case 1: launch_tm_mr<FMT, 1, T>(ka, pf, grid, s); break;
+        case 2: launch_tm_mr<FMT, 2, T>(ka, pf, grid, s); break;
+        default: launch_tm_mr<FMT, 4, T>(ka, pf, grid, s); break;
     }
 }
 
 template <int FMT>
-void launch_tm_t(const GemvTmArgs &ka, int it, int tiles, unsigned grid, hipStream_t s) {
-    if (tiles == 2) launch_tm_it<FMT, 2>(ka, it, grid, s);
-    else launch_tm_it<FMT, 1>(ka, it, grid, s);
+void launch_tm_t(const GemvTmArgs &ka, int it, int tiles, bool pf, unsigned grid, hipStream_t s) {
+    if (tiles == 2) launch_tm_it<FMT, 2>(ka, it, pf, grid, s);
+    else launch_tm_it<FMT, 1>(ka, it, pf, grid, s);
 }
 
 template <int FMT>
@@ -357,18 +394,32 @@ constexpr size_t kTmMaxLds = 160 * 1024;  // LDS of a gfx950 CU
 // VALU kernels are faster for Q8_0 (3.51 against 3.82 us at 1024x4096) and
 // long Q4_0 rows (5.32 against 5.50 us at 5120x1280), slower for short Q4_0
 // rows (4.67 against 4.00 us at 1280x5120).
-bool gemv_tm_supported(int fmt, int64_t M, int64_t K) {
+// What the kernel can run: Q8_0 / Q4_0, M = 1..8, K whole chunks.
+bool gemv_tm_capable(int fmt, int64_t M, int64_t K) {
     const int64_t e = fmt == TML_FMT_Q8_0 ? 16 : fmt == TML_FMT_Q4_0 ? 32 : 0;
-    if (e == 0 || M < 2 || M > kPreparedGemvMaxM || K <= 0 || K % e != 0 || K >= ((int64_t)1 << 30)) return false;
-    const int mode = env_int("TML_GEMVTM", 1);  // 0: off; 2: every M >= 2 (tests)
+    return e > 0 && M >= 1 && M <= kPreparedGemvMaxM && K > 0 && K % e == 0 && K < ((int64_t)1 << 30);
+}
+
+// Q4_0 at M = 1 with at least 32768 columns (a vocabulary projection): the
+// int4 decode makes the VALU kernel instruction-bound there (12.71 against
+// 10.61 us at 1280x51866); on the layer shapes it is the faster one.
+bool gemv_tm_m1_preferred(int fmt, int64_t N, int64_t K) {
+    return fmt == TML_FMT_Q4_0 && N >= 32768 && gemv_tm_capable(fmt, 1, K) && env_int("TML_GEMVTM", 1) != 0;
+}
+
+bool gemv_tm_supported(int fmt, int64_t M, int64_t K) {
+    const int64_t e = fmt == TML_FMT_Q8_0 ? 16 : 32;
+    if (!gemv_tm_capable(fmt, M, K)) return false;
+    const int mode = env_int("TML_GEMVTM", 1);  // 0: off; 2: every M (tests)
     if (mode == 0) return false;
-    return M >= 3 || mode == 2 || (fmt == TML_FMT_Q4_0 && K / e <= 64);
+    if (mode == 2) return true;
+    return M >= 3 || (M == 2 && fmt == TML_FMT_Q4_0 && K / e <= 64);
 }
 
 Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
                       const float *bias, const float *res, float *C, float alpha_eff, float beta, int act,
                       long long tail0, const float *colscale, hipStream_t s) {
-    if (!gemv_tm_supported(fmt, M, K)) return Status::Err(TML_ERR_INVALID_ARG, "matrix-core GEMV: unsupported");
+    if (!gemv_tm_capable(fmt, M, K)) return Status::Err(TML_ERR_INVALID_ARG, "matrix-core GEMV: unsupported");
     const int64_t e = fmt == TML_FMT_Q8_0 ? 16 : 32;
     if (ldt < prepared_row_bytes(fmt, K) || ldt % 16 != 0 || ((uintptr_t)Bt % 16) != 0 || ((uintptr_t)A % 16) != 0)
         return Status::Err(TML_ERR_INVALID_ARG, "matrix-core GEMV: prepared layout or alignment");
@@ -422,6 +473,14 @@ Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, 
                 }
             }
     }
+    // With eight or more workgroups a CU (vocabulary-sized N) two waves of
+    // runs of four: more workgroups resident per CU hide more latency
+    // (Q4_0 1280x51866, M = 1: 10.61 us, against 11.22 with four waves and
+    // 14.57 with ten).
+    if (grid >= 8LL * cus) {
+        it = 1;
+        nw = (int)std::min<int64_t>(2, (ka.nchunk + 3) / 4);
+    }
     const int forced_nw = env_int("TML_GEMVTM_NW", 0), forced_it = env_int("TML_GEMVTM_IT", 0);
     if (forced_it == 1 || forced_it == 2 || forced_it == 4) it = forced_it;
     if (forced_nw >= 1 && forced_nw <= 16) nw = forced_nw;
@@ -431,9 +490,14 @@ Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, 
     if (tm_lds_need(fmt, M, it, nw, tiles) > kTmMaxLds)
         return Status::Err(TML_ERR_INVALID_ARG, "matrix-core GEMV: staging exceeds the LDS");
     ka.nw = nw;
+    // Two rounds in flight: measured no faster on the decoder shapes (Q4_0
+    // vocabulary 10.64 against 10.61 us), so only on request.
+    bool pf = false;
+    const int forced_pf = env_int("TML_GEMVTM_PF", -1);
+    if (forced_pf == 0 || forced_pf == 1) pf = forced_pf == 1;
     switch (fmt) {
-        case TML_FMT_Q8_0: launch_tm_t<TML_FMT_Q8_0>(ka, it, tiles, (unsigned)grid, s); break;
-        default: launch_tm_t<TML_FMT_Q4_0>(ka, it, tiles, (unsigned)grid, s); break;
+        case TML_FMT_Q8_0: launch_tm_t<TML_FMT_Q8_0>(ka, it, tiles, pf, (unsigned)grid, s); break;
+        default: launch_tm_t<TML_FMT_Q4_0>(ka, it, tiles, pf, (unsigned)grid, s); break;
     }
     TML_HIP_TRY(hipGetLastError());
     return Status::Ok();

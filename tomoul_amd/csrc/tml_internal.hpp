@@ -194,8 +194,10 @@ bool prepared_gemv_supported(int fmt, int64_t M, int64_t K);
 // when the [K,N] weight is also at hand.
 bool prepared_gemv_preferred(int fmt, int64_t M, int64_t K);
 // Matrix-core decoder GEMV on a prepared Q8_0 / Q4_0 weight (gemv_tm.hip):
-// M = 2..8, K a whole number of chunks (16 int8 / 32 int4 elements).
+// K a whole number of chunks (16 int8 / 32 int4 elements); chosen for M =
+// 3..8, M = 2 on short Q4_0 rows, and Q4_0 M = 1 on vocabulary-sized N.
 bool gemv_tm_supported(int fmt, int64_t M, int64_t K);
+bool gemv_tm_m1_preferred(int fmt, int64_t N, int64_t K);
 Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
                       const float *bias, const float *res, float *C, float alpha_eff, float beta, int act,
                       long long tail0, const float *colscale, hipStream_t s);
