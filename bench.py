@@ -571,6 +571,10 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
                 log(f"gemv {label} M={M} {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s "
                     f"({floor_us / (ms * 1e3):.2f} of the copy floor)")
             res[f"M{M}"] = entry
+        # the decoder's growth with M: each row count's prepared time over M = 1's
+        if "M1" in res:
+            for key, entry in res.items():
+                entry["prepared"]["x_of_M1"] = round(entry["prepared"]["us"] / res["M1"]["prepared"]["us"], 3)
         for h in handles:
             _abi.prepared_free(h)
         del copies
@@ -663,7 +667,7 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
 
     out["torch_copy_floor"] = {"2MiB": copy_floor(2 << 20), "4MiB": copy_floor(4 << 20),
                                "32MiB": copy_floor(32 << 20)}
-    out["q8_1024x4096"] = run(_abi.FMT_Q8_0, 1024, 4096, [1, 8], 2002, "q8 1024x4096")
+    out["q8_1024x4096"] = run(_abi.FMT_Q8_0, 1024, 4096, [1, 4, 8], 2002, "q8 1024x4096")
     out["q4_1280x5120"] = run(_abi.FMT_Q4_0, 1280, 5120, [1, 4, 8], 2002, "q4 1280x5120")
     out["q4_5120x1280"] = run(_abi.FMT_Q4_0, 5120, 1280, [1, 4, 8], 2003, "q4 5120x1280")
     # config 3 read as "one scale per output column" (Q8_0_PC, an extension)
@@ -765,14 +769,17 @@ def bench_sentence_transformer(torch, dev, sptr, timer, _abi, synth, tokens: int
 
 
 def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
-    """Decoder GEMVs for kernel traces / counters: Q8_0 1024x4096 at M = 1
-    and 8, Q4_0 1280x5120 and 5120x1280 at M = 1 and 4, each on its prepared
-    copy and in the [K,N] layout, `launches` times over 16 distinct weight
-    copies (eager launches, one kernel per call); then the Q8_0 and Q4_0
-    vocabulary projections (1280 x 51866, M = 1) on 3 / 4 prepared copies."""
-    for fmt, K, N, M in ((_abi.FMT_Q8_0, 1024, 4096, 1), (_abi.FMT_Q8_0, 1024, 4096, 8),
+    """Decoder GEMVs for kernel traces / counters: Q8_0 1024x4096 and Q4_0
+    1280x5120 and 5120x1280 at M = 1, 4 and 8, each on its prepared copy and
+    in the [K,N] layout, `launches` times over 16 distinct weight copies
+    (eager launches, one kernel per call); then the Q8_0 and Q4_0 vocabulary
+    projections (1280 x 51866, M = 1) on 3 / 4 prepared copies."""
+    for fmt, K, N, M in ((_abi.FMT_Q8_0, 1024, 4096, 1), (_abi.FMT_Q8_0, 1024, 4096, 4),
+                         (_abi.FMT_Q8_0, 1024, 4096, 8),
                          (_abi.FMT_Q4_0, 1280, 5120, 1), (_abi.FMT_Q4_0, 1280, 5120, 4),
-                         (_abi.FMT_Q4_0, 5120, 1280, 1), (_abi.FMT_Q4_0, 5120, 1280, 4)):
+                         (_abi.FMT_Q4_0, 1280, 5120, 8),
+                         (_abi.FMT_Q4_0, 5120, 1280, 1), (_abi.FMT_Q4_0, 5120, 1280, 4),
+                         (_abi.FMT_Q4_0, 5120, 1280, 8)):
         w = torch.from_numpy(synth.normal_matrix(2002, K, N, 0.02)).to(dev)
         nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
         q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
