@@ -83,7 +83,8 @@ def test_tanh_split_follows_flat_index(orc):
 
 @pytest.fixture
 def forced_env():
-    keys = ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE", "TML_GEMM_FUSED")
+    keys = ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_GEMM_DMA", "TML_GEMM_TILE", "TML_GEMM_FUSED",
+            "TML_GEMM_VEC_EPI", "TML_GEMM_DMA_Q")
     saved = {key: os.environ.get(key) for key in keys}
     yield os.environ
     for key, v in saved.items():
@@ -307,3 +308,37 @@ def test_prepared_rows_in_place_and_errors(orc):
     with pytest.raises(_abi.TmlError) as ex:
         _abi.prepare_rows_dev(_abi.FMT_F32, k, n, E.data_ptr(), 4 * k - 4)
     assert ex.value.code == _abi.TML_ERR_INVALID_ARG
+
+
+# --------------------------------------------- staged (16-byte) GEMM epilogue
+@pytest.mark.parametrize("tile", [5, 6, 8, 9])
+def test_staged_epilogue(orc, forced_env, tile):
+    # Tiles whose C tile fits an A stage (BN <= BK: 128x64 and 64x64 at
+    # BK 64, 32x64 at BK 64, 96x32) write C through LDS in 16-byte pieces.
+    # Every epilogue term (alpha, beta * C, bias, residual, GELU, per-column
+    # scales) on ragged M and N (N a multiple of 4 but not of the tile):
+    # against the oracle, and against the 4-byte epilogue within rounding.
+    import torch
+    forced_env["TML_GEMM_DMA_TILE"] = str(tile)
+    forced_env["TML_GEMM_DMA_Q"] = "1"
+    m, n, k = 203, 340, 516
+    a, w, c0, r = rnd(681, m, k), rnd(682, k, n, 0.05), rnd(683, m, n), rnd(684, m, n)
+    bias = synth.normal(685, n, 0.0, 0.5)
+    qc, sc = orc.quantize_q8_cols(w)
+    cases = [(_abi.FMT_F32, w, None, orc.matmul(a, w)),
+             (_abi.FMT_Q8_0_PC, qc, sc, orc.matmul_cols(a, 17, qc, sc, k, n))]
+    for fmt, b, scales, prod in cases:
+        ref = orc.gelu_exact(0.75 * prod - 0.5 * c0 + bias + r)
+        got = {}
+        for staged in ("1", "0"):
+            forced_env["TML_GEMM_VEC_EPI"] = staged
+            A, B, C, R, Bias = _dev(a), _dev(b), _dev(c0), _dev(r), _dev(bias)
+            S = _dev(scales) if scales is not None else None
+            _abi.gemm_ex_dev(fmt, m, n, k, A.data_ptr(), B.data_ptr(), C.data_ptr(), act=_abi.ACT_GELU_ERF,
+                             residual_ptr=R.data_ptr(), scales_ptr=S.data_ptr() if S is not None else None,
+                             bias_ptr=Bias.data_ptr(), alpha=0.75, beta=-0.5)
+            torch.cuda.synchronize()
+            got[staged] = C.cpu().numpy()
+        tol = FP32_TOL if fmt == _abi.FMT_F32 else Q_TOL
+        assert rel_err(got["1"], ref) <= tol, (tile, fmt, rel_err(got["1"], ref))
+        assert rel_err(got["1"], got["0"]) <= 1e-6, (tile, fmt)
