@@ -313,6 +313,19 @@ inline tml_emu_u32x2 __builtin_amdgcn_raw_buffer_load_b64(tml_emu_rsrc r, unsign
 inline uint32_t __builtin_amdgcn_raw_buffer_load_b32(tml_emu_rsrc r, unsigned off, int soff, int) {
     return tml_emu_buf_dword(r, (uint64_t)off + (uint64_t)soff);
 }
+// 2- and 1-byte loads: zero when the bytes run past the byte count.
+inline unsigned short __builtin_amdgcn_raw_buffer_load_b16(tml_emu_rsrc r, unsigned off, int soff, int) {
+    const uint64_t o = (uint64_t)off + (uint64_t)soff;
+    if (o + 2 > r.num) return 0;
+    unsigned short v;
+    std::memcpy(&v, r.base + o, 2);
+    return v;
+}
+inline unsigned char __builtin_amdgcn_raw_buffer_load_b8(tml_emu_rsrc r, unsigned off, int soff, int) {
+    const uint64_t o = (uint64_t)off + (uint64_t)soff;
+    if (o + 1 > r.num) return 0;
+    return (unsigned char)r.base[o];
+}
 // LDS DMA: lane l's `size` bytes land at lds + l * size.
 inline void __builtin_amdgcn_raw_ptr_buffer_load_lds(tml_emu_rsrc r, __attribute__((address_space(3))) void *lds,
                                                      int size, unsigned off, int soff, int imm, int) {

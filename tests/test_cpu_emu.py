@@ -11,8 +11,9 @@ overflow or other undefined behaviour aborts the case.
 * test_planted_mistakes: a B operand 16 bytes short must be reported for
   every kernel family (the harness itself works);
 * test_cases: every kernel family, tile config (TML_GEMM_DMA_TILE 1-10,
-  TML_GEMM_TILE 1-10), K split (1, 2, 3, 4, 8), format, epilogue and the
-  fused split-K exchange, on shapes with ragged edges in M, N and K;
+  TML_GEMM_TILE 1-10, TML_GEMM_QBF_TILE 1-4), K split (1, 2, 3, 4, 8),
+  format, epilogue and the fused split-K exchange, on shapes with ragged
+  edges in M, N and K;
 * test_fault_sweep_replay (TML_EMU_FULL=1): every (format, shape, forced
   plan) of the narrow-format calibration sweep that once ended in a GPU
   memory fault, at its full sizes (880 cases, about 2.5 minutes on 8 cores).
@@ -93,6 +94,15 @@ def _default_cases():
         for tile in range(1, 11):
             cs.append(f"gemm {fmt} {M} {N} {K} bre TML_GEMM_DMA=0 TML_GEMM_TILE={tile}")
         cs.append(f"gemm {fmt} {M} {N - 1 if fmt in (F32, F16, Q8_0, Q8_0_PC) else N} {K - 2} b TML_GEMM_DMA=0")
+        if fmt in (Q8_0, Q4_0, Q8_0_PC, Q4_0_PC):
+            # the bf16 matrix-core kernel: every tile, K split or not (K a
+            # multiple of 8 here), and the planner's own choice
+            for tile in range(1, 5):
+                for split in (1, 3):
+                    cs.append(f"gemm {fmt} {M} {N} {K - K % 8 + 8} br TML_GEMM_QBF=2 TML_GEMM_QBF_TILE={tile} "
+                              f"TML_GEMM_QBF_SPLIT={split}")
+            cs.append(f"gemm {fmt} 33 {N + 2} 40 te TML_GEMM_QBF=2")
+            cs.append(f"gemm {fmt} 300 70 1288 bB")
     # [K,N] GEMV and the prepared GEMV at every row count
     for fmt in (F32, F16, Q8_0, Q4_0, Q8_K, Q8_0_PC, Q4_0_PC):
         for M in range(1, 9):
@@ -255,7 +265,8 @@ def test_noalloc_entry_point(emu):
     ok_cases = ["noalloc 0 256 512 4096 br TML_GEMM_SPLIT=4", "noalloc 0 96 256 2048 bt TML_GEMM_SPLIT=4",
                 "noalloc 1 4 1024 8192 b", "noalloc 1 3 512 4096 br", "noalloc 0 300 260 516 be",
                 "noalloc 17 6 1000 3000 b", "noalloc 2 8 640 5120 b", "noalloc 3 5 384 1536 b",
-                "noalloc 0 128 256 2048 b TML_GEMM_SPLIT=4 TML_GEMM_DMA_TILE=2 TML_GEMM_FUSED=1"]
+                "noalloc 0 128 256 2048 b TML_GEMM_SPLIT=4 TML_GEMM_DMA_TILE=2 TML_GEMM_FUSED=1",
+                "noalloc 1 512 1024 4096 br", "noalloc 2 300 512 1024 b TML_GEMM_QBF_SPLIT=4"]
     outs, fails = run_cases(emu, ok_cases, workers=3)
     assert not fails, fails
     assert len(_ok_lines(outs)) == len(ok_cases), _err_lines(outs)

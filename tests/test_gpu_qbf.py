@@ -1,0 +1,181 @@
+"""The bf16 matrix-core Q8_0 / Q4_0 GEMM (gemm_qbf.hip, M > 8) against the oracle.
+
+The int8 / int4 weights are exact in bf16 and each fp32 activation is split
+into bf16 hi + lo terms (|x - hi - lo| <= 2^-17 |x|), so the product matches
+the reference's dequantize-then-fp32-accumulate result (matmulF32Q8 /
+matmulF32Q4, src/core/quantization.zig:240-311, :829-957; per-column scales
+through oracle.matmul_cols) to ~1e-5.  The bound here is 2e-5, not the 1e-3
+bar of the quantized paths: a dropped lo term costs ~4e-3, a misplaced k,
+column or nibble far more.  The planner takes this kernel from M = 256 on;
+TML_GEMM_QBF=2 (or a forced tile / split) takes it for every M > 8, which
+these tests use to reach it on small shapes.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from tomoul_amd import _abi, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-5
+KEYS = ("TML_GEMM_QBF_TILE", "TML_GEMM_QBF", "TML_GEMM_QBF_SPLIT")
+
+
+def rnd(seed, m, n, std=1.0):
+    return synth.normal_matrix(seed, m, n, std)
+
+
+@pytest.fixture
+def env():
+    saved = {key: os.environ.get(key) for key in KEYS}
+    yield os.environ
+    for key, v in saved.items():
+        if v is None:
+            os.environ.pop(key, None)
+        else:
+            os.environ[key] = v
+
+
+def _cases(orc, w, k, n, a):
+    """(format, weight bytes, per-tensor scale, per-column scales, oracle product)."""
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    qc, sc = orc.quantize_q8_cols(w)
+    pc, sc4 = orc.quantize_q4_cols(w)
+    return [(_abi.FMT_Q8_0, q, s, None, orc.matmul_q8(a, q, s)),
+            (_abi.FMT_Q4_0, p, s4, None, orc.matmul_q4(a, p, k, n, s4)),
+            (_abi.FMT_Q8_0_PC, qc, 1.0, sc, orc.matmul_cols(a, _abi.FMT_Q8_0_PC, qc, sc, k, n)),
+            (_abi.FMT_Q4_0_PC, pc, 1.0, sc4, orc.matmul_cols(a, _abi.FMT_Q4_0_PC, pc, sc4, k, n))]
+
+
+def _gemm(fmt, m, n, k, a, b, scale, scales, bias=None):
+    c = np.zeros((m, n), np.float32)
+    _abi.gemm(fmt, m, n, k, a, np.ascontiguousarray(b), c, scale=scale, scales=scales, bias=bias)
+    return c
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4])
+def test_qbf_tiles_vs_oracle(orc, env, tile):
+    # Every tile config (0: the planner's choice) on shapes ragged in M and N
+    # (partial tiles, N not a multiple of 16), K from one slice to many, with
+    # a bias.
+    env["TML_GEMM_QBF"] = "2"
+    if tile:
+        env["TML_GEMM_QBF_TILE"] = str(tile)
+    for (m, n, k) in [(9, 130, 64), (200, 336, 520), (33, 4098, 40), (300, 70, 1288)]:
+        w = rnd(301, k, n, 0.02)
+        a = rnd(302 + m, m, k)
+        bias = synth.normal(303, n, 0.0, 0.02)
+        for fmt, b, scale, scales, ref in _cases(orc, w, k, n, a):
+            got = _gemm(fmt, m, n, k, a, b, scale, scales, bias)
+            err = rel_err(got, ref + bias)
+            assert err <= TOL, (m, n, k, fmt, err)
+
+
+@pytest.mark.parametrize("split", [2, 3, 5])
+@pytest.mark.parametrize("tile", [1, 2, 4])
+def test_qbf_split_vs_oracle(orc, env, tile, split):
+    # K split over workgroups (each over its own range of 32-deep slices,
+    # the last range short), raw partials summed in split order by the
+    # reduce launch, which runs the epilogue: bias and residual here.
+    env["TML_GEMM_QBF_TILE"] = str(tile)
+    env["TML_GEMM_QBF_SPLIT"] = str(split)
+    for (m, n, k) in [(200, 336, 520), (300, 70, 1288)]:
+        w = rnd(351, k, n, 0.02)
+        a = rnd(352 + m, m, k)
+        bias = synth.normal(353, n, 0.0, 0.02)
+        res = rnd(354, m, n)
+        for fmt, b, scale, scales, ref in _cases(orc, w, k, n, a):
+            c = np.zeros((m, n), np.float32)
+            _abi.gemm_residual(fmt, m, n, k, a, np.ascontiguousarray(b), res, c, scale=scale, scales=scales,
+                               bias=bias)
+            err = rel_err(c, ref + bias + res)
+            assert err <= TOL, (m, n, k, fmt, err)
+
+
+@pytest.mark.parametrize("m", [128, 512])
+def test_qbf_config3(orc, m):
+    # BASELINE config 3 at M = 128 / 512: X[M x 1024] . W[1024 x 4096] in
+    # Q8_0 (and Q4_0 on the same weight).
+    k, n = 1024, 4096
+    w = rnd(2002, k, n, 0.02)
+    a = rnd(1001, m, k)
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    nt = min(16, orc.max_threads())
+    for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8_mt(a, q, s, nt)),
+                               (_abi.FMT_Q4_0, p, s4, orc.matmul_q4_mt(a, p, k, n, s4, nt))]:
+        got = _gemm(fmt, m, n, k, a, b, scale, None)
+        assert rel_err(got, ref) <= TOL, (m, fmt, rel_err(got, ref))
+
+
+def test_qbf_epilogue(orc, env):
+    # Residual, GELU (erf and tanh forms) and per-column scales in the
+    # kernel's epilogue.
+    env["TML_GEMM_QBF"] = "2"
+    m, n, k = 150, 200, 264
+    w = rnd(311, k, n, 0.02)
+    a = rnd(312, m, k)
+    bias = synth.normal(313, n, 0.0, 0.02)
+    res = rnd(314, m, n)
+    for fmt, b, scale, scales, ref in _cases(orc, w, k, n, a):
+        c = np.zeros((m, n), np.float32)
+        _abi.gemm_residual(fmt, m, n, k, a, np.ascontiguousarray(b), res, c, scale=scale, scales=scales, bias=bias)
+        assert rel_err(c, ref + bias + res) <= TOL, fmt
+        for act in (_abi.ACT_GELU_ERF, _abi.ACT_GELU_TANH):
+            c = np.zeros((m, n), np.float32)
+            _abi.gemm_act(fmt, m, n, k, a, np.ascontiguousarray(b), c, act=act, scale=scale, scales=scales, bias=bias)
+            assert rel_err(c, orc.apply_act(ref + bias, act)) <= TOL, (fmt, act)
+
+
+def test_qbf_alpha_beta_device(orc, env):
+    # C = alpha * A . W + beta * C on device pointers.
+    import torch
+    env["TML_GEMM_QBF"] = "2"
+    m, n, k = 70, 96, 128
+    w = rnd(321, k, n, 0.02)
+    a, c0 = rnd(322, m, k), rnd(323, m, n)
+    q, s = orc.quantize_q8(w)
+    A, Q, C = (torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0") for x in (a, q, c0))
+    _abi.gemm_dev(_abi.FMT_Q8_0, m, n, k, A.data_ptr(), Q.data_ptr(), C.data_ptr(), scale=s, alpha=0.5, beta=-2.0)
+    torch.cuda.synchronize()
+    assert rel_err(C.cpu().numpy(), 0.5 * orc.matmul_q8(a, q, s) - 2.0 * c0) <= TOL
+
+
+def test_qbf_inf_nan(orc, env):
+    # Infinite and NaN activations: each output is inf, -inf or nan exactly
+    # where the reference's fp32 product is (inf . 0 = nan included), the
+    # other rows within the bound.
+    env["TML_GEMM_QBF"] = "2"
+    m, n, k = 40, 300, 1280
+    w = rnd(331, k, n, 0.02)
+    a = rnd(332, m, k)
+    a[1, 5] = np.inf
+    a[1, 700] = -np.inf
+    a[2, 9] = np.nan
+    a[30, 1279] = np.inf
+    for fmt, b, scale, scales, ref in _cases(orc, w, k, n, a):
+        got = _gemm(fmt, m, n, k, a, b, scale, scales)
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+        np.testing.assert_array_equal(np.isposinf(got), np.isposinf(ref))
+        np.testing.assert_array_equal(np.isneginf(got), np.isneginf(ref))
+        fin = np.isfinite(ref)
+        assert rel_err(got[fin], ref[fin]) <= TOL, fmt
+
+
+def test_qbf_off_switch_agrees(orc, env):
+    # TML_GEMM_QBF=0 runs the fp32-MFMA kernels on the same problem: both
+    # within the bound of the oracle, and of each other.
+    m, n, k = 96, 256, 512
+    w = rnd(341, k, n, 0.02)
+    a = rnd(342, m, k)
+    for fmt, b, scale, scales, ref in _cases(orc, w, k, n, a):
+        env["TML_GEMM_QBF"] = "2"
+        got = _gemm(fmt, m, n, k, a, b, scale, scales)
+        env["TML_GEMM_QBF"] = "0"
+        old = _gemm(fmt, m, n, k, a, b, scale, scales)
+        env.pop("TML_GEMM_QBF")
+        assert rel_err(got, ref) <= TOL and rel_err(old, ref) <= 1e-5 and rel_err(got, old) <= TOL, fmt

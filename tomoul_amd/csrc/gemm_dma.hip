@@ -872,17 +872,20 @@ Status launch_gemm_f32_dma(const MatmulArgs &m, const GemmPlan &p, const Workspa
     }
     TML_TRY(st);
     TML_HIP_TRY(hipGetLastError());
-    if (p.nsplit > 1 && !p.fused) {
-        const int64_t n4 = (m.M * m.N + 3) / 4;
-        const int64_t blocks = (n4 + 255) / 256;
-        splitk_reduce_kernel<<<dim3((unsigned)(blocks < 65535 ? blocks : 65535)), 256, 0, s>>>(
-            ws.partials, p.nsplit, m.M * m.N, m.N, m.C, m.alpha_eff, m.beta, m.bias, m.res, m.colscale,
-            m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0) &&
-                (m.res == nullptr || ((uintptr_t)m.res % 16) == 0) &&
-                (m.colscale == nullptr || ((uintptr_t)m.colscale % 16) == 0),
-            m.act, tml_act_tail0((long long)m.M * m.N));
-        TML_HIP_TRY(hipGetLastError());
-    }
+    if (p.nsplit > 1 && !p.fused) TML_TRY(launch_splitk_reduce(ws.partials, p.nsplit, m, s));
+    return Status::Ok();
+}
+
+Status launch_splitk_reduce(const float *partials, int nsplit, const MatmulArgs &m, hipStream_t s) {
+    const int64_t n4 = (m.M * m.N + 3) / 4;
+    const int64_t blocks = (n4 + 255) / 256;
+    splitk_reduce_kernel<<<dim3((unsigned)(blocks < 65535 ? blocks : 65535)), 256, 0, s>>>(
+        partials, nsplit, m.M * m.N, m.N, m.C, m.alpha_eff, m.beta, m.bias, m.res, m.colscale,
+        m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0) &&
+            (m.res == nullptr || ((uintptr_t)m.res % 16) == 0) &&
+            (m.colscale == nullptr || ((uintptr_t)m.colscale % 16) == 0),
+        m.act, tml_act_tail0((long long)m.M * m.N));
+    TML_HIP_TRY(hipGetLastError());
     return Status::Ok();
 }
 

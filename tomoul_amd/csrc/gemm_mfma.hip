@@ -586,6 +586,23 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
 
 GemmPlan plan_gemm(const MatmulArgs &m) {
     GemmPlan p;
+    // Q8_0 / Q4_0 (per-tensor or per-column scales) take the bf16
+    // matrix-core kernel whenever its layout conditions hold (gemm_qbf.hip),
+    // unless TML_GEMM_QBF=0 or an override asks for a tile or K split of the
+    // fp32-MFMA kernels below (tests of those kernels).
+    auto set = [](const char *k) {
+        const char *v = std::getenv(k);
+        return v != nullptr && *v != '\0';
+    };
+    const bool fp32_forced = set("TML_GEMM_DMA_Q") || set("TML_GEMM_TILE") || set("TML_GEMM_DMA_TILE") ||
+                             set("TML_GEMM_SPLIT");
+    if (!fp32_forced && gemm_qbf_supported(m) && (m.M >= 256 || env_int("TML_GEMM_QBF", 1) == 2 ||
+                                                  env_int("TML_GEMM_QBF_TILE", 0) > 0 ||
+                                                  env_int("TML_GEMM_QBF_SPLIT", 0) > 0)) {
+        p.qbf = true;
+        pick_qbf(m, &p);
+        return p;
+    }
     // f32 B takes the direct-copy kernel whenever its rows allow it.  For
     // the narrow formats both kernels read B through buffer resources and
     // the direct-copy kernel reads two adjacent columns per LDS access;
@@ -627,6 +644,7 @@ void gemm_workspace_need(const MatmulArgs &m, size_t *partial_floats, size_t *co
     const GemmPlan p = plan_gemm(m);
     *partial_floats = 0;
     *counters = 0;
+    if (p.qbf && p.nsplit > 1) *partial_floats = (size_t)p.nsplit * (size_t)m.M * (size_t)m.N;
     if (p.dma && p.nsplit > 1) gemm_dma_workspace_need(m, p, partial_floats, counters);
 }
 
@@ -649,7 +667,7 @@ constexpr uint64_t kForcedPlanMaxMNK = TML_FORCED_PLAN_MAX_MNK;
 bool plan_forced() {
     static const char *const keys[] = {"TML_GEMM_DMA_TILE", "TML_GEMM_SPLIT", "TML_GEMM_TILE",  "TML_GEMM_DMA_Q",
                                        "TML_GEMM_DMA",      "TML_GEMM_FUSED", "TML_GEMM_XCDPART", "TML_GEMM_XCD",
-                                       "TML_GEMM_GROUPM"};
+                                       "TML_GEMM_GROUPM",   "TML_GEMM_QBF_TILE", "TML_GEMM_QBF_SPLIT"};
     for (const char *k : keys) {
         const char *v = std::getenv(k);
         if (v != nullptr && *v != '\0') return true;
@@ -668,6 +686,7 @@ Status launch_gemm_mfma(const MatmulArgs &m, const Workspace &ws, hipStream_t s)
                            "forced GEMM plans (TML_GEMM_* overrides) are refused above M*N*K = 512*1024*4096, "
                            "the largest size the tests run them at");
     const GemmPlan p = plan_gemm(m);
+    if (p.qbf) return launch_gemm_qbf(m, p, ws, s);
     if (p.dma) return launch_gemm_f32_dma(m, p, ws, s);
     const int cus = device_cus();
     switch (m.fmt) {

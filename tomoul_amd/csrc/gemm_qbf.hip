@@ -1,0 +1,451 @@
+// gemm_qbf.hip -- Q8_0 / Q4_0 weight-only GEMM for M > 8 on the bf16 matrix
+// cores, the weights dequantized into LDS.
+//
+//   C[M,N] = act(alpha * A[M,K] . q[K,N] + beta * C + bias[N] + R)
+//   (q: int8, or int4 two per byte, even n in the low nibble; alpha carries
+//   the per-tensor scale, colscale the per-column ones of the _PC formats)
+//
+// The reference multiplies fp32 activations by dequantized weights and
+// accumulates in fp32 (src/core/quantization.zig:240-311 Q8_0,
+// :829-957 Q4_0).  Here the products run on v_mfma_f32_16x16x32_bf16 with
+// fp32 accumulation:
+//   * weights: int8 and int4 values are exact in bf16, so B is converted
+//     once per workgroup when a slice is staged in LDS;
+//   * activations: each fp32 x is split into hi = bf16(x) and lo =
+//     bf16(x - hi), round to nearest even both, so |x - hi - lo| <= 2^-17 |x|
+//     (an infinite x keeps lo = 0); the product is hi . q + lo . q, two
+//     MFMAs into the same fp32 accumulator.
+// The result equals the dequantize-then-fp32-accumulate product to ~1e-5
+// relative (summation order and the 2^-17 split), inside the 1e-3 bar of the
+// quantized paths.  A bf16 MFMA does 16x the work of the fp32 MFMA of the
+// other GEMM kernels in half the cycles, so even the two of them per product
+// leave the kernel bound by its LDS traffic, not by the matrix cores.
+//
+// Tiles.  A workgroup of four waves owns a BM x BN tile of C (each wave a
+// WM x WN sub-tile of (WM/16) x (WN/16) MFMA tiles) and walks K in 32-deep
+// slices through two LDS stages: the next slice's global loads are issued
+// before the current slice's MFMAs, converted and written after them, one
+// barrier a slice.  LDS holds, per stage, A's hi and lo planes and B as bf16,
+// each as rows of four 16-byte slots (8 k each) -- A by output row, B by
+// output column, both k-contiguous as the MFMA operands want them -- with
+// slot s of row r stored at s ^ ((r / 4) % 4), which keeps the operand reads
+// (16 rows, one slot) and the staging writes free of bank conflicts.
+#include "tml_internal.hpp"
+
+#include <algorithm>
+
+namespace tml {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uintx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+constexpr int kQbfXcd = 8;  // XCDs of an MI355X: workgroups are dealt to them round robin
+
+struct QbfArgs {
+    int M, N, K;
+    const float *A;         // [M,K], K % 8 == 0, 16-byte aligned
+    const uint8_t *B;       // [K,N]: N bytes a row (int8) or N / 2 (int4)
+    int ldb;                // bytes per B row
+    const float *bias;      // [N] or nullptr
+    const float *colscale;  // [N] per-column factor on A.B, or nullptr
+    const float *res;       // [M,N] residual after the bias, or nullptr (may equal C)
+    float *C;
+    float alpha, beta;
+    int act;
+    long long tail0;
+    unsigned a_bytes, b_bytes;  // M * K * 4, K * ldb
+    int tiles_m, tiles_n;
+    int nsplit, spl;        // K splits, 32-deep slices per split
+    float *ws;              // nsplit > 1: [nsplit][M][N] raw partials
+};
+
+__device__ __forceinline__ uintx4 qbf_load16(const void *base, unsigned nbytes, unsigned off) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)nbytes, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t qbf_load2(const void *base, unsigned nbytes, unsigned off) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)nbytes, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t qbf_load1(const void *base, unsigned nbytes, unsigned off) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)nbytes, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+
+// Two floats to two bf16 (round to nearest even), a in the low half.
+__device__ __forceinline__ uint32_t qbf_pk(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, bf16x2));
+}
+// hi = bf16(x), lo = bf16(x - hi) of a pair; an infinite x gets lo = 0 (x - hi
+// would be NaN), so x . q stays the reference's inf . q.
+__device__ __forceinline__ void qbf_split(float a, float b, uint32_t &hi, uint32_t &lo) {
+    hi = qbf_pk(a, b);
+    const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
+    lo = qbf_pk(ra == ra ? ra : 0.0f, rb == rb ? rb : 0.0f);
+}
+
+// Physical slot of logical slot s (8 k) in LDS row r.
+__device__ __forceinline__ int qbf_slot(int r, int s) { return r * 4 + (s ^ ((r >> 2) & 3)); }
+
+template <int FMT, int BM, int BN, int WM, int WN, int D>
+__global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
+    constexpr int NT = 256;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    constexpr int WAVES_N = BN / WN;
+    static_assert((BM / WM) * (BN / WN) == 4, "four waves, one per WM x WN sub-tile");
+    static_assert(WM % 16 == 0 && WN % 16 == 0, "whole 16 x 16 MFMA tiles");
+    // staging tasks of a slice: A one (row, 8-k slot) each; B one (column
+    // pair, 8-k slot) each
+    constexpr int TA = BM * 4, TB = (BN / 2) * 4;
+    constexpr int PA = (TA + NT - 1) / NT, PB = (TB + NT - 1) / NT;
+    static_assert(TA % NT == 0 || TA < NT, "A tasks split evenly");
+
+    __shared__ uintx4 Ah[2][BM * 4], Al[2][BM * 4], Bs[2][BN * 4];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
+    const int c = lane & 15, g = lane >> 4;
+
+    // Workgroup -> (tile, K split): consecutive ids within each XCD (own
+    // L2), the splits of a tile adjacent, then groups of four tile rows so
+    // that neighbours share A rows and B columns.
+    int tile_m, tile_n, split;
+    {
+        const int nblk = gridDim.x, b = blockIdx.x;
+        const int per = nblk / kQbfXcd, rem = nblk % kQbfXcd;
+        const int xcd = b % kQbfXcd, idx = b / kQbfXcd;
+        const int lin = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+        split = lin % a.nsplit;
+        const int tlin = lin / a.nsplit;
+        constexpr int GM = 4;
+        const int group = GM * a.tiles_n;
+        const int first_m = (tlin / group) * GM;
+        const int gsize = min(a.tiles_m - first_m, GM);
+        tile_m = first_m + (tlin % group) % gsize;
+        tile_n = (tlin % group) / gsize;
+    }
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    // this split's k range [kbase, kend)
+    const int kbase = split * a.spl * 32, kend = min(a.K, kbase + a.spl * 32);
+
+    // ---- staging: global -> registers, D slices ahead -> bf16 in LDS (after
+    // the MFMAs of the slice before).  Offsets are formed without branches
+    // (a branch around a load makes the compiler wait for every load in
+    // flight): rows of A past M and k-rows of B past K lie past the buffer's
+    // byte count and read zeros; A slots past the split's end get bit 31 set
+    // (past every byte count) so they read zeros instead of the next row or
+    // the next split's k (B rows there are finite integers times those
+    // zeros); B columns past N read bytes of the next k-row that only feed
+    // dropped outputs; tasks past TA / TB (small tiles) repeat a valid task's
+    // loads and skip its store.  k0 counts from kbase.
+    uintx4 ra[D][PA][2];
+    uint32_t rb[D][PB][8];
+    auto load = [&](int d, int k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < PA; ++p) {
+            const int j = (tid + p * NT) % TA;
+            const int row = j >> 2, k = kbase + k0 + 8 * (j & 3);
+            const unsigned past_k = (unsigned)(kend - 1 - k) & 0x80000000u;
+            const unsigned off = (((unsigned)(m0 + row) * (unsigned)a.K + (unsigned)k) * 4u) | past_k;
+            ra[d][p][0] = qbf_load16(a.A, a.a_bytes, off);
+            ra[d][p][1] = qbf_load16(a.A, a.a_bytes, off + 16u);
+        }
+#pragma unroll
+        for (int p = 0; p < PB; ++p) {
+            const int j = (tid + p * NT) % TB;
+            const int cp = j % (BN / 2), s = j / (BN / 2);
+            const unsigned col_byte = FMT == TML_FMT_Q8_0 ? (unsigned)(n0 + 2 * cp) : (unsigned)((n0 + 2 * cp) / 2);
+            const unsigned off0 = (unsigned)(kbase + k0 + 8 * s) * (unsigned)a.ldb + col_byte;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const unsigned off = off0 + (unsigned)kk * (unsigned)a.ldb;
+                rb[d][p][kk] = FMT == TML_FMT_Q8_0 ? qbf_load2(a.B, a.b_bytes, off) : qbf_load1(a.B, a.b_bytes, off);
+            }
+        }
+    };
+    auto store = [&](int d, int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < PA; ++p) {
+            const int j = tid + p * NT;
+            if (TA % NT == 0 || j < TA) {
+                const int row = j >> 2, s = j & 3;
+                const floatx4 x0 = __builtin_bit_cast(floatx4, ra[d][p][0]), x1 = __builtin_bit_cast(floatx4, ra[d][p][1]);
+                uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+                qbf_split(x0[0], x0[1], h0, l0);
+                qbf_split(x0[2], x0[3], h1, l1);
+                qbf_split(x1[0], x1[1], h2, l2);
+                qbf_split(x1[2], x1[3], h3, l3);
+                Ah[st][qbf_slot(row, s)] = (uintx4){h0, h1, h2, h3};
+                Al[st][qbf_slot(row, s)] = (uintx4){l0, l1, l2, l3};
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PB; ++p) {
+            const int j = tid + p * NT;
+            if (TB % NT == 0 || j < TB) {
+                const int cp = j % (BN / 2), s = j / (BN / 2);
+                uintx4 e, o;  // columns 2 cp (even) and 2 cp + 1, k = 8 s .. 8 s + 7
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    uint32_t w0 = rb[d][p][2 * q], w1 = rb[d][p][2 * q + 1];
+                    // pin the words here: otherwise the compiler moves part of
+                    // the unpacking of a set loaded this step up to the step's
+                    // end, where it must wait for every load in flight
+                    __asm__ volatile("" : "+v"(w0), "+v"(w1));
+                    if constexpr (FMT == TML_FMT_Q8_0) {
+                        e[q] = qbf_pk((float)(int8_t)(w0 & 0xFFu), (float)(int8_t)(w1 & 0xFFu));
+                        o[q] = qbf_pk((float)(int8_t)(w0 >> 8), (float)(int8_t)(w1 >> 8));
+                    } else {
+                        e[q] = qbf_pk((float)((int32_t)(w0 << 28) >> 28), (float)((int32_t)(w1 << 28) >> 28));
+                        o[q] = qbf_pk((float)((int32_t)(w0 << 24) >> 28), (float)((int32_t)(w1 << 24) >> 28));
+                    }
+                }
+                Bs[st][qbf_slot(2 * cp, s)] = e;
+                Bs[st][qbf_slot(2 * cp + 1, s)] = o;
+            }
+        }
+    };
+
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
+    // One 32-deep slice: lane (c, g) reads k = 8 g .. 8 g + 7 of A rows
+    // wm0 + 16 i + c (hi and lo) and of B columns wn0 + 16 j + c.  All hi
+    // products first, then the lo ones, so no MFMA waits on the one before.
+    auto compute = [&](int st) __attribute__((always_inline)) {
+        bf16x8 ah[TM], al[TM], bv[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int slot = qbf_slot(wm0 + 16 * i + c, g);
+            ah[i] = __builtin_bit_cast(bf16x8, Ah[st][slot]);
+            al[i] = __builtin_bit_cast(bf16x8, Al[st][slot]);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bv[j] = __builtin_bit_cast(bf16x8, Bs[st][qbf_slot(wn0 + 16 * j + c, g)]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bv[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bv[j], acc[i][j], 0, 0, 0);
+    };
+
+    // Register set d holds slice kt with kt % D == d: slices 0 .. D-1 are
+    // requested up front, and each step refills the set its slice left (slice
+    // kt + D) before the MFMAs, so D slices of loads are in flight while a
+    // slice is multiplied.  The step count is rounded up to a multiple of D
+    // (D even): steps past K multiply zeros, and every step of the unrolled
+    // body is the same straight-line code with its LDS stage fixed.
+    static_assert(D % 2 == 0, "LDS stage of step u is u % 2");
+    const int nk = ((kend - kbase + 31) / 32 + D - 1) / D * D;
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(d, d * 32);
+    store(0, 0);
+    __syncthreads();
+    for (int kt0 = 0; kt0 < nk; kt0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            // the scheduler keeps the three phases in this order, so the
+            // loads of a set are always older than the D - 1 sets after it
+            load(u, (kt0 + u + D) * 32);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(u & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            store((u + 1) % D, (u + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+        }
+    }
+
+    // Epilogue: lane (c, g) holds rows 4 g + r, column c of each MFMA tile.
+    if (a.nsplit > 1) {
+        // raw partial of this split; launch_splitk_reduce adds the splits in
+        // order and runs the epilogue
+        float *const part = a.ws + (size_t)split * a.M * a.N;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn0 + 16 * j + c;
+            if (col >= a.N) continue;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wm0 + 16 * i + 4 * g + r;
+                    if (row < a.M) part[(size_t)row * a.N + col] = acc[i][j][r];
+                }
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn0 + 16 * j + c;
+        if (col >= a.N) continue;
+        const float colf = a.colscale ? a.alpha * a.colscale[col] : a.alpha;
+        const float biasc = a.bias ? a.bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm0 + 16 * i + 4 * g + r;
+                if (row < a.M) {
+                    const long long flat = (long long)row * a.N + col;
+                    float v = colf * acc[i][j][r];
+                    if (a.beta != 0.0f) v += a.beta * a.C[flat];
+                    if (a.bias) v += biasc;
+                    if (a.res) v += a.res[flat];
+                    a.C[flat] = tml_apply_act(v, a.act, flat, a.tail0);
+                }
+            }
+    }
+}
+
+struct QbfCfg {
+    int bm, bn;
+};
+// Tile configs (index = TML_GEMM_QBF_TILE - 1): <BM, BN> with four waves of
+// BM/2 x BN/2.  The two large tiles keep two slices of loads in flight (D =
+// 2: 130 / 100 registers, two and three workgroups a CU), the small ones
+// four; at the large tiles D = 2 measured as fast as or faster than D = 4,
+// which holds one workgroup a CU at 128 x 128.
+constexpr QbfCfg kQbfCfgs[] = {{128, 128}, {64, 128}, {64, 64}, {32, 64}};
+constexpr int kQbfNumCfgs = (int)(sizeof(kQbfCfgs) / sizeof(kQbfCfgs[0]));
+
+template <int FMT>
+void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
+    switch (cfg) {
+        case 0: gemm_qbf_kernel<FMT, 128, 128, 64, 64, 2><<<grid, 256, 0, s>>>(a); break;
+        case 1: gemm_qbf_kernel<FMT, 64, 128, 32, 64, 2><<<grid, 256, 0, s>>>(a); break;
+        case 2: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 4><<<grid, 256, 0, s>>>(a); break;
+        default: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 4><<<grid, 256, 0, s>>>(a); break;
+    }
+}
+
+}  // namespace
+
+// Tile and K split: forced by TML_GEMM_QBF_TILE / TML_GEMM_QBF_SPLIT, else
+// the first of (split 1..4, then tile 128x128, 64x128; then the same over
+// 64x64, 32x64) whose units (tiles x splits) give every CU about two to three
+// workgroups, 1.75 to 3 x CUs, with at least eight 32-deep slices a split.  Measured on MI355X
+// (Q8_0 / Q4_0, us): 1500x3840x1280 64x128 unsplit 51.8 (128x128 split 2:
+// 63); 1500x5120x1280 128x128 unsplit 62 (64x128: 69.5); 1500x1280x5120
+// 64x128 split 2 70.2 (best 128x128 split 4: 64.9; unsplit 99.7);
+// 512x4096x1024 64x128 split 2 25.0.  No such plan: the largest tile
+// unsplit when even it has more units, else the plan with the most units.
+// Splits stay within the caller's workspace cap.
+void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+    }
+    const int64_t nk = (m.K + 31) / 32;
+    auto tiles_of = [&](int c) {
+        return ((m.M + kQbfCfgs[c].bm - 1) / kQbfCfgs[c].bm) * ((m.N + kQbfCfgs[c].bn - 1) / kQbfCfgs[c].bn);
+    };
+    auto fits = [&](int64_t ns) { return ns == 1 || (size_t)ns * (size_t)m.M * (size_t)m.N <= m.ws_cap_floats; };
+    int cfg = -1;
+    int64_t nsplit = 1;
+    const double lo = 1.75 * cus, hi = 3.0 * cus;
+    for (int c0 = 0; c0 < kQbfNumCfgs && cfg < 0; c0 += 2)
+        for (int64_t ns = 1; ns <= 4 && cfg < 0; ++ns) {
+            if (ns > 1 && (nk / ns < 8 || !fits(ns))) break;
+            for (int c = c0; c < c0 + 2 && cfg < 0; ++c) {
+                const double units = (double)tiles_of(c) * ns;
+                if (units >= lo && units <= hi) {
+                    cfg = c;
+                    nsplit = ns;
+                }
+            }
+        }
+    if (cfg < 0) {
+        if ((double)tiles_of(0) > hi) {
+            cfg = 0;
+        } else {
+            int64_t best = -1;
+            for (int64_t ns = 1; ns <= 4; ++ns) {
+                if (ns > 1 && (nk / ns < 8 || !fits(ns))) break;
+                for (int c = 0; c < kQbfNumCfgs; ++c)
+                    if (tiles_of(c) * ns > best) {
+                        best = tiles_of(c) * ns;
+                        cfg = c;
+                        nsplit = ns;
+                    }
+            }
+        }
+    }
+    const int forced_tile = env_int("TML_GEMM_QBF_TILE", 0) - 1;
+    if (forced_tile >= 0 && forced_tile < kQbfNumCfgs) cfg = forced_tile;
+    const int forced = env_int("TML_GEMM_QBF_SPLIT", 0);
+    if (forced >= 1) nsplit = std::min<int64_t>(forced, nk);
+    int64_t spl = (nk + nsplit - 1) / nsplit;
+    nsplit = (nk + spl - 1) / spl;  // no split without slices
+    if (!fits(nsplit)) {
+        nsplit = 1;
+        spl = nk;
+    }
+    p->cfg = cfg;
+    p->nsplit = (int)nsplit;
+    p->spl = (int)std::max<int64_t>(spl, 1);
+    p->tiles = (int)tiles_of(cfg);
+}
+
+bool gemm_qbf_supported(const MatmulArgs &m) {
+    if (m.fmt != TML_FMT_Q8_0 && m.fmt != TML_FMT_Q4_0) return false;
+    if (m.M <= kGemvMaxM || m.K <= 0 || m.K % 8 != 0 || m.N % 2 != 0 || ((uintptr_t)m.A % 16) != 0) return false;
+    if (env_int("TML_GEMM_QBF", 1) == 0) return false;
+    // every buffer offset below 2^31: A rows up to M + 128, B k-rows up to K + 288
+    const uint64_t lim = (uint64_t)1 << 31;
+    const uint64_t ldb = m.fmt == TML_FMT_Q8_0 ? (uint64_t)m.N : (uint64_t)m.N / 2;
+    // (the loads run up to 2 x 4 slices past K, zero-filled)
+    return (uint64_t)(m.M + 128) * (uint64_t)m.K * 4u < lim && (uint64_t)(m.K + 288) * ldb < lim &&
+           m.M < ((int64_t)1 << 30) && m.N < ((int64_t)1 << 30);
+}
+
+Status launch_gemm_qbf(const MatmulArgs &m, const GemmPlan &p, const Workspace &ws, hipStream_t s) {
+    if (!gemm_qbf_supported(m))
+        return Status::Err(TML_ERR_INVALID_ARG, "bf16 matrix-core GEMM: needs Q8_0 / Q4_0, M > 8, K % 8 == 0, even N, "
+                                                "16-byte aligned A");
+    QbfArgs a;
+    a.M = (int)m.M; a.N = (int)m.N; a.K = (int)m.K;
+    a.A = m.A; a.B = (const uint8_t *)m.B;
+    a.ldb = (int)(m.fmt == TML_FMT_Q8_0 ? m.N : m.N / 2);
+    a.bias = m.bias; a.colscale = m.colscale; a.res = m.res; a.C = m.C;
+    a.alpha = m.alpha_eff; a.beta = m.beta;
+    a.act = m.act;
+    a.tail0 = tml_act_tail0((long long)m.M * m.N);
+    a.a_bytes = (unsigned)((uint64_t)m.M * (uint64_t)m.K * 4u);
+    a.b_bytes = (unsigned)((uint64_t)m.K * (uint64_t)a.ldb);
+    const int cfg = p.cfg;
+    if (cfg < 0 || cfg >= kQbfNumCfgs) return Status::Err(TML_ERR_INVALID_ARG, "bf16 matrix-core GEMM: bad tile config");
+    const int64_t nk = (m.K + 31) / 32;
+    if (p.nsplit < 1 || p.spl < 1 || (int64_t)p.spl * p.nsplit < nk || (int64_t)p.spl * (p.nsplit - 1) >= nk)
+        return Status::Err(TML_ERR_INVALID_ARG, "bf16 matrix-core GEMM: split plan does not cover K");
+    if (p.nsplit > 1 && (ws.partials == nullptr || ws.partial_floats < (size_t)p.nsplit * (size_t)m.M * (size_t)m.N))
+        return Status::Err(TML_ERR_INVALID_ARG, "bf16 matrix-core GEMM: split-K workspace too small");
+    a.tiles_m = (int)((m.M + kQbfCfgs[cfg].bm - 1) / kQbfCfgs[cfg].bm);
+    a.tiles_n = (int)((m.N + kQbfCfgs[cfg].bn - 1) / kQbfCfgs[cfg].bn);
+    a.nsplit = p.nsplit;
+    a.spl = p.spl;
+    a.ws = p.nsplit > 1 ? ws.partials : nullptr;
+    const int64_t grid = (int64_t)a.tiles_m * a.tiles_n * p.nsplit;
+    if (grid >= ((int64_t)1 << 31)) return Status::Err(TML_ERR_INVALID_SHAPE, "bf16 matrix-core GEMM: grid too large");
+    if (m.fmt == TML_FMT_Q8_0) launch_qbf_cfg<TML_FMT_Q8_0>(cfg, (unsigned)grid, a, s);
+    else launch_qbf_cfg<TML_FMT_Q4_0>(cfg, (unsigned)grid, a, s);
+    TML_HIP_TRY(hipGetLastError());
+    if (p.nsplit > 1) TML_TRY(launch_splitk_reduce(ws.partials, p.nsplit, m, s));
+    return Status::Ok();
+}
+
+}  // namespace tml

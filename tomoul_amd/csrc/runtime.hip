@@ -350,9 +350,10 @@ Status gemm_dev_noalloc(int fmt, int64_t M, int64_t N, int64_t K, const float *A
     if (empty) return Status::Ok();
     void *base = nullptr;
     TML_TRY(scratch_setup(s, &base));
+    const size_t cap_floats = (kScratchBytes - kScratchPartialOff) / sizeof(float);
+    m.ws_cap_floats = cap_floats;
     size_t pf = 0, nc = 0;
     workspace_need(m, &pf, &nc);
-    const size_t cap_floats = (kScratchBytes - kScratchPartialOff) / sizeof(float);
     if (pf > cap_floats || nc > kScratchCounters)
         return Status::Err(TML_ERR_INVALID_SHAPE,
                            "this problem's split-K plan needs " + std::to_string(pf * sizeof(float)) +

@@ -63,6 +63,10 @@ struct MatmulArgs {
     int act = TML_ACT_NONE;  // activation after the bias (TML_ACT_*)
     const float *res = nullptr;  // [M,N] residual added after the bias (may equal C)
     const float *colscale = nullptr;  // [N] per-column factor on A.B (per-channel formats), or nullptr
+    // Largest split-K workspace (partial floats) the caller can supply; the
+    // planners keep their K splits within it (the allocation-free entry
+    // point's static scratch).
+    size_t ws_cap_floats = SIZE_MAX;
 };
 
 // Activations of the epilogue, restating the reference's CPU code.
@@ -158,6 +162,7 @@ struct GemmPlan {
     int spl = 0;       // BK-slices per split
     int tiles = 0;
     bool fused = false;  // split-K partials combined in the GEMM kernel (no reduce launch)
+    bool qbf = false;    // Q8_0 / Q4_0 on the bf16 matrix cores (gemm_qbf.hip; cfg, nsplit, spl its plan)
 };
 GemmPlan plan_gemm(const MatmulArgs &a);
 void gemm_workspace_need(const MatmulArgs &a, size_t *partial_floats, size_t *counters);
@@ -170,6 +175,15 @@ bool gemm_dma_cfg_ok(int cfg, int fmt);  // the tile config has a kernel for B f
 void gemm_dma_tile(int cfg, int *bm, int *bn, int *bk);
 bool gemm_dma_cfg_fusable(int cfg);  // the tile config can combine K splits in the kernel
 Status launch_gemm_f32_dma(const MatmulArgs &a, const GemmPlan &p, const Workspace &ws, hipStream_t s);
+// Q8_0 / Q4_0 weight-only GEMM on the bf16 matrix cores (gemm_qbf.hip):
+// M > kGemvMaxM, K % 8 == 0, even N, 16-byte aligned A.  pick_qbf sets
+// p->cfg / nsplit / spl; K splits write nsplit * M * N partial floats that
+// launch_splitk_reduce sums.
+bool gemm_qbf_supported(const MatmulArgs &a);
+void pick_qbf(const MatmulArgs &a, GemmPlan *p);
+Status launch_gemm_qbf(const MatmulArgs &a, const GemmPlan &p, const Workspace &ws, hipStream_t s);
+// C = act(alpha * sum of the nsplit [M,N] partials (in split order) * colscale + beta * C + bias + res).
+Status launch_splitk_reduce(const float *partials, int nsplit, const MatmulArgs &a, hipStream_t s);
 void gemm_dma_workspace_need(const MatmulArgs &a, const GemmPlan &p, size_t *partial_floats, size_t *counters);
 Status launch_gemv(const MatmulArgs &a, const Workspace &ws, hipStream_t s);
 // Workspace needed by launch_gemv for this problem.
