@@ -103,6 +103,8 @@ def parse():
                    help="only the XLM-R layer step (config 2), for kernel traces")
     p.add_argument("--config1-only", action="store_true",
                    help="only config 1 (Whisper-tiny MLP + bias, 20 launches per replay), for kernel traces")
+    p.add_argument("--config5-quant-only", action="store_true",
+                   help="only the config-5 sweep with Q8_0 / Q4_0 weights (bf16 matrix-core GEMM), for kernel traces")
     p.add_argument("--profile-gemv", action="store_true",
                    help="only run the decoder GEMVs (configs 3/4, M = 1) 50 times per path, eagerly, for rocprofv3")
     return p.parse_args()
@@ -229,6 +231,9 @@ def main():
     wdev = [[torch.from_numpy(w).to(dev) for w in layer] for layer in host_w]
     outs = [torch.empty((M, N), dtype=torch.float32, device=dev) for (_, M, N, K) in ENC_SHAPES]
     sweep_flops = L * sum(2.0 * M * N * K for (_, M, N, K) in ENC_SHAPES)
+    if args.config5_quant_only:
+        print(json.dumps({"config5_q": bench_config5_quant(torch, dev, sptr, _abi, wdev, x, h, outs, L)}), flush=True)
+        return
 
     def sweep(st=sptr, layers=None):
         for li in (range(L) if layers is None else layers):
