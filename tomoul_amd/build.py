@@ -36,9 +36,15 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP backend cannot be built")
 
 
+# Per-source flags.  gemm_qbf.hip: keep MFMA accumulators in ordinary VGPRs
+# (the compiler otherwise splits them over the accumulation registers and
+# copies them back and forth inside the K loop: 72 extra moves a loop trip).
+SOURCE_FLAGS = {"gemm_qbf.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str, obj_dir: str) -> str:
     obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")

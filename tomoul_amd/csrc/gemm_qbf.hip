@@ -84,7 +84,9 @@ __device__ __forceinline__ uint32_t qbf_pk(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, bf16x2));
 }
 // hi = bf16(x), lo = bf16(x - hi) of a pair; an infinite x gets lo = 0 (x - hi
-// would be NaN), so x . q stays the reference's inf . q.
+// would be NaN), so x . q stays the reference's inf . q.  (Clamping the
+// residual with fminf / fmaxf instead compiles to v_med3_f32, which returned
+// NaN for the NaN residual on MI355X.)
 __device__ __forceinline__ void qbf_split(float a, float b, uint32_t &hi, uint32_t &lo) {
     hi = qbf_pk(a, b);
     const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
@@ -316,9 +318,10 @@ struct QbfCfg {
 };
 // Tile configs (index = TML_GEMM_QBF_TILE - 1): <BM, BN> with four waves of
 // BM/2 x BN/2.  The two large tiles keep two slices of loads in flight (D =
-// 2: 130 / 100 registers, two and three workgroups a CU), the small ones
-// four; at the large tiles D = 2 measured as fast as or faster than D = 4,
-// which holds one workgroup a CU at 128 x 128.
+// 2: 170 / 117 registers with the accumulators in ordinary VGPRs, two and
+// four workgroups a CU), the small ones four; at the large tiles D = 2
+// measured as fast as or faster than D = 4, which holds one workgroup a CU at
+// 128 x 128.
 constexpr QbfCfg kQbfCfgs[] = {{128, 128}, {64, 128}, {64, 64}, {32, 64}};
 constexpr int kQbfNumCfgs = (int)(sizeof(kQbfCfgs) / sizeof(kQbfCfgs[0]));
 
@@ -335,14 +338,16 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
 }  // namespace
 
 // Tile and K split: forced by TML_GEMM_QBF_TILE / TML_GEMM_QBF_SPLIT, else
-// the first of (split 1..4, then tile 128x128, 64x128; then the same over
-// 64x64, 32x64) whose units (tiles x splits) give every CU about two to three
-// workgroups, 1.75 to 3 x CUs, with at least eight 32-deep slices a split.  Measured on MI355X
-// (Q8_0 / Q4_0, us): 1500x3840x1280 64x128 unsplit 51.8 (128x128 split 2:
-// 63); 1500x5120x1280 128x128 unsplit 62 (64x128: 69.5); 1500x1280x5120
-// 64x128 split 2 70.2 (best 128x128 split 4: 64.9; unsplit 99.7);
-// 512x4096x1024 64x128 split 2 25.0.  No such plan: the largest tile
-// unsplit when even it has more units, else the plan with the most units.
+//   * 64x128 unsplit when its tiles give each CU 1.75 to 4.5 workgroups
+//     (117 registers, LDS for four a CU);
+//   * 128x128 unsplit when 64x128 gives more than 4.5;
+//   * else the tile (64x128, then 64x64, then 32x64) and the fewest K splits
+//     (2..4, at least eight 32-deep slices a split) that reach 2.75 units
+//     (tiles x splits) a CU, or the most units found.
+// Measured on MI355X (Q8_0 / Q4_0, us): 1500x3840x1280 64x128 unsplit
+// 48.1 / 48.9 (128x128: 61); 1500x5120x1280 64x128 unsplit 59.5 / 59.0
+// (128x128: 61.8); 1500x1280x5120 64x128 split 3 61.1 / 62.8 (split 2:
+// 65.7; unsplit 91); 512x4096x1024 64x128 split 3 24.5 (split 2: 24.1).
 // Splits stay within the caller's workspace cap.
 void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     int dev = 0, cus = 256;
@@ -354,35 +359,29 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     auto tiles_of = [&](int c) {
         return ((m.M + kQbfCfgs[c].bm - 1) / kQbfCfgs[c].bm) * ((m.N + kQbfCfgs[c].bn - 1) / kQbfCfgs[c].bn);
     };
-    auto fits = [&](int64_t ns) { return ns == 1 || (size_t)ns * (size_t)m.M * (size_t)m.N <= m.ws_cap_floats; };
-    int cfg = -1;
+    auto split_ok = [&](int64_t ns) {
+        return ns == 1 || (nk / ns >= 8 && (size_t)ns * (size_t)m.M * (size_t)m.N <= m.ws_cap_floats);
+    };
+    int cfg = 1;
     int64_t nsplit = 1;
-    const double lo = 1.75 * cus, hi = 3.0 * cus;
-    for (int c0 = 0; c0 < kQbfNumCfgs && cfg < 0; c0 += 2)
-        for (int64_t ns = 1; ns <= 4 && cfg < 0; ++ns) {
-            if (ns > 1 && (nk / ns < 8 || !fits(ns))) break;
-            for (int c = c0; c < c0 + 2 && cfg < 0; ++c) {
-                const double units = (double)tiles_of(c) * ns;
-                if (units >= lo && units <= hi) {
+    const double u1 = (double)tiles_of(1);
+    if (u1 > 4.5 * cus) {
+        cfg = 0;
+    } else if (u1 < 1.75 * cus) {
+        bool found = false;
+        int64_t best = -1;
+        for (int c : {1, 2, 3}) {
+            for (int64_t ns = 1; ns <= 4 && !found; ++ns) {
+                if (!split_ok(ns)) break;
+                const int64_t units = tiles_of(c) * ns;
+                if ((double)units >= 2.75 * cus) found = true;
+                if (found || units > best) {
+                    best = units;
                     cfg = c;
                     nsplit = ns;
                 }
             }
-        }
-    if (cfg < 0) {
-        if ((double)tiles_of(0) > hi) {
-            cfg = 0;
-        } else {
-            int64_t best = -1;
-            for (int64_t ns = 1; ns <= 4; ++ns) {
-                if (ns > 1 && (nk / ns < 8 || !fits(ns))) break;
-                for (int c = 0; c < kQbfNumCfgs; ++c)
-                    if (tiles_of(c) * ns > best) {
-                        best = tiles_of(c) * ns;
-                        cfg = c;
-                        nsplit = ns;
-                    }
-            }
+            if (found || (double)best >= 1.75 * cus) break;
         }
     }
     const int forced_tile = env_int("TML_GEMM_QBF_TILE", 0) - 1;
@@ -391,7 +390,7 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     if (forced >= 1) nsplit = std::min<int64_t>(forced, nk);
     int64_t spl = (nk + nsplit - 1) / nsplit;
     nsplit = (nk + spl - 1) / spl;  // no split without slices
-    if (!fits(nsplit)) {
+    if (nsplit > 1 && (size_t)nsplit * (size_t)m.M * (size_t)m.N > m.ws_cap_floats) {
         nsplit = 1;
         spl = nk;
     }
