@@ -676,11 +676,11 @@ def test_prepared_matrix_core_plans(orc, nw, it, t):
 
 
 def test_prepared_matrix_core_vocabulary(orc):
-    # Q4_0 at M = 1 on a vocabulary-sized N takes the matrix-core kernel by
-    # default (two waves a workgroup, eight or more workgroups a CU); Q8_0
-    # there and Q4_0 on a layer-sized N stay on the VALU kernels.
-    k = 256
-    for n in (33000, 5000):
+    # Q8_0 and Q4_0 at M = 1 on a vocabulary-sized N take the matrix-core
+    # kernel by default (eight or more workgroups a CU; Q8_0 with two rounds
+    # in flight, K = 1280 giving it two rounds); on a layer-sized N they stay
+    # on the VALU kernels.
+    for (k, n) in ((256, 33000), (1280, 33000), (256, 5000)):
         w = rnd(231, k, n, 0.02)
         q, s = orc.quantize_q8(w)
         p, s4 = orc.quantize_q4(w)

@@ -400,11 +400,13 @@ bool gemv_tm_capable(int fmt, int64_t M, int64_t K) {
     return e > 0 && M >= 1 && M <= kPreparedGemvMaxM && K > 0 && K % e == 0 && K < ((int64_t)1 << 30);
 }
 
-// Q4_0 at M = 1 with at least 32768 columns (a vocabulary projection): the
-// int4 decode makes the VALU kernel instruction-bound there (12.71 against
-// 10.61 us at 1280x51866); on the layer shapes it is the faster one.
+// M = 1 with at least 32768 columns (a vocabulary projection): Q4_0's int4
+// decode makes the VALU kernel instruction-bound there (12.71 against 10.61
+// us at 1280x51866), and Q8_0 runs 13.98 against 14.89 us; on the layer
+// shapes the VALU kernel is the faster one.
 bool gemv_tm_m1_preferred(int fmt, int64_t N, int64_t K) {
-    return fmt == TML_FMT_Q4_0 && N >= 32768 && gemv_tm_capable(fmt, 1, K) && env_int("TML_GEMVTM", 1) != 0;
+    return (fmt == TML_FMT_Q4_0 || fmt == TML_FMT_Q8_0) && N >= 32768 && gemv_tm_capable(fmt, 1, K) &&
+           env_int("TML_GEMVTM", 1) != 0;
 }
 
 bool gemv_tm_supported(int fmt, int64_t M, int64_t K) {
@@ -473,13 +475,21 @@ Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, 
                 }
             }
     }
-    // With eight or more workgroups a CU (vocabulary-sized N) two waves of
-    // runs of four: more workgroups resident per CU hide more latency
-    // (Q4_0 1280x51866, M = 1: 10.61 us, against 11.22 with four waves and
-    // 14.57 with ten).
+    // With eight or more workgroups a CU (vocabulary-sized N), Q4_0: two
+    // waves of runs of four, more workgroups resident per CU hiding more
+    // latency (1280x51866, M = 1: 10.61 us, against 11.22 with four waves
+    // and 14.57 with ten); Q8_0: five waves of runs of eight with two rounds
+    // in flight (13.98 us; 14.22 with four waves, 14.59 with one round).
+    bool pf = false;
     if (grid >= 8LL * cus) {
-        it = 1;
-        nw = (int)std::min<int64_t>(2, (ka.nchunk + 3) / 4);
+        if (fmt == TML_FMT_Q8_0) {
+            it = 2;
+            nw = (int)std::min<int64_t>(5, (ka.nchunk + 7) / 8);
+            pf = true;
+        } else {
+            it = 1;
+            nw = (int)std::min<int64_t>(2, (ka.nchunk + 3) / 4);
+        }
     }
     const int forced_nw = env_int("TML_GEMVTM_NW", 0), forced_it = env_int("TML_GEMVTM_IT", 0);
     if (forced_it == 1 || forced_it == 2 || forced_it == 4) it = forced_it;
@@ -490,9 +500,8 @@ Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, 
     if (tm_lds_need(fmt, M, it, nw, tiles) > kTmMaxLds)
         return Status::Err(TML_ERR_INVALID_ARG, "matrix-core GEMV: staging exceeds the LDS");
     ka.nw = nw;
-    // Two rounds in flight: measured no faster on the decoder shapes (Q4_0
-    // vocabulary 10.64 against 10.61 us), so only on request.
-    bool pf = false;
+    // Two rounds in flight elsewhere: measured no faster on the decoder
+    // shapes (Q4_0 vocabulary 10.64 against 10.61 us), so only on request.
     const int forced_pf = env_int("TML_GEMVTM_PF", -1);
     if (forced_pf == 0 || forced_pf == 1) pf = forced_pf == 1;
     switch (fmt) {
