@@ -6,7 +6,7 @@ the reference's dequantize-then-fp32-accumulate result (matmulF32Q8 /
 matmulF32Q4, src/core/quantization.zig:240-311, :829-957; per-column scales
 through oracle.matmul_cols) to ~1e-5.  The bound here is 2e-5, not the 1e-3
 bar of the quantized paths: a dropped lo term costs ~4e-3, a misplaced k,
-column or nibble far more.  The planner takes this kernel from M = 256 on;
+column or nibble far more.  The planner takes this kernel from M = 128 on;
 TML_GEMM_QBF=2 (or a forced tile / split) takes it for every M > 8, which
 these tests use to reach it on small shapes.
 """

@@ -596,7 +596,7 @@ GemmPlan plan_gemm(const MatmulArgs &m) {
     };
     const bool fp32_forced = set("TML_GEMM_DMA_Q") || set("TML_GEMM_TILE") || set("TML_GEMM_DMA_TILE") ||
                              set("TML_GEMM_SPLIT");
-    if (!fp32_forced && gemm_qbf_supported(m) && (m.M >= 256 || env_int("TML_GEMM_QBF", 1) == 2 ||
+    if (!fp32_forced && gemm_qbf_supported(m) && (m.M >= 128 || env_int("TML_GEMM_QBF", 1) == 2 ||
                                                   env_int("TML_GEMM_QBF_TILE", 0) > 0 ||
                                                   env_int("TML_GEMM_QBF_SPLIT", 0) > 0)) {
         p.qbf = true;

@@ -338,17 +338,21 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
 }  // namespace
 
 // Tile and K split: forced by TML_GEMM_QBF_TILE / TML_GEMM_QBF_SPLIT, else
-//   * 64x128 unsplit when its tiles give each CU 1.75 to 4.5 workgroups
-//     (117 registers, LDS for four a CU);
-//   * 128x128 unsplit when 64x128 gives more than 4.5;
-//   * else the tile (64x128, then 64x64, then 32x64) and the fewest K splits
-//     (2..4, at least eight 32-deep slices a split) that reach 2.75 units
-//     (tiles x splits) a CU, or the most units found.
-// Measured on MI355X (Q8_0 / Q4_0, us): 1500x3840x1280 64x128 unsplit
-// 48.1 / 48.9 (128x128: 61); 1500x5120x1280 64x128 unsplit 59.5 / 59.0
-// (128x128: 61.8); 1500x1280x5120 64x128 split 3 61.1 / 62.8 (split 2:
-// 65.7; unsplit 91); 512x4096x1024 64x128 split 3 24.5 (split 2: 24.1).
-// Splits stay within the caller's workspace cap.
+//   * 128x128 unsplit when 64x128 tiles would give each CU more than 4.5;
+//   * else the tile (64x128, 64x64, 32x64) and K split s in 1..4 (at least
+//     eight 32-deep slices a split, within the workspace cap) of least
+//     modelled time
+//       t = ceil(tiles s / CUs) * (slices / s) * c / eff + 5.3 us + 1.7 us * (s - 1),
+//     c = 0.57 / 0.46 / 0.36 us a slice for the three tiles, eff = 1, 1.39,
+//     1.49 for one, two, three or more units a CU (the co-resident
+//     workgroups' overlap), the last term the partials and the reduce
+//     launch.  Fitted to sweeps on MI355X (us, Q8_0; 64x128 at s = 1..4):
+//     128x4096x1024 23.5 / 16.0 / 15.5 / 15.0 (64x64: 19.9 / 15.0, 32x64:
+//     16.7); 128x5120x1280 27.5 / 18.3 / 17.0 / 19.4; 192x4096x1024 23.6 /
+//     17.4 / 19.6 / 19.3; 1500x1280x5120 91 / 65.7 / 61.1 / 61.4;
+//     512x4096x1024 24.9 / 23.8 / 24.2 / 25.2; 512x384x384 32x64 9.0, 64x64
+//     10.9.  (1500x3840x1280 unsplit 48.1 against 61 at 128x128;
+//     1500x5120x1280 59.5 against 61.8.)
 void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) {
@@ -364,25 +368,24 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     };
     int cfg = 1;
     int64_t nsplit = 1;
-    const double u1 = (double)tiles_of(1);
-    if (u1 > 4.5 * cus) {
+    if ((double)tiles_of(1) > 4.5 * cus) {
         cfg = 0;
-    } else if (u1 < 1.75 * cus) {
-        bool found = false;
-        int64_t best = -1;
-        for (int c : {1, 2, 3}) {
-            for (int64_t ns = 1; ns <= 4 && !found; ++ns) {
+    } else {
+        static const double slice_us[] = {0.0, 0.57, 0.46, 0.36};
+        double best = 1e300;
+        for (int c = 1; c <= 3; ++c)
+            for (int64_t ns = 1; ns <= 4; ++ns) {
                 if (!split_ok(ns)) break;
-                const int64_t units = tiles_of(c) * ns;
-                if ((double)units >= 2.75 * cus) found = true;
-                if (found || units > best) {
-                    best = units;
+                const int64_t per_cu = (tiles_of(c) * ns + cus - 1) / cus;
+                const double eff = per_cu >= 3 ? 1.49 : per_cu == 2 ? 1.39 : 1.0;
+                const double t =
+                    (double)per_cu * ((double)nk / (double)ns) * slice_us[c] / eff + 5.3 + 1.7 * (double)(ns - 1);
+                if (t < best) {
+                    best = t;
                     cfg = c;
                     nsplit = ns;
                 }
             }
-            if (found || (double)best >= 1.75 * cus) break;
-        }
     }
     const int forced_tile = env_int("TML_GEMM_QBF_TILE", 0) - 1;
     if (forced_tile >= 0 && forced_tile < kQbfNumCfgs) cfg = forced_tile;
