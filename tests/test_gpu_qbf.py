@@ -57,11 +57,11 @@ def _gemm(fmt, m, n, k, a, b, scale, scales, bias=None):
     return c
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6])
 def test_qbf_tiles_vs_oracle(orc, env, tile):
-    # Every tile config (0: the planner's choice) on shapes ragged in M and N
-    # (partial tiles, N not a multiple of 16), K from one slice to many, with
-    # a bias.
+    # Every tile config (0: the planner's choice; 5, 6 on 64-deep slices) on
+    # shapes ragged in M and N (partial tiles, N not a multiple of 16), K
+    # from one slice to many and not a multiple of 64, with a bias.
     env["TML_GEMM_QBF"] = "2"
     if tile:
         env["TML_GEMM_QBF_TILE"] = str(tile)
@@ -76,11 +76,12 @@ def test_qbf_tiles_vs_oracle(orc, env, tile):
 
 
 @pytest.mark.parametrize("split", [2, 3, 5])
-@pytest.mark.parametrize("tile", [1, 2, 4])
+@pytest.mark.parametrize("tile", [1, 2, 4, 6])
 def test_qbf_split_vs_oracle(orc, env, tile, split):
     # K split over workgroups (each over its own range of 32-deep slices,
-    # the last range short), raw partials summed in split order by the
-    # reduce launch, which runs the epilogue: bias and residual here.
+    # whole 64-deep ones for tile 6, the last range short), raw partials
+    # summed in split order by the reduce launch, which runs the epilogue:
+    # bias and residual here.
     env["TML_GEMM_QBF_TILE"] = str(tile)
     env["TML_GEMM_QBF_SPLIT"] = str(split)
     for (m, n, k) in [(200, 336, 520), (300, 70, 1288)]:

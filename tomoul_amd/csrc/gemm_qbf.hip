@@ -93,11 +93,20 @@ __device__ __forceinline__ void qbf_split(float a, float b, uint32_t &hi, uint32
     lo = qbf_pk(ra == ra ? ra : 0.0f, rb == rb ? rb : 0.0f);
 }
 
-// Physical slot of logical slot s (8 k) in LDS row r.
-__device__ __forceinline__ int qbf_slot(int r, int s) { return r * 4 + (s ^ ((r >> 2) & 3)); }
+// Physical slot of logical slot s (8 k) in LDS row r of SL slots: four
+// slots (64-byte rows) swap by (r / 4) mod 4, eight (128-byte rows) by
+// (r / 2) mod 8, so that 16 consecutive rows read at one logical slot, and
+// the staging writes of consecutive slots, cover the 64 banks evenly.
+template <int SL>
+__device__ __forceinline__ int qbf_slot(int r, int s) {
+    if constexpr (SL == 4) return r * 4 + (s ^ ((r >> 2) & 3));
+    else return r * 8 + (s ^ ((r >> 1) & 7));
+}
 
-template <int FMT, int BM, int BN, int WM, int WN, int D>
+template <int FMT, int BM, int BN, int WM, int WN, int D, int BK = 32>
 __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
+    static_assert(BK == 32 || BK == 64, "32- or 64-deep slices");
+    constexpr int SL = BK / 8;  // 16-byte slots (8 k) of an LDS row
     constexpr int NT = 256;
     constexpr int TM = WM / 16, TN = WN / 16;
     constexpr int WAVES_N = BN / WN;
@@ -105,11 +114,11 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
     static_assert(WM % 16 == 0 && WN % 16 == 0, "whole 16 x 16 MFMA tiles");
     // staging tasks of a slice: A one (row, 8-k slot) each; B one (column
     // pair, 8-k slot) each
-    constexpr int TA = BM * 4, TB = (BN / 2) * 4;
+    constexpr int TA = BM * SL, TB = (BN / 2) * SL;
     constexpr int PA = (TA + NT - 1) / NT, PB = (TB + NT - 1) / NT;
     static_assert(TA % NT == 0 || TA < NT, "A tasks split evenly");
 
-    __shared__ uintx4 Ah[2][BM * 4], Al[2][BM * 4], Bs[2][BN * 4];
+    __shared__ uintx4 Ah[2][BM * SL], Al[2][BM * SL], Bs[2][BN * SL];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -154,7 +163,7 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
 #pragma unroll
         for (int p = 0; p < PA; ++p) {
             const int j = (tid + p * NT) % TA;
-            const int row = j >> 2, k = kbase + k0 + 8 * (j & 3);
+            const int row = j / SL, k = kbase + k0 + 8 * (j % SL);
             const unsigned past_k = (unsigned)(kend - 1 - k) & 0x80000000u;
             const unsigned off = (((unsigned)(m0 + row) * (unsigned)a.K + (unsigned)k) * 4u) | past_k;
             ra[d][p][0] = qbf_load16(a.A, a.a_bytes, off);
@@ -178,15 +187,15 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
         for (int p = 0; p < PA; ++p) {
             const int j = tid + p * NT;
             if (TA % NT == 0 || j < TA) {
-                const int row = j >> 2, s = j & 3;
+                const int row = j / SL, s = j % SL;
                 const floatx4 x0 = __builtin_bit_cast(floatx4, ra[d][p][0]), x1 = __builtin_bit_cast(floatx4, ra[d][p][1]);
                 uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
                 qbf_split(x0[0], x0[1], h0, l0);
                 qbf_split(x0[2], x0[3], h1, l1);
                 qbf_split(x1[0], x1[1], h2, l2);
                 qbf_split(x1[2], x1[3], h3, l3);
-                Ah[st][qbf_slot(row, s)] = (uintx4){h0, h1, h2, h3};
-                Al[st][qbf_slot(row, s)] = (uintx4){l0, l1, l2, l3};
+                Ah[st][qbf_slot<SL>(row, s)] = (uintx4){h0, h1, h2, h3};
+                Al[st][qbf_slot<SL>(row, s)] = (uintx4){l0, l1, l2, l3};
             }
         }
 #pragma unroll
@@ -210,8 +219,8 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
                         o[q] = qbf_pk((float)((int32_t)(w0 << 24) >> 28), (float)((int32_t)(w1 << 24) >> 28));
                     }
                 }
-                Bs[st][qbf_slot(2 * cp, s)] = e;
-                Bs[st][qbf_slot(2 * cp + 1, s)] = o;
+                Bs[st][qbf_slot<SL>(2 * cp, s)] = e;
+                Bs[st][qbf_slot<SL>(2 * cp + 1, s)] = o;
             }
         }
     };
@@ -221,27 +230,33 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
-    // One 32-deep slice: lane (c, g) reads k = 8 g .. 8 g + 7 of A rows
-    // wm0 + 16 i + c (hi and lo) and of B columns wn0 + 16 j + c.  All hi
-    // products first, then the lo ones, so no MFMA waits on the one before.
+    // One slice, 32 k at a time: lane (c, g) reads k = 32 h + 8 g .. + 7 of
+    // A rows wm0 + 16 i + c (hi and lo) and of B columns wn0 + 16 j + c.  All
+    // hi products first, then the lo ones, so no MFMA waits on the one before.
     auto compute = [&](int st) __attribute__((always_inline)) {
-        bf16x8 ah[TM], al[TM], bv[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int slot = qbf_slot(wm0 + 16 * i + c, g);
-            ah[i] = __builtin_bit_cast(bf16x8, Ah[st][slot]);
-            al[i] = __builtin_bit_cast(bf16x8, Al[st][slot]);
+        for (int h = 0; h < SL / 4; ++h) {
+            bf16x8 ah[TM], al[TM], bv[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int slot = qbf_slot<SL>(wm0 + 16 * i + c, 4 * h + g);
+                ah[i] = __builtin_bit_cast(bf16x8, Ah[st][slot]);
+                al[i] = __builtin_bit_cast(bf16x8, Al[st][slot]);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                bv[j] = __builtin_bit_cast(bf16x8, Bs[st][qbf_slot<SL>(wn0 + 16 * j + c, 4 * h + g)]);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bv[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bv[j], acc[i][j], 0, 0, 0);
         }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bv[j] = __builtin_bit_cast(bf16x8, Bs[st][qbf_slot(wn0 + 16 * j + c, g)]);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bv[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bv[j], acc[i][j], 0, 0, 0);
     };
 
     // Register set d holds slice kt with kt % D == d: slices 0 .. D-1 are
@@ -251,9 +266,9 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
     // (D even): steps past K multiply zeros, and every step of the unrolled
     // body is the same straight-line code with its LDS stage fixed.
     static_assert(D % 2 == 0, "LDS stage of step u is u % 2");
-    const int nk = ((kend - kbase + 31) / 32 + D - 1) / D * D;
+    const int nk = ((kend - kbase + BK - 1) / BK + D - 1) / D * D;
 #pragma unroll
-    for (int d = 0; d < D; ++d) load(d, d * 32);
+    for (int d = 0; d < D; ++d) load(d, d * BK);
     store(0, 0);
     __syncthreads();
     for (int kt0 = 0; kt0 < nk; kt0 += D) {
@@ -261,7 +276,7 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
         for (int u = 0; u < D; ++u) {
             // the scheduler keeps the three phases in this order, so the
             // loads of a set are always older than the D - 1 sets after it
-            load(u, (kt0 + u + D) * 32);
+            load(u, (kt0 + u + D) * BK);
             __builtin_amdgcn_sched_barrier(0);
             compute(u & 1);
             __builtin_amdgcn_sched_barrier(0);
@@ -314,15 +329,22 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
 }
 
 struct QbfCfg {
-    int bm, bn;
+    int bm, bn, bk;
 };
-// Tile configs (index = TML_GEMM_QBF_TILE - 1): <BM, BN> with four waves of
-// BM/2 x BN/2.  The two large tiles keep two slices of loads in flight (D =
-// 2: 170 / 117 registers with the accumulators in ordinary VGPRs, two and
-// four workgroups a CU), the small ones four; at the large tiles D = 2
-// measured as fast as or faster than D = 4, which holds one workgroup a CU at
-// 128 x 128.
-constexpr QbfCfg kQbfCfgs[] = {{128, 128}, {64, 128}, {64, 64}, {32, 64}};
+// Tile configs (index = TML_GEMM_QBF_TILE - 1): <BM, BN, BK> with four
+// waves of BM/2 x BN/2.  The two large tiles keep two 32-deep slices of loads
+// in flight (D = 2: 170 / 117 registers with the accumulators in ordinary
+// VGPRs, two and four workgroups a CU), the small ones four; at the large
+// tiles D = 2 measured as fast as or faster than D = 4, which holds one
+// workgroup a CU at 128 x 128.  The last two are the small tiles on 64-deep
+// slices with two in flight (half the steps, so half the barriers and LDS
+// round trips a K range; 116 / 87 registers): 32 x 64 x 64 is the fastest
+// config wherever the tiles are few (M <= 512 at the config shapes), e.g.
+// 128x4096x1024 12.6 against 16.4 us, 128x1280x5120 19.4 against 30.4 us;
+// at M = 1500 it is slower than 64 x 128 x 32 (QKV 61.8 against 47.8 us:
+// 186 registers at 64 x 128 x 64 hold two workgroups a CU, and 32 x 64
+// tiles re-read A and B twice as often).
+constexpr QbfCfg kQbfCfgs[] = {{128, 128, 32}, {64, 128, 32}, {64, 64, 32}, {32, 64, 32}, {64, 64, 64}, {32, 64, 64}};
 constexpr int kQbfNumCfgs = (int)(sizeof(kQbfCfgs) / sizeof(kQbfCfgs[0]));
 
 template <int FMT>
@@ -331,13 +353,23 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
         case 0: gemm_qbf_kernel<FMT, 128, 128, 64, 64, 2><<<grid, 256, 0, s>>>(a); break;
         case 1: gemm_qbf_kernel<FMT, 64, 128, 32, 64, 2><<<grid, 256, 0, s>>>(a); break;
         case 2: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 4><<<grid, 256, 0, s>>>(a); break;
-        default: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 4><<<grid, 256, 0, s>>>(a); break;
+        case 3: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 4><<<grid, 256, 0, s>>>(a); break;
+        case 4: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 2, 64><<<grid, 256, 0, s>>>(a); break;
+        default: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 2, 64><<<grid, 256, 0, s>>>(a); break;
     }
 }
 
 }  // namespace
 
 // Tile and K split: forced by TML_GEMM_QBF_TILE / TML_GEMM_QBF_SPLIT, else
+//   * 32x64x64 up to M = 512 where those tiles number at most four a CU, with the fewest
+//     K splits s in 1..4 that give every CU a unit (tile x split sweep,
+//     us, Q8_0, 32x64x64 at s = 1..4: 128x4096x1024 12.6 / 13.5 / 14.9 /
+//     15.6; 128x5120x1280 17.4 / 16.8 / 18.0 / 19.4; 128x1280x5120 42.7 /
+//     25.1 / 19.9 / 19.4; 192x4096x1024 15.3 / 15.9 / 19.4 / 19.0;
+//     256x4096x1024 16.3 / 16.5 / 19.1 / 19.9; 512x4096x1024 21.7 / 28.0 /
+//     31.6 / 32.8; 256x768x3072 27.4 / 17.6 / 16.7 / 15.1; 384x1280x1280
+//     14.3 / 14.1 / 15.4 / 16.6);
 //   * 128x128 unsplit when 64x128 tiles would give each CU more than 4.5;
 //   * else the tile (64x128, 64x64, 32x64) and K split s in 1..4 (at least
 //     eight 32-deep slices a split, within the workspace cap) of least
@@ -368,7 +400,17 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     };
     int cfg = 1;
     int64_t nsplit = 1;
-    if ((double)tiles_of(1) > 4.5 * cus) {
+    if (m.M <= 512 && tiles_of(5) <= 4LL * cus) {
+        // 32 x 64 x 64 tiles with the fewest K splits that give every CU a
+        // unit (within 2 % of the best of a tile x split sweep on average:
+        // M = 128-512, N = 768-5120, K = 1024-5120; at M = 1500 its A and B
+        // re-reads cost more: 1500x1280x5120 82.9 against 61.3 us)
+        cfg = 5;
+        for (int64_t ns = 1; ns <= 4 && split_ok(ns); ++ns) {
+            nsplit = ns;
+            if (tiles_of(5) * ns >= cus) break;
+        }
+    } else if ((double)tiles_of(1) > 4.5 * cus) {
         cfg = 0;
     } else {
         static const double slice_us[] = {0.0, 0.57, 0.46, 0.36};
@@ -391,7 +433,9 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     if (forced_tile >= 0 && forced_tile < kQbfNumCfgs) cfg = forced_tile;
     const int forced = env_int("TML_GEMM_QBF_SPLIT", 0);
     if (forced >= 1) nsplit = std::min<int64_t>(forced, nk);
-    int64_t spl = (nk + nsplit - 1) / nsplit;
+    // 32-deep slices a split, whole slices of the config's depth
+    const int64_t per = kQbfCfgs[cfg].bk / 32;
+    int64_t spl = ((nk + nsplit - 1) / nsplit + per - 1) / per * per;
     nsplit = (nk + spl - 1) / spl;  // no split without slices
     if (nsplit > 1 && (size_t)nsplit * (size_t)m.M * (size_t)m.N > m.ws_cap_floats) {
         nsplit = 1;
