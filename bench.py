@@ -103,6 +103,8 @@ def parse():
                    help="only the XLM-R layer step (config 2), for kernel traces")
     p.add_argument("--config1-only", action="store_true",
                    help="only config 1 (Whisper-tiny MLP + bias, 20 launches per replay), for kernel traces")
+    p.add_argument("--qgemm-only", action="store_true",
+                   help="only config 3 at M = 128 / 512 (Q8_0, bf16 matrix-core GEMM), for kernel traces")
     p.add_argument("--config5-quant-only", action="store_true",
                    help="only the config-5 sweep with Q8_0 / Q4_0 weights (bf16 matrix-core GEMM), for kernel traces")
     p.add_argument("--profile-gemv", action="store_true",
@@ -187,7 +189,8 @@ def main():
 
     from tomoul_amd import synth
 
-    headline = not (args.config1_only or args.config2_only or args.profile_gemv or args.calibrate_copy)
+    headline = not (args.config1_only or args.config2_only or args.qgemm_only or args.profile_gemv or
+                    args.calibrate_copy)
     if headline:
         t0 = time.perf_counter()
         host_w = encoder_weights(args.layers, args.gen_workers)
@@ -214,6 +217,9 @@ def main():
         return
     if args.config2_only:
         print(json.dumps({"config2": bench_config2(torch, dev, sptr, timer, _abi, synth, args)}), flush=True)
+        return
+    if args.qgemm_only:
+        print(json.dumps({"qgemm": bench_qgemm(torch, dev, sptr, timer, _abi, synth, np)}), flush=True)
         return
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
