@@ -101,7 +101,11 @@ const char *tml_hip_last_error(void);
 /* Writes the device name (e.g. "AMD Instinct MI355X") into buf. */
 int tml_hip_device_name(char *buf, size_t len);
 
-/* ---------------------------------------------------- host-pointer API */
+/* ---------------------------------------------------- host-pointer API
+ * Blocking.  Operands and C pass through the device's pinned staging
+ * buffers (up to 256 MiB a direction; larger ones are sent from the
+ * caller's memory), with host copies on up to seven worker threads the
+ * library starts on first use and joins at process exit. */
 
 /* C = alpha * A.B + beta * C.  Replaces zblas.sgemm(m, n, k, a, b, c, alpha,
  * beta) at src/core/ops.zig:273 and :513, and blas.sgemm -> cblas_sgemm

@@ -146,6 +146,31 @@ inline hipError_t hipFree(void *p) {
     }
     return hipSuccess;
 }
+// Pinned host memory: plain host memory of exactly the asked size.
+constexpr unsigned hipHostMallocDefault = 0;
+inline hipError_t hipHostMalloc(void **p, size_t n, unsigned) {
+    void *q = std::malloc(n ? n : 1);
+    if (q == nullptr) return hipErrorOutOfMemory;
+    *p = q;
+    return hipSuccess;
+}
+inline hipError_t hipHostFree(void *p) {
+    std::free(p);
+    return hipSuccess;
+}
+// Events: work runs when it is issued, so every event has completed.
+typedef struct tml_emu_event *hipEvent_t;
+constexpr unsigned hipEventDisableTiming = 2;
+inline hipError_t hipEventCreateWithFlags(hipEvent_t *e, unsigned) {
+    *e = (hipEvent_t)std::malloc(1);
+    return *e ? hipSuccess : hipErrorOutOfMemory;
+}
+inline hipError_t hipEventRecord(hipEvent_t, hipStream_t = nullptr) { return hipSuccess; }
+inline hipError_t hipEventSynchronize(hipEvent_t) { return hipSuccess; }
+inline hipError_t hipEventDestroy(hipEvent_t e) {
+    std::free(e);
+    return hipSuccess;
+}
 inline hipError_t hipMemset(void *p, int v, size_t n) {
     std::memset(p, v, n);
     return hipSuccess;

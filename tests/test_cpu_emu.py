@@ -127,7 +127,10 @@ def _default_cases():
             cs.append(f"rows {fmt} 13 300 384 b")
     # odd shapes through the generic paths, quantizers, transposing loaders, host API
     cs += ["gemm 0 9 7 5 b", "gemm 2 33 17 9 b", "gemm 3 40 64 32 b", "gemm 4 3 5 7 br", "gemm 0 1 1 1 -",
-           "gemm 1 12 48 3000 b TML_GEMV_SPLIT=7", "host 0 70 96 64 b", "host 1 5 4096 1024 b", "host 18 3 256 96 b"]
+           "gemm 1 12 48 3000 b TML_GEMV_SPLIT=7", "host 0 70 96 64 b", "host 1 5 4096 1024 b", "host 18 3 256 96 b",
+           # pinned staging split over the host copy threads: a 2.8 MB A and an 11 MB weight
+           # (three 4 MiB chunks), a 2.4 MB C, a 4.5 MB C (two chunks)
+           "host 0 1 4 700000 b", "host 0 600 1024 4 b", "host 0 1100 1024 4 b"]
     for fmt in (Q8_0, Q4_0, Q8_K, F16):
         cs += [f"quant {fmt} 0 1 100003 -", f"quant {fmt} 0 33 17 -"]
     for fmt in (Q8_0_PC, Q4_0_PC):
