@@ -94,7 +94,8 @@ OPTIMISED = {"gemm_dma", "gemm_mfma", "emu_main"}
 
 def _deps() -> list[str]:
     return [os.path.join(HERE, "hip", "hip_runtime.h"), os.path.join(CSRC, "tml_internal.hpp"),
-            os.path.join(ROOT, "include", "tomoul_hip.h"), os.path.abspath(__file__)]
+            os.path.join(CSRC, "host_copier.hpp"), os.path.join(ROOT, "include", "tomoul_hip.h"),
+            os.path.abspath(__file__)]
 
 
 def _stale(out: str, inputs: list[str]) -> bool:
