@@ -712,7 +712,9 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
 
 
 def bench_qgemm(torch, dev, sptr, timer, _abi, synth, np):
-    """Config 3 at M in {128, 512}: Q8_0 W[1024x4096] (MFMA path)."""
+    """Config 3 at M in {128, 512}: Q8_0 W[1024x4096] (bf16 matrix-core GEMM).
+    Each launch reads a different copy of the weight, rotating through >= 1 GiB
+    of copies, so neither L2 nor the Infinity Cache holds it between launches."""
     res = {}
     K, N = 1024, 4096
     w = torch.from_numpy(synth.normal_matrix(2002, K, N, 0.02)).to(dev)
@@ -721,17 +723,22 @@ def bench_qgemm(torch, dev, sptr, timer, _abi, synth, np):
     _abi.quantize_dev(_abi.FMT_Q8_0, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
     torch.cuda.synchronize()
     scale = float(sc.item())
+    ncopy = -(-(1 << 30) // (K * N))
+    copies = q.repeat(ncopy).view(ncopy, K * N)
+    ptrs = [copies[i].data_ptr() for i in range(ncopy)]
     for M in (128, 512):
         x = torch.from_numpy(synth.normal_matrix(1001, M, K)).to(dev)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
-        fn = lambda st: _abi.gemm_dev(_abi.FMT_Q8_0, M, N, K, x.data_ptr(), q.data_ptr(),  # noqa: E731
-                                      y.data_ptr(), scale=scale, stream=st)
-        # 20 launches per graph replay, as for the per-shape fp32 figures (a
-        # graph of one launch adds a graph launch to every kernel)
-        ms = timer.time_ms(lambda st, fn=fn: [fn(st) for _ in range(20)], 5, per_replay=20)
+
+        def fn(st, M=M, x=x, y=y):
+            for p in ptrs:
+                _abi.gemm_dev(_abi.FMT_Q8_0, M, N, K, x.data_ptr(), p, y.data_ptr(), scale=scale, stream=st)
+        ms = timer.time_ms(fn, 3, per_replay=ncopy)
         tf = 2.0 * M * N * K / ms / 1e9
         res[f"q8_M{M}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac": qgemm_frac(M, tf), **qgemm_peak(M)}
         log(f"qgemm q8 M={M}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
+    del copies
+    torch.cuda.empty_cache()
     return res
 
 

@@ -362,14 +362,17 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
 }  // namespace
 
 // Tile and K split: forced by TML_GEMM_QBF_TILE / TML_GEMM_QBF_SPLIT, else
-//   * 32x64x64 up to M = 512 where those tiles number at most four a CU, with the fewest
+//   * up to M = 512: 64x64x64 unsplit where those tiles give every CU two,
+//     else 32x64x64 where those tiles number at most four a CU, with the fewest
 //     K splits s in 1..4 that give every CU a unit (tile x split sweep,
 //     us, Q8_0, 32x64x64 at s = 1..4: 128x4096x1024 12.6 / 13.5 / 14.9 /
 //     15.6; 128x5120x1280 17.4 / 16.8 / 18.0 / 19.4; 128x1280x5120 42.7 /
 //     25.1 / 19.9 / 19.4; 192x4096x1024 15.3 / 15.9 / 19.4 / 19.0;
 //     256x4096x1024 16.3 / 16.5 / 19.1 / 19.9; 512x4096x1024 21.7 / 28.0 /
 //     31.6 / 32.8; 256x768x3072 27.4 / 17.6 / 16.7 / 15.1; 384x1280x1280
-//     14.3 / 14.1 / 15.4 / 16.6);
+//     14.3 / 14.1 / 15.4 / 16.6; the same sweep with every launch reading
+//     its own weight copy out of >= 1 GiB, so from HBM: within 1 % of
+//     these, except 512x4096x1024 23.6 against 22.4 us at 64x64x64);
 //   * 128x128 unsplit when 64x128 tiles would give each CU more than 4.5;
 //   * else the tile (64x128, 64x64, 32x64) and K split s in 1..4 (at least
 //     eight 32-deep slices a split, within the workspace cap) of least
@@ -400,7 +403,11 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     };
     int cfg = 1;
     int64_t nsplit = 1;
-    if (m.M <= 512 && tiles_of(5) <= 4LL * cus) {
+    if (m.M <= 512 && tiles_of(4) >= 2LL * cus) {
+        // 64 x 64 x 64 tiles, unsplit, where they give every CU two: half
+        // the A and B re-reads of 32 x 64 (512x4096x1024: 22.4 against 23.6 us)
+        cfg = 4;
+    } else if (m.M <= 512 && tiles_of(5) <= 4LL * cus) {
         // 32 x 64 x 64 tiles with the fewest K splits that give every CU a
         // unit (within 2 % of the best of a tile x split sweep on average:
         // M = 128-512, N = 768-5120, K = 1024-5120; at M = 1500 its A and B
