@@ -122,6 +122,10 @@ def _default_cases():
                         for t in (1, 2):
                             cs.append(f"prep {fmt} {M} 40 2080 b TML_GEMVTM_NW={nw} TML_GEMVTM_IT={it} "
                                       f"TML_GEMVTM_T={t} TML_GEMVTM_PF={(nw + it + t) % 2}")
+            # rows split over two workgroups (grid.y), odd row counts included
+            for M in (5, 7, 8):
+                cs.append(f"prep {fmt} {M} 2050 1280 br TML_GEMVTM_MSPLIT=2")
+                cs.append(f"prep {fmt} {M} 40 2080 bt TML_GEMVTM_MSPLIT=2 TML_GEMVTM_T=2")
         if fmt in (F32, F16, Q8_0, Q4_0):
             cs.append(f"rows {fmt} 3 777 260 b")
             cs.append(f"rows {fmt} 13 300 384 b")

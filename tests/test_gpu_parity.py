@@ -675,6 +675,38 @@ def test_prepared_matrix_core_plans(orc, nw, it, t):
                 os.environ[key] = v
 
 
+@pytest.mark.parametrize("t", [1, 2])
+def test_prepared_matrix_core_row_parts(orc, t):
+    # The matrix-core GEMV with its rows split over two workgroups
+    # (TML_GEMVTM_MSPLIT=2, grid.y): M = 5 / 7 / 8 as parts of 3 + 2, 4 + 3,
+    # 4 + 4 rows, each part staging its own activations and writing its own
+    # rows of C (with beta, bias and alpha), one or two column tiles a
+    # workgroup, several superchunks and ragged N.  Bound 2e-5 as for the
+    # other matrix-core plans.
+    keys = ("TML_GEMVTM", "TML_GEMVTM_MSPLIT", "TML_GEMVTM_T")
+    saved = {key: os.environ.get(key) for key in keys}
+    os.environ.update({"TML_GEMVTM": "2", "TML_GEMVTM_MSPLIT": "2", "TML_GEMVTM_T": str(t)})
+    try:
+        for (k, n) in [(4160, 70), (1280, 600), (5120, 1280)]:
+            w = rnd(271, k, n, 0.02)
+            q, s = orc.quantize_q8(w)
+            p, s4 = orc.quantize_q4(w)
+            bias = synth.normal(273, n, 0.0, 0.02)
+            for m in (5, 7, 8):
+                a, c0 = rnd(274 + m, m, k), rnd(284 + m, m, n)
+                for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
+                                           (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
+                    got = _run_prepared(fmt, b, scale, k, n, m, a, bias=bias, c0=c0, alpha=0.75, beta=0.5)
+                    err = rel_err(got, 0.75 * ref + 0.5 * c0 + bias)
+                    assert err <= 2e-5, (k, n, m, fmt, err)
+    finally:
+        for key, v in saved.items():
+            if v is None:
+                os.environ.pop(key, None)
+            else:
+                os.environ[key] = v
+
+
 def test_prepared_matrix_core_vocabulary(orc):
     # Q8_0 and Q4_0 at M = 1 on a vocabulary-sized N take the matrix-core
     # kernel by default (eight or more workgroups a CU; Q8_0 with two rounds

@@ -63,6 +63,7 @@ struct GemvTmArgs {
     unsigned wbytes;        // N * ldt
     unsigned xbytes;        // M * K * 4
     int nw;                 // waves per workgroup, 1 .. 16
+    int mpart;              // rows of a workgroup: row part blockIdx.y is rows [y mpart, (y + 1) mpart)
 };
 
 __device__ __forceinline__ uintx4 tm_load16(const void *base, unsigned nbytes, unsigned off) {
@@ -170,6 +171,8 @@ __global__ __launch_bounds__(1024) void gemv_tm_kernel(GemvTmArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, g = lane >> 4;  // B: column n0 + 16 tile + c; A: row c
     const int n0 = blockIdx.x * 16 * T;
+    // this workgroup's rows: [row0, row0 + mloc)
+    const int row0 = blockIdx.y * a.mpart, mloc = min(a.mpart, a.M - row0);
     bool col_ok[T];
     unsigned wrow[T];
 #pragma unroll
@@ -207,10 +210,10 @@ __global__ __launch_bounds__(1024) void gemv_tm_kernel(GemvTmArgs a) {
             const int j = lane + 64 * t;
             const int u = j % R, rest = j / R, q = rest % NQ, m = rest / NQ;
             const int ch = base + u;
-            const bool in = j < TOT && ch < a.nchunk && m < a.M;
+            const bool in = j < TOT && ch < a.nchunk && m < mloc;
             const unsigned k = in ? (unsigned)tm_group_k(ch, q, a.nchunk, E) : 0u;
             x[t] = __builtin_bit_cast(floatx4,
-                                      tm_load16(a.A, a.xbytes, in ? 4u * ((unsigned)m * (unsigned)a.K + k) : kOutOfRange));
+                                      tm_load16(a.A, a.xbytes, in ? 4u * ((unsigned)(row0 + m) * (unsigned)a.K + k) : kOutOfRange));
         }
     };
     auto compute_round = [&](const uintx4 (&w)[IT][T], const floatx4 (&x)[TASKS]) __attribute__((always_inline)) {
@@ -313,8 +316,8 @@ __global__ __launch_bounds__(1024) void gemv_tm_kernel(GemvTmArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = 4 * g + r;
-            if (m < MR && m < a.M) {
-                const long long flat = (long long)m * a.N + n;
+            if (m < MR && m < mloc) {
+                const long long flat = (long long)(row0 + m) * a.N + n;
                 float v = colf * v4[r];
                 if (a.beta != 0.0f) v += a.beta * a.C[flat];
                 if (a.bias) v += biasn;
@@ -337,17 +340,17 @@ void launch_tm_pf(const GemvTmArgs &ka, bool pf, unsigned grid, hipStream_t s) {
     // runs of 16 chunks hold too many registers for two rounds in flight
     if constexpr (IT < 4) {
         if (pf) {
-            gemv_tm_kernel<FMT, IT, MR, T, true><<<dim3(grid), block, lds, s>>>(ka);
+            gemv_tm_kernel<FMT, IT, MR, T, true><<<dim3(grid, (unsigned)((ka.M + ka.mpart - 1) / ka.mpart)), block, lds, s>>>(ka);
             return;
         }
     }
-    gemv_tm_kernel<FMT, IT, MR, T, false><<<dim3(grid), block, lds, s>>>(ka);
+    gemv_tm_kernel<FMT, IT, MR, T, false><<<dim3(grid, (unsigned)((ka.M + ka.mpart - 1) / ka.mpart)), block, lds, s>>>(ka);
 }
 
 template <int FMT, int IT, int T>
 void launch_tm_mr(const GemvTmArgs &ka, bool pf, unsigned grid, hipStream_t s) {
-    if (ka.M <= 2) launch_tm_pf<FMT, IT, 2, T>(ka, pf, grid, s);
-    else if (ka.M <= 4) launch_tm_pf<FMT, IT, 4, T>(ka, pf, grid, s);
+    if (ka.mpart <= 2) launch_tm_pf<FMT, IT, 2, T>(ka, pf, grid, s);
+    else if (ka.mpart <= 4) launch_tm_pf<FMT, IT, 4, T>(ka, pf, grid, s);
     else launch_tm_pf<FMT, IT, 8, T>(ka, pf, grid, s);
 }
 
@@ -448,7 +451,27 @@ Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, 
     // for 32 columns instead of twice for 16 (1280x5120 Q4_0, M = 8: 5.48
     // against 5.77 us; at M <= 4 the second tile's registers cost more than
     // the staging saves: 4.57 against 4.01 us at M = 2).
-    int tiles = M > 4 && (N + 15) / 16 > cus ? 2 : 1;
+    // Rows of a workgroup.  Where the column tiles alone give fewer
+    // workgroups than CUs, M >= 4 rows are split into row parts (grid.y),
+    // up to ceil(CUs / workgroups) of them, 2 (3 from M = 7); each part
+    // stages only its rows' activations and streams the same weights (from
+    // L2 after the first).  Measured (us, unsplit -> split, parts): Q4_0
+    // 5120x1280 M = 4 6.67 -> 5.59 (2), M = 8 8.14 -> 6.27 (3; 6.62 with
+    // 2, 7.36 with 4); 1280x5120 M = 8 6.02 -> 5.59 (2); Q8_0 4096x1024
+    // M = 4 7.36 -> 6.37 (2), M = 8 8.16 -> 7.14 (3).  Where every CU
+    // already has a workgroup the weight re-reads cost more: Q8_0
+    // 1024x4096 M = 8 4.67 -> 4.99.  TML_GEMVTM_MSPLIT forces the count.
+    {
+        const int64_t wg0 = M > 4 && (N + 15) / 16 > cus ? (N + 31) / 32 : (N + 15) / 16;
+        int parts = 1;
+        if (M >= 4 && wg0 < cus)
+            parts = (int)std::min<int64_t>((cus + wg0 - 1) / wg0, M >= 7 ? 3 : 2);
+        const int forced_parts = env_int("TML_GEMVTM_MSPLIT", 0);
+        if (forced_parts >= 1 && forced_parts <= 8) parts = forced_parts;
+        ka.mpart = (int)((M + parts - 1) / parts);
+    }
+    const int64_t mp = ka.mpart;
+    int tiles = mp > 4 && (N + 15) / 16 > cus ? 2 : 1;
     const int forced_t = env_int("TML_GEMVTM_T", 0);
     if (forced_t == 1 || forced_t == 2) tiles = forced_t;
     const int64_t grid = (N + 16 * tiles - 1) / (16 * tiles);
@@ -496,8 +519,8 @@ Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, 
     if (forced_nw >= 1 && forced_nw <= 16) nw = forced_nw;
     // at most half the LDS where a CU may get two workgroups
     const size_t lds_cap = forced_nw || grid <= cus ? kTmMaxLds : kTmMaxLds / 2;
-    while (nw > 1 && tm_lds_need(fmt, M, it, nw, tiles) > lds_cap) --nw;
-    if (tm_lds_need(fmt, M, it, nw, tiles) > kTmMaxLds)
+    while (nw > 1 && tm_lds_need(fmt, mp, it, nw, tiles) > lds_cap) --nw;
+    if (tm_lds_need(fmt, mp, it, nw, tiles) > kTmMaxLds)
         return Status::Err(TML_ERR_INVALID_ARG, "matrix-core GEMV: staging exceeds the LDS");
     ka.nw = nw;
     // Two rounds in flight elsewhere: measured no faster on the decoder
