@@ -707,6 +707,55 @@ def test_prepared_matrix_core_row_parts(orc, t):
                 os.environ[key] = v
 
 
+@pytest.mark.parametrize("m", [4, 5, 8])
+def test_prepared_row_parts_bitwise(orc, m):
+    # Splitting the rows over workgroups changes no output's arithmetic
+    # (each output row's MFMA sums and its lo-into-hi add are the same), so
+    # the row-part plans must equal the unsplit ones bit for bit, fused
+    # epilogue included: bias, beta, a residual, GELU (erf) and per-column
+    # scales, at 5120 x 1280 (80 column tiles: the planner splits) and with
+    # 2, 3 and 4 forced parts.
+    import torch
+    k, n = 5120, 1280
+    w = rnd(291, k, n, 0.02)
+    q, s = orc.quantize_q8(w)
+    p, s4 = orc.quantize_q4(w)
+    qc, sc = orc.quantize_q8_cols(w)
+    a, c0, res = rnd(292 + m, m, k), rnd(293, m, n), rnd(294, m, n)
+    bias = synth.normal(295, n, 0.0, 0.02)
+    A, R, Bias = _dev(a), _dev(res), _dev(bias)
+    saved = os.environ.get("TML_GEMVTM_MSPLIT")
+    try:
+        for fmt, b, scale, cols in [(_abi.FMT_Q8_0, q, s, None), (_abi.FMT_Q4_0, p, s4, None),
+                                    (_abi.FMT_Q8_0_PC, qc, 1.0, sc)]:
+            B = _dev(b)
+            S = _dev(cols) if cols is not None else None
+            h = _abi.prepare_ex_dev(fmt, k, n, B.data_ptr(), scale=scale,
+                                    scales_ptr=S.data_ptr() if S is not None else None)
+            try:
+                outs = []
+                for parts in ("1", None, "2", "3", "4"):
+                    if parts is None:
+                        os.environ.pop("TML_GEMVTM_MSPLIT", None)
+                    else:
+                        os.environ["TML_GEMVTM_MSPLIT"] = parts
+                    C = _dev(c0)
+                    _abi.gemm_prepared_ex(h, m, A.data_ptr(), C.data_ptr(), act=_abi.ACT_GELU_ERF,
+                                          residual_ptr=R.data_ptr(), bias_ptr=Bias.data_ptr(), alpha=0.5,
+                                          beta=0.25)
+                    torch.cuda.synchronize()
+                    outs.append(C.cpu().numpy())
+                for o in outs[1:]:
+                    np.testing.assert_array_equal(o, outs[0])
+            finally:
+                _abi.prepared_free(h)
+    finally:
+        if saved is None:
+            os.environ.pop("TML_GEMVTM_MSPLIT", None)
+        else:
+            os.environ["TML_GEMVTM_MSPLIT"] = saved
+
+
 def test_prepared_matrix_core_vocabulary(orc):
     # Q8_0 and Q4_0 at M = 1 on a vocabulary-sized N take the matrix-core
     # kernel by default (eight or more workgroups a CU; Q8_0 with two rounds
