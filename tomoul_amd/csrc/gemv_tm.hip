@@ -453,7 +453,8 @@ Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, 
     // the staging saves: 4.57 against 4.01 us at M = 2).
     // Rows of a workgroup.  Where the column tiles alone give fewer
     // workgroups than CUs, M >= 4 rows are split into row parts (grid.y),
-    // up to ceil(CUs / workgroups) of them, 2 (3 from M = 7); each part
+    // up to ceil(CUs / workgroups) of them, 2 (3 from M = 7), and M = 4
+    // into two parts below twice the CUs; each part
     // stages only its rows' activations and streams the same weights (from
     // L2 after the first).  Measured (us, unsplit -> split, parts): Q4_0
     // 5120x1280 M = 4 6.67 -> 5.59 (2), M = 8 8.14 -> 6.27 (3; 6.62 with
@@ -466,6 +467,8 @@ Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, 
         int parts = 1;
         if (M >= 4 && wg0 < cus)
             parts = (int)std::min<int64_t>((cus + wg0 - 1) / wg0, M >= 7 ? 3 : 2);
+        else if (M == 4 && wg0 < 2LL * cus)
+            parts = 2;  // two parts of two rows: 1280x5120 Q4_0 4.96 -> 4.71 us, 1024x4096 Q8_0 4.39 -> 4.40
         const int forced_parts = env_int("TML_GEMVTM_MSPLIT", 0);
         if (forced_parts >= 1 && forced_parts <= 8) parts = forced_parts;
         ka.mpart = (int)((M + parts - 1) / parts);
