@@ -22,14 +22,17 @@
 // leave the kernel bound by its LDS traffic, not by the matrix cores.
 //
 // Tiles.  A workgroup of four waves owns a BM x BN tile of C (each wave a
-// WM x WN sub-tile of (WM/16) x (WN/16) MFMA tiles) and walks K in 32-deep
-// slices through two LDS stages: the next slice's global loads are issued
-// before the current slice's MFMAs, converted and written after them, one
-// barrier a slice.  LDS holds, per stage, A's hi and lo planes and B as bf16,
-// each as rows of four 16-byte slots (8 k each) -- A by output row, B by
-// output column, both k-contiguous as the MFMA operands want them -- with
-// slot s of row r stored at s ^ ((r / 4) % 4), which keeps the operand reads
-// (16 rows, one slot) and the staging writes free of bank conflicts.
+// WM x WN sub-tile of (WM/16) x (WN/16) MFMA tiles) and walks K in 32- or
+// 64-deep slices (BK) through two LDS stages: the next slice's global loads
+// are issued before the current slice's MFMAs, converted and written after
+// them, one barrier a slice.  LDS holds, per stage, A's hi and lo planes and
+// B as bf16, each as rows of BK / 8 16-byte slots (8 k each) -- A by output
+// row, B by output column, both k-contiguous as the MFMA operands want them
+// -- with slot s of row r stored at s ^ ((r / 4) % 4) for four slots and
+// s ^ ((r / 2) % 8) for eight, which keeps the operand reads (16 rows, one
+// slot) and the staging writes free of bank conflicts.  The 64-deep slices
+// halve the steps (barriers, LDS round trips) over a K range; they pay on
+// the small tiles, where the tiles are few (M <= 512).
 #include "tml_internal.hpp"
 
 #include <algorithm>
