@@ -21,7 +21,9 @@
 // the epilogue as in every other kernel.
 //
 // Work split.  A workgroup of NW waves owns 16 output columns (the MFMA's N)
-// and all of K.  The MFMA's M is the activation row: rows >= M read zeros.
+// and all of K, for all M rows or, where the column tiles leave CUs idle, for
+// one row part (grid.y).  The MFMA's M is the activation row: rows past the
+// part read zeros.
 // The row of column n is a sequence of 16-byte chunks (16 int8 or 32 int4
 // k); chunk ch goes to lane group g = slot % 4 of wave slot / 4, slot =
 // ch % (4 NW).  Lane (c, g) of a wave loads chunk ch of column n0 + c (the
