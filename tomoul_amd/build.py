@@ -21,11 +21,14 @@ SOURCES = ["runtime.hip", "gemm_mfma.hip", "gemm_dma.hip", "gemm_qbf.hip", "gemv
 ARCH = os.environ.get("TML_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops off: hipcc may otherwise emit v_pk_* fp32 instructions
-# on its own from scalar float code.
+# on its own from scalar float code.  Shadowed names are errors: a lambda
+# parameter named like the enclosing function's row offset once computed
+# silently wrong rows (-Wshadow-all is the clang group that covers lambda
+# parameters; plain -Wshadow does not).
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wall", "-Wno-unused-function",
+    "-Wall", "-Wno-unused-function", "-Wshadow-all", "-Werror=shadow-all",
 ]
 
 
