@@ -614,8 +614,13 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
         # The tied vocabulary projection as the reference stores it: the f32
         # token embedding E [n_vocab, d], logits = x . E^T, with E used in
         # place as a rows-prepared weight (no per-step transpose, no copy).
+        # "kn": the reference's own per-step call, ops.matmul of x by the
+        # transposed embedding [K, N] (decoder.zig:936-940), through the
+        # [K,N] GEMV (N = 51866 is not a whole number of lane chunks); the
+        # transpose is the caller's and is not timed.
         e = torch.from_numpy(synth.normal_matrix(seed, N, K, 0.02)).to(dev)
         copies = e.reshape(1, N * K).repeat(ncopy, 1)
+        copies_t = e.t().contiguous().reshape(1, K * N).repeat(ncopy, 1)
         del e
         handles = [_abi.prepare_rows_dev(_abi.FMT_F32, K, N, copies[i].data_ptr(), 4 * K, 1.0, sptr)
                    for i in range(ncopy)]
@@ -630,14 +635,21 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
                 for h in handles:
                     _abi.gemm_prepared(h, M, x.data_ptr(), y.data_ptr(), stream=st)
 
-            ms = timer.time_ms(prep, 3, per_replay=ncopy)
-            gbs = alg / (ms * 1e-3) / 1e9
-            res[f"M{M}"] = {"bytes": alg, "prepared_rows": {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                                                             "frac": round(gbs / HBM_PEAK_GBS, 4)}}
-            log(f"gemv {label} M={M} rows in place: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+            def kn(st):
+                for i in range(ncopy):
+                    _abi.gemm_dev(_abi.FMT_F32, M, N, K, x.data_ptr(), copies_t[i].data_ptr(), y.data_ptr(),
+                                  stream=st)
+
+            res[f"M{M}"] = {"bytes": alg}
+            for name, fn in (("prepared_rows", prep), ("kn", kn)):
+                ms = timer.time_ms(fn, 3, per_replay=ncopy)
+                gbs = alg / (ms * 1e-3) / 1e9
+                res[f"M{M}"][name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                      "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                log(f"gemv {label} M={M} {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
         for h in handles:
             _abi.prepared_free(h)
-        del copies
+        del copies, copies_t
         torch.cuda.empty_cache()
         return res
 

@@ -13,6 +13,9 @@
 //     bytes (and the activations of those rows) back to back, branch-free,
 //     before it does any arithmetic.  The grid holds as many workgroups as
 //     there are (segment, K split) units, typically one to a few per CU.
+//   * Rows need not be a whole number of lane chunks (a 51866-token
+//     vocabulary): a chunk is then read as the aligned dwords that cover it
+//     and funnel-shifted into place (kRagged below).
 //   * Dequantization happens in registers (sign-extending bit-field
 //     extracts); Q8_0 / Q4_0 per-tensor scales are applied once in the
 //     epilogue, Q8_K block scales per chunk.
@@ -57,7 +60,17 @@ struct GemvKArgs {
     int act;             // TML_ACT_* after the bias
     const float *res;    // [M,N] residual added after the bias, or nullptr
     long long tail0;     // tml_act_tail0(M * N)
+    unsigned bbytes;     // byte count of B (kRagged: the buffer resource's range)
 };
+
+// How the kernel reads B:
+//   kGeneric  element by element, each checked (any N, block, alignment);
+//   kAligned  one LW-byte load per chunk (N % E == 0, B LW-byte aligned);
+//   kRagged   any N, B 4-byte aligned and under 2 GiB: a chunk starts at
+//             any element, so it is assembled from the LW / 4 + 1 aligned
+//             dwords that cover it, read through a buffer resource, and
+//             funnel-shifted into place.
+enum { kGeneric = 0, kAligned = 1, kRagged = 2 };
 
 // Elements of B held in LW bytes.
 template <int FMT, int LW> struct Elems;
@@ -67,7 +80,9 @@ template <int LW> struct Elems<TML_FMT_Q8_K, LW> { static constexpr int value = 
 template <int LW> struct Elems<TML_FMT_Q4_0, LW> { static constexpr int value = 2 * LW; };
 template <int LW> struct Elems<TML_FMT_F16, LW> { static constexpr int value = LW / 2; };
 
-template <int LW> struct Raw { uint32_t w[LW / 4]; float s; };
+// One chunk as loaded: LW / 4 words (kRagged: one more, and the bit shift
+// that aligns the chunk, applied when it is used).
+template <int LW> struct Raw { uint32_t w[LW / 4 + 1]; float s; unsigned sh; };
 
 // Sign-extending field extracts (compile to v_bfe_i32).
 __device__ __forceinline__ float sext8(uint32_t word, int byte) {
@@ -110,6 +125,64 @@ __device__ __forceinline__ void load_chunk(const GemvKArgs &a, bool in, int k, i
         r.w[0] = *(const uint32_t *)p;
     }
     if constexpr (FMT == TML_FMT_Q8_K) r.s = *(in ? a.scales + e / a.block : (const float *)a.zero);
+}
+
+template <int FMT> constexpr int kElemBits = FMT == TML_FMT_F32 ? 32 : FMT == TML_FMT_F16 ? 16 : FMT == TML_FMT_Q4_0 ? 4 : 8;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t b_rsrc(const GemvKArgs &a) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.B), (short)0, (int)a.bbytes, 0x00020000);
+}
+
+// kRagged: the LW bytes of row k at column n, wherever they start.  Element
+// e = k*N + n begins at bit b = e * bits of B; the dwords from b / 32 on are
+// read (each range-checked on its own: dwords past B read zero, so an
+// invalid chunk points at bbytes rounded up); shift_chunk, called once the
+// loads are needed, shifts them right by b % 32.
+// A chunk running past the end of its row picks up the next row's first
+// elements; they only ever reach columns >= N, whose sums are dropped, and
+// past the end of B (elements e >= K*N, columns >= N of the last row) it
+// reads zeros.
+template <int FMT, int LW>
+__device__ __forceinline__ void load_chunk_ragged(const GemvKArgs &a, bool in, int k, int n, Raw<LW> &r) {
+    constexpr int ND = LW / 4;
+    constexpr int NL = FMT == TML_FMT_F32 ? ND : ND + 1;  // f32 chunks start on a dword
+    static_assert(FMT != TML_FMT_F32 || LW == 16, "f32 chunks are 16 bytes");
+    const unsigned long long bit = ((unsigned long long)k * (unsigned)a.N + (unsigned)n) * kElemBits<FMT>;
+    const unsigned far = (a.bbytes + 3u) & ~3u;
+    const unsigned off = in ? (unsigned)(bit >> 5) << 2 : far;
+    const __amdgpu_buffer_rsrc_t rs = b_rsrc(a);
+    if constexpr (LW == 16) {
+        const uintx4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3];
+    } else {
+        const uintx2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+        r.w[0] = v[0]; r.w[1] = v[1];
+    }
+    if constexpr (NL > 2 && NL > ND) r.w[ND] = __builtin_amdgcn_raw_buffer_load_b32(rs, off + 4u * ND, 0, 0);
+    if constexpr (FMT != TML_FMT_F32) {
+        // B ending inside a dword: that dword is out of range as a whole
+        // (it reads zero), but its first bytes are the last elements of B,
+        // so the lanes whose chunk covers it rebuild it from byte loads.
+        const unsigned tail = a.bbytes & 3u, full = a.bbytes & ~3u;
+        if (tail != 0u && full - off < 4u * NL) {
+            uint32_t v = 0;
+            for (unsigned i = 0; i < tail; ++i)
+                v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, full + i, 0, 0) << (8 * i);
+#pragma unroll
+            for (int i = 0; i < NL; ++i)
+                if (off + 4u * i == full) r.w[i] = v;
+        }
+    }
+    r.sh = (unsigned)bit & 31u;
+}
+
+template <int FMT, int LW>
+__device__ __forceinline__ void shift_chunk(Raw<LW> &r) {
+    if constexpr (FMT != TML_FMT_F32) {
+#pragma unroll
+        for (int i = 0; i < LW / 4; ++i)
+            r.w[i] = (uint32_t)((((unsigned long long)r.w[i + 1] << 32) | r.w[i]) >> r.sh);
+    }
 }
 
 template <int FMT, int LW>
@@ -158,7 +231,7 @@ __device__ __forceinline__ void load_elems(const GemvKArgs &a, bool row_ok, int 
 
 constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
 
-template <int FMT, int MR, int LW, int LPR, int U, bool VEC>
+template <int FMT, int MR, int LW, int LPR, int U, int MODE>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
     constexpr int E = Elems<FMT, LW>::value;
     constexpr int RW = 64 / LPR;          // row lanes per wave (rows per load instruction)
@@ -206,7 +279,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
         for (int u = 0; u < U; ++u) {
             const int k = kbeg + bt * RB + lrow + u;
             const bool valid = k < kend;
-            if constexpr (VEC) load_chunk<FMT, LW>(a, valid && col_in, valid ? k : 0, col_in ? n : 0, w[u]);
+            if constexpr (MODE == kAligned) load_chunk<FMT, LW>(a, valid && col_in, valid ? k : 0, col_in ? n : 0, w[u]);
+            else if constexpr (MODE == kRagged) load_chunk_ragged<FMT, LW>(a, valid && col_in, k, n, w[u]);
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 const bool ok = valid && m < a.M;
@@ -218,7 +292,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float wv[E];
-            if constexpr (VEC) {
+            if constexpr (MODE == kRagged) {
+                Raw<LW> c = w[u];
+                shift_chunk<FMT, LW>(c);
+                decode_chunk<FMT, LW>(c, wv);
+            } else if constexpr (MODE == kAligned) {
                 decode_chunk<FMT, LW>(w[u], wv);
             } else {
                 const int k = kbeg + bt * RB + lrow + u;
@@ -354,7 +432,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvKArgs a) {
 struct GemvPlan {
     int mr, lw, e, lpr, u, sc, rb;
     int nseg, nsplit, nb;
-    bool vec;
+    int mode;         // kGeneric / kAligned / kRagged
+    unsigned bbytes;  // kRagged: byte count of B
 };
 
 constexpr int kU = 4;         // loads per lane per batch
@@ -400,11 +479,20 @@ GemvPlan make_plan(const MatmulArgs &m) {
     p.lw = pick_lw(m.fmt, p.mr);
     p.e = elems_per_lane(m.fmt, p.lw);
     p.u = kU;
-    p.vec = (m.N % p.e == 0) && is_aligned(m.B, (size_t)p.lw);
-    if (m.fmt == TML_FMT_Q8_K) p.vec = p.vec && (m.block % p.e == 0) && (m.N % m.block == 0);
     const int64_t bpe_num = m.fmt == TML_FMT_F32 ? 4 : (m.fmt == TML_FMT_F16 ? 2 : 1),
                   bpe_den = m.fmt == TML_FMT_Q4_0 ? 2 : 1;
     const int64_t rowbytes = (m.N * bpe_num + bpe_den - 1) / bpe_den;
+    bool aligned = (m.N % p.e == 0) && is_aligned(m.B, (size_t)p.lw);
+    if (m.fmt == TML_FMT_Q8_K) aligned = aligned && (m.block % p.e == 0) && (m.N % m.block == 0);
+    // Ragged rows (N not a whole number of chunks, e.g. a 51866-token
+    // vocabulary): Q8_0 1280x51866 M = 1 94.5 us on the element-wise path
+    // against 17.8 us for the chunked one at N = 51840, f32 80.5 against
+    // 52.5 us.  The buffer resource's 32-bit range bounds B at 2 GiB.
+    const int64_t bbytes = (m.K * m.N * bpe_num + bpe_den - 1) / bpe_den;
+    const bool ragged_ok = m.fmt != TML_FMT_Q8_K && is_aligned(m.B, 4) && bbytes <= ((int64_t)1 << 31) - 64 &&
+                           env_int("TML_GEMV_RAGGED", 1) != 0;
+    p.mode = aligned ? kAligned : ragged_ok ? kRagged : kGeneric;
+    p.bbytes = (unsigned)(ragged_ok ? bbytes : 0);
     // Segment width per row: 128 bytes (one line) for f32, 64 bytes for
     // quantized B at M <= 2 and 32 bytes at M > 2 -- measured best on MI355X
     // at the decoder shapes (narrower segments scatter the loads over more
@@ -414,10 +502,20 @@ GemvPlan make_plan(const MatmulArgs &m) {
     // lane) takes 16 bytes, four lanes per row like the other quantized
     // plans at M > 2: 5120x1280 M = 8 14.4 -> 11.3 us, 1280x5120 10.39 ->
     // 10.22 us (a sweep of every segment width and batches per split).
-    const int seg_bytes = (m.fmt == TML_FMT_F32 || m.fmt == TML_FMT_F16) ? 128
-                        : p.mr <= 2                                  ? 64
-                        : (m.fmt == TML_FMT_Q4_0 && p.mr > 4)        ? 16
-                                                                     : 32;
+    int seg_bytes = (m.fmt == TML_FMT_F32 || m.fmt == TML_FMT_F16) ? 128
+                  : p.mr <= 2                                  ? 64
+                  : (m.fmt == TML_FMT_Q4_0 && p.mr > 4)        ? 16
+                                                               : 32;
+    // Weights streaming 16 MiB or more (vocabulary projections) take wider
+    // segments.  At 1280 x 51866: Q8_0 / Q4_0 at M = 1 22.7 / 21.6 us ->
+    // 19.4 / 15.8 us with 256 bytes a row, at M = 2 24.9 / 27.5 -> 22.1 /
+    // 19.3 us; f32 at M = 1 / 4 54.0 / 61.1 us -> 50.3 / 55.1 us with 1 KiB.
+    // Quantized at M = 4 the narrow segments stay best (32.3 against
+    // 33.8 us).  Layer-sized weights (3-5 MB) keep the narrow ones.
+    if (bbytes >= ((int64_t)16 << 20)) {
+        if ((m.fmt == TML_FMT_Q8_0 || m.fmt == TML_FMT_Q4_0) && p.mr <= 2) seg_bytes = 256;
+        else if (m.fmt == TML_FMT_F32 && p.mr <= 4) seg_bytes = 1024;
+    }
     int lpr = seg_bytes / p.lw;
     if (lpr < 4) lpr = 4;
     if (rowbytes < seg_bytes) {
@@ -427,7 +525,7 @@ GemvPlan make_plan(const MatmulArgs &m) {
     const int forced_lpr = env_int("TML_GEMV_LPR", 0);
     if (forced_lpr == 4 || forced_lpr == 8 || forced_lpr == 16 || forced_lpr == 32 || forced_lpr == 64)
         lpr = forced_lpr;
-    if (!p.vec) lpr = 16;  // the generic path is instantiated for one shape
+    if (p.mode == kGeneric) lpr = 16;  // the generic path is instantiated for one shape
     p.lpr = lpr;
     p.sc = lpr * p.e;
     p.rb = kWaves * (64 / lpr) * p.u;
@@ -455,24 +553,35 @@ GemvPlan make_plan(const MatmulArgs &m) {
     return p;
 }
 
-template <int FMT, int MR, int LW, int LPR, bool VEC>
+template <int FMT, int MR, int LW, int LPR, int MODE>
 void launch_one(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
-    gemv_kernel<FMT, MR, LW, LPR, kU, VEC><<<dim3((unsigned)(p.nseg * p.nsplit)), dim3(kThreads), 0, s>>>(ka);
+    gemv_kernel<FMT, MR, LW, LPR, kU, MODE><<<dim3((unsigned)(p.nseg * p.nsplit)), dim3(kThreads), 0, s>>>(ka);
+}
+
+template <int FMT, int MR, int LW, int MODE>
+void launch_mode(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
+    switch (p.lpr) {
+        case 4: launch_one<FMT, MR, LW, 4, MODE>(ka, p, s); break;
+        case 8: launch_one<FMT, MR, LW, 8, MODE>(ka, p, s); break;
+        case 16: launch_one<FMT, MR, LW, 16, MODE>(ka, p, s); break;
+        case 32: launch_one<FMT, MR, LW, 32, MODE>(ka, p, s); break;
+        default: launch_one<FMT, MR, LW, 64, MODE>(ka, p, s); break;
+    }
 }
 
 template <int FMT, int MR, int LW>
 void launch_lpr(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
-    if (!p.vec) {
-        launch_one<FMT, MR, LW, 16, false>(ka, p, s);
+    if (p.mode == kGeneric) {
+        launch_one<FMT, MR, LW, 16, kGeneric>(ka, p, s);
         return;
     }
-    switch (p.lpr) {
-        case 4: launch_one<FMT, MR, LW, 4, true>(ka, p, s); break;
-        case 8: launch_one<FMT, MR, LW, 8, true>(ka, p, s); break;
-        case 16: launch_one<FMT, MR, LW, 16, true>(ka, p, s); break;
-        case 32: launch_one<FMT, MR, LW, 32, true>(ka, p, s); break;
-        default: launch_one<FMT, MR, LW, 64, true>(ka, p, s); break;
+    if constexpr (FMT != TML_FMT_Q8_K) {
+        if (p.mode == kRagged) {
+            launch_mode<FMT, MR, LW, kRagged>(ka, p, s);
+            return;
+        }
     }
+    launch_mode<FMT, MR, LW, kAligned>(ka, p, s);
 }
 
 template <int FMT, int MR>
@@ -524,6 +633,7 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     ka.nseg = p.nseg; ka.nsplit = p.nsplit; ka.nb = p.nb;
     ka.ws = ws.partials; ka.counters = ws.counters;
     ka.zero = m.zero;
+    ka.bbytes = p.bbytes;
     ka.act = m.act; ka.res = m.res; ka.colscale = m.colscale; ka.tail0 = tml_act_tail0((long long)m.M * m.N);
     switch (m.fmt) {
         case TML_FMT_F32: return launch_fmt<TML_FMT_F32>(ka, p, s);
