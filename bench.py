@@ -821,7 +821,10 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
     1280x5120 and 5120x1280 at M = 1, 4 and 8, each on its prepared copy and
     in the [K,N] layout, `launches` times over 16 distinct weight copies
     (eager launches, one kernel per call); then the Q8_0 and Q4_0 vocabulary
-    projections (1280 x 51866, M = 1) on 3 / 4 prepared copies."""
+    projections (1280 x 51866, M = 1) on 3 / 4 prepared copies and on the
+    same copies in the [K,N] layout, and the f32 one on the token embedding
+    used in place (rows-prepared) and on its transpose in the [K,N] layout
+    (the reference's own per-step call), 3 copies each."""
     for fmt, K, N, M in ((_abi.FMT_Q8_0, 1024, 4096, 1), (_abi.FMT_Q8_0, 1024, 4096, 4),
                          (_abi.FMT_Q8_0, 1024, 4096, 8),
                          (_abi.FMT_Q4_0, 1280, 5120, 1), (_abi.FMT_Q4_0, 1280, 5120, 4),
@@ -864,28 +867,34 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
         y = torch.empty((1, N), dtype=torch.float32, device=dev)
         for i in range(launches):
             _abi.gemm_prepared(hs[i % ncopy], 1, x.data_ptr(), y.data_ptr(), stream=sptr)
+        for i in range(launches):
+            _abi.gemm_dev(fmt, 1, N, K, x.data_ptr(), copies[i % ncopy].data_ptr(), y.data_ptr(),
+                          scale=float(sc.item()), stream=sptr)
         torch.cuda.synchronize()
         for h_ in hs:
             _abi.prepared_free(h_)
         del copies
         torch.cuda.empty_cache()
-        log(f"profile-gemv: fmt {fmt} vocab {K}x{N}: {launches} prepared launches")
+        log(f"profile-gemv: fmt {fmt} vocab {K}x{N}: {launches} prepared + {launches} [K,N] launches")
     # the f32 token embedding [51866 x 1280] used in place (rows-prepared), M = 1
     K, N, ncopy = 1280, 51866, 3
     e = torch.from_numpy(synth.normal_matrix(2004, N, K, 0.02)).to(dev)
     copies = e.reshape(1, N * K).repeat(ncopy, 1)
+    copies_t = e.t().contiguous().reshape(1, K * N).repeat(ncopy, 1)
     del e
     hs = [_abi.prepare_rows_dev(_abi.FMT_F32, K, N, copies[i].data_ptr(), 4 * K, 1.0, sptr) for i in range(ncopy)]
     x = torch.from_numpy(synth.normal_matrix(1001, 1, K)).to(dev)
     y = torch.empty((1, N), dtype=torch.float32, device=dev)
     for i in range(launches):
         _abi.gemm_prepared(hs[i % ncopy], 1, x.data_ptr(), y.data_ptr(), stream=sptr)
+    for i in range(launches):
+        _abi.gemm_dev(_abi.FMT_F32, 1, N, K, x.data_ptr(), copies_t[i % ncopy].data_ptr(), y.data_ptr(), stream=sptr)
     torch.cuda.synchronize()
     for h_ in hs:
         _abi.prepared_free(h_)
-    del copies
+    del copies, copies_t
     torch.cuda.empty_cache()
-    log(f"profile-gemv: f32 embedding rows {N}x{K} in place: {launches} launches")
+    log(f"profile-gemv: f32 embedding {N}x{K}: {launches} launches in place + {launches} on its transpose")
     print(json.dumps({"profile_gemv": True}), flush=True)
 
 
