@@ -454,7 +454,7 @@ def gemv_env():
             os.environ[k] = v
 
 
-@pytest.mark.parametrize("lpr", [4, 8, 16, 32, 64])
+@pytest.mark.parametrize("lpr", [1, 2, 4, 8, 16, 32, 64])
 @pytest.mark.parametrize("nb", [1, 3])
 def test_gemv_segments_and_splits(orc, gemv_env, lpr, nb):
     # Every segment width (lanes per row) and batches-per-split setting of
@@ -482,6 +482,21 @@ def test_gemv_segments_and_splits(orc, gemv_env, lpr, nb):
             _abi.gemm(fmt, m, n, k, a, np.ascontiguousarray(b), got, scale=scale, scales=scales, bias=bias)
             err = rel_err(got, ref + bias)
             assert err <= tol, (fmt, m, err)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_q8_kn_one_lane_a_row(orc, m):
+    # Config 3's Q8_0 1024x4096 in the [K,N] layout at M <= 4: the planner's
+    # one-lane-a-row plan (256 segments of 16 columns, all of K in one
+    # batch, no K split), with a bias
+    k, n = 1024, 4096
+    w = rnd(141, k, n, 0.02)
+    q, s = orc.quantize_q8(w)
+    bias = synth.normal(142, n, 0.0, 0.02)
+    a = rnd(143 + m, m, k)
+    got = np.zeros((m, n), np.float32)
+    _abi.gemm(_abi.FMT_Q8_0, m, n, k, a, q.reshape(k, n), got, scale=s, bias=bias)
+    assert rel_err(got, orc.matmul_q8(a, q, s) + bias) <= Q_TOL
 
 
 @pytest.mark.parametrize("m", [1, 4, 8])

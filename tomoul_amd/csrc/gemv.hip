@@ -522,9 +522,18 @@ GemvPlan make_plan(const MatmulArgs &m) {
         lpr = 4;
         while (lpr < 64 && (int64_t)lpr * p.lw < rowbytes) lpr *= 2;
     }
+    // One lane a row (16 int8 columns a lane) for Q8_0 at M <= 4 when that
+    // still gives every CU a segment and K fits one batch: no K split, so no
+    // partial-sum exchange.  1024x4096 at M = 1 / 2 / 4: 6.25 / 6.83 / 7.75
+    // -> 5.46 / 6.05 / 7.21 us.  Slower at M = 8 (8.3 -> 10.5 us) and for
+    // Q4_0 and f32 at their layer shapes.
+    if (m.fmt == TML_FMT_Q8_0 && aligned && p.mr <= 4 && m.K <= (int64_t)kWaves * 64 * kU &&
+        m.N / p.e >= gemv_cus())
+        lpr = 1;
     const int forced_lpr = env_int("TML_GEMV_LPR", 0);
     if (forced_lpr == 4 || forced_lpr == 8 || forced_lpr == 16 || forced_lpr == 32 || forced_lpr == 64)
         lpr = forced_lpr;
+    if ((forced_lpr == 1 || forced_lpr == 2) && aligned) lpr = forced_lpr;  // one or two lanes a row
     if (p.mode == kGeneric) lpr = 16;  // the generic path is instantiated for one shape
     p.lpr = lpr;
     p.sc = lpr * p.e;
@@ -560,6 +569,10 @@ void launch_one(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
 
 template <int FMT, int MR, int LW, int MODE>
 void launch_mode(const GemvKArgs &ka, const GemvPlan &p, hipStream_t s) {
+    if constexpr (MODE == kAligned) {
+        if (p.lpr == 1) return launch_one<FMT, MR, LW, 1, MODE>(ka, p, s);
+        if (p.lpr == 2) return launch_one<FMT, MR, LW, 2, MODE>(ka, p, s);
+    }
     switch (p.lpr) {
         case 4: launch_one<FMT, MR, LW, 4, MODE>(ka, p, s); break;
         case 8: launch_one<FMT, MR, LW, 8, MODE>(ka, p, s); break;
