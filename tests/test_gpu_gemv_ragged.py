@@ -12,6 +12,8 @@ per-step transpose of the token embedding, [1280, 51866]
 * A non-finite weight at the start of every row.  A chunk that runs past the
   end of its row picks it up, and it must reach only the dropped columns.
 * B not 4-byte aligned takes the element-wise path, with the same result.
+* Per-output-column scales (the Q8_0_PC / Q4_0_PC extension) on ragged rows,
+  through the residual and GELU epilogues.
 Tolerances are the north star's (1e-4 fp32 / F16 weights, 1e-3 quantized).
 """
 import os
@@ -135,3 +137,24 @@ def test_unaligned_weight_pointer(orc, fmt, offset):
         _abi.gemm_dev(fmt, m, n, k, x.data_ptr(), buf.data_ptr() + offset, y.data_ptr(), scale=scale)
         torch.cuda.synchronize()
         assert rel_err(y.cpu().numpy(), ref(a)) <= tol, (fmt, offset, m)
+
+
+@pytest.mark.parametrize("fmt", [_abi.FMT_Q8_0_PC, _abi.FMT_Q4_0_PC])
+def test_ragged_per_column_scales(orc, fmt):
+    # Per-output-column scales (Q8_0 / Q4_0 bytes, one scale a column) on
+    # ragged rows, with a bias and a residual, and with the exact GELU after
+    # the bias.
+    k, n = 517, 333
+    w = rnd(941, k, n, 0.02)
+    q, s = (orc.quantize_q8_cols if fmt == _abi.FMT_Q8_0_PC else orc.quantize_q4_cols)(w)
+    bias = synth.normal(942, n, 0.0, 0.02)
+    for m in (1, 2, 3, 5, 8):
+        a = rnd(943 + m, m, k)
+        ref = orc.matmul_cols(a, fmt, q, s, k, n) + bias
+        res = rnd(950 + m, m, n)
+        c = np.zeros((m, n), np.float32)
+        _abi.gemm_residual(fmt, m, n, k, a, np.ascontiguousarray(q), res, c, scales=s, bias=bias)
+        assert rel_err(c, ref + res) <= Q_TOL, (fmt, m)
+        c = np.zeros((m, n), np.float32)
+        _abi.gemm_act(fmt, m, n, k, a, np.ascontiguousarray(q), c, act=_abi.ACT_GELU_ERF, scales=s, bias=bias)
+        assert rel_err(c, orc.apply_act(ref, _abi.ACT_GELU_ERF)) <= Q_TOL, (fmt, m)
