@@ -485,9 +485,9 @@ GemvPlan make_plan(const MatmulArgs &m) {
     bool aligned = (m.N % p.e == 0) && is_aligned(m.B, (size_t)p.lw);
     if (m.fmt == TML_FMT_Q8_K) aligned = aligned && (m.block % p.e == 0) && (m.N % m.block == 0);
     // Ragged rows (N not a whole number of chunks, e.g. a 51866-token
-    // vocabulary): Q8_0 1280x51866 M = 1 94.5 us on the element-wise path
-    // against 17.8 us for the chunked one at N = 51840, f32 80.5 against
-    // 52.5 us.  The buffer resource's 32-bit range bounds B at 2 GiB.
+    // vocabulary): Q8_0 / Q4_0 / f32 1280x51866 M = 1 94.4 / 77.0 / 80.2 us
+    // on the element-wise path, 19.4 / 15.8 / 50.3 us on the ragged-row
+    // loads.  The buffer resource's 32-bit range bounds B at 2 GiB.
     const int64_t bbytes = (m.K * m.N * bpe_num + bpe_den - 1) / bpe_den;
     const bool ragged_ok = m.fmt != TML_FMT_Q8_K && is_aligned(m.B, 4) && bbytes <= ((int64_t)1 << 31) - 64 &&
                            env_int("TML_GEMV_RAGGED", 1) != 0;
