@@ -510,11 +510,12 @@ GemvPlan make_plan(const MatmulArgs &m) {
     // segments.  At 1280 x 51866: Q8_0 / Q4_0 at M = 1 22.7 / 21.6 us ->
     // 19.4 / 15.8 us with 256 bytes a row, at M = 2 24.9 / 27.5 -> 22.1 /
     // 19.3 us; f32 at M = 1 / 4 54.0 / 61.1 us -> 50.3 / 55.1 us with 1 KiB.
-    // Quantized at M = 4 the narrow segments stay best (32.3 against
-    // 33.8 us).  Layer-sized weights (3-5 MB) keep the narrow ones.
+    // F16 at M = 1 32.4 -> 31.3 us with 1 KiB.  Quantized at M = 4 the
+    // narrow segments stay best (32.3 against 33.8 us), and so do F16 at
+    // M = 4 (39.7 against 51.4 us) and layer-sized weights (3-5 MB).
     if (bbytes >= ((int64_t)16 << 20)) {
         if ((m.fmt == TML_FMT_Q8_0 || m.fmt == TML_FMT_Q4_0) && p.mr <= 2) seg_bytes = 256;
-        else if (m.fmt == TML_FMT_F32 && p.mr <= 4) seg_bytes = 1024;
+        else if ((m.fmt == TML_FMT_F32 && p.mr <= 4) || (m.fmt == TML_FMT_F16 && p.mr == 1)) seg_bytes = 1024;
     }
     int lpr = seg_bytes / p.lw;
     if (lpr < 4) lpr = 4;
