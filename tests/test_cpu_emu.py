@@ -140,6 +140,11 @@ def _default_cases():
     cs += ["gemm 0 1 51866 161 br", "gemm 0 4 51866 161 b", "gemm 1 1 51866 700 br", "gemm 2 2 51866 1299 bB"]
     # Q8_0 at M <= 4 with a segment per CU: one lane a row, K in one batch
     cs += ["gemm 1 1 4096 1024 br", "gemm 1 3 4096 1000 bB", "gemm 1 4 8192 1024 bt"]
+    # one and two lanes a row forced, every format (the aligned path)
+    for fmt in (F32, F16, Q8_0, Q4_0, Q8_K):
+        for M in (1, 5, 8):
+            for lpr in (1, 2):
+                cs.append(f"gemm {fmt} {M} 640 {1024 if fmt == Q8_K else 333} bB TML_GEMV_LPR={lpr} TML_GEMV_NB=1")
     # odd shapes through the generic paths, quantizers, transposing loaders, host API
     cs += ["gemm 0 9 7 5 b", "gemm 2 33 17 9 b", "gemm 3 40 64 32 b", "gemm 4 3 5 7 br", "gemm 0 1 1 1 -",
            "gemm 1 12 48 3000 b TML_GEMV_SPLIT=7", "host 0 70 96 64 b", "host 1 5 4096 1024 b", "host 18 3 256 96 b",
