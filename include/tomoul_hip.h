@@ -211,6 +211,9 @@ int tml_hip_weight_release(const void *host);
  * bias      device pointer to N floats, or NULL.
  * stream    hipStream_t to launch on (NULL = the null stream).
  * All pointers are device pointers.  Asynchronous: returns after the launch.
+ * B may have any alignment.  At M <= 8 the GEMV reads B in 4- to 16-byte
+ * chunks when B is 4-byte aligned (also when N is not a whole number of
+ * chunks), and element by element otherwise, which is several times slower.
  *
  * Workspace and HIP graphs: a problem whose plan splits K uses the device's
  * split-K workspace, which the library grows (hipMalloc) the first time a
