@@ -76,7 +76,7 @@ def test_ragged_bitwise_vs_elementwise(orc, env, fmt, nb):
         for m in (1, 2, 3, 5, 8):
             a = rnd(903 + m, m, k)
             outs = []
-            for ragged in ("1", "0"):
+            for ragged in ("2", "0"):  # 2: the call fails unless it takes the ragged-row loads
                 env["TML_GEMV_RAGGED"] = ragged
                 c = np.zeros((m, n), np.float32)
                 _abi.gemm(fmt, m, n, k, a, np.ascontiguousarray(b), c, scale=scale, bias=bias)
@@ -86,9 +86,10 @@ def test_ragged_bitwise_vs_elementwise(orc, env, fmt, nb):
 
 
 @pytest.mark.parametrize("fmt", [F32, F16, Q8_0, Q4_0])
-def test_vocabulary_projection_shape(orc, fmt):
+def test_vocabulary_projection_shape(orc, env, fmt):
     # [M, 1280] . [1280, 51866] on the planner's own plan (wide segments:
-    # B streams more than 16 MiB)
+    # B streams more than 16 MiB), on the ragged-row loads
+    env["TML_GEMV_RAGGED"] = "2"
     k, n = 1280, 51866
     b, scale, ref, tol = weight(orc, fmt, rnd(911, k, n, 0.02))
     for m in (1, 2, 4):
@@ -105,6 +106,7 @@ def test_next_row_nonfinite_stays_in_dropped_columns(orc, env, fmt, lpr):
     # elements == 1) reads it as a column past N.  Column 0 itself must come
     # out NaN (x has both signs), every other column finite and right.
     env["TML_GEMV_LPR"] = lpr
+    env["TML_GEMV_RAGGED"] = "2"
     k, n = 300, 1001
     w = rnd(921, k, n, 0.02)
     w[:, 0] = np.inf
@@ -120,9 +122,10 @@ def test_next_row_nonfinite_stays_in_dropped_columns(orc, env, fmt, lpr):
 
 
 @pytest.mark.parametrize("fmt,offset", [(Q8_0, 1), (Q8_0, 2), (Q4_0, 3), (F16, 2)])
-def test_unaligned_weight_pointer(orc, fmt, offset):
+def test_unaligned_weight_pointer(orc, env, fmt, offset):
     # B starting 1-3 bytes past an aligned address cannot take the dword
-    # path; the element-wise one gives the same answer.
+    # path (TML_GEMV_RAGGED=2 refuses the call); the element-wise one gives
+    # the same answer.
     import torch
     k, n = 517, 333
     b, scale, ref, tol = weight(orc, fmt, rnd(931, k, n, 0.02))
@@ -134,16 +137,21 @@ def test_unaligned_weight_pointer(orc, fmt, offset):
         a = rnd(932 + m, m, k)
         x = torch.from_numpy(a).to(dev)
         y = torch.zeros((m, n), dtype=torch.float32, device=dev)
+        env["TML_GEMV_RAGGED"] = "2"
+        with pytest.raises(_abi.TmlError):
+            _abi.gemm_dev(fmt, m, n, k, x.data_ptr(), buf.data_ptr() + offset, y.data_ptr(), scale=scale)
+        env["TML_GEMV_RAGGED"] = "1"
         _abi.gemm_dev(fmt, m, n, k, x.data_ptr(), buf.data_ptr() + offset, y.data_ptr(), scale=scale)
         torch.cuda.synchronize()
         assert rel_err(y.cpu().numpy(), ref(a)) <= tol, (fmt, offset, m)
 
 
 @pytest.mark.parametrize("fmt", [_abi.FMT_Q8_0_PC, _abi.FMT_Q4_0_PC])
-def test_ragged_per_column_scales(orc, fmt):
+def test_ragged_per_column_scales(orc, env, fmt):
     # Per-output-column scales (Q8_0 / Q4_0 bytes, one scale a column) on
     # ragged rows, with a bias and a residual, and with the exact GELU after
     # the bias.
+    env["TML_GEMV_RAGGED"] = "2"
     k, n = 517, 333
     w = rnd(941, k, n, 0.02)
     q, s = (orc.quantize_q8_cols if fmt == _abi.FMT_Q8_0_PC else orc.quantize_q4_cols)(w)

@@ -632,6 +632,10 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     const int64_t lim = (int64_t)1 << 30;
     if (m.N >= lim || m.K >= lim) return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV dimension exceeds 2^30");
     const GemvPlan p = make_plan(m);
+    // TML_GEMV_RAGGED=2 (tests): refuse a call that would not take the
+    // ragged-row loads, so a test proves that they ran
+    if (p.mode != kRagged && env_int("TML_GEMV_RAGGED", 1) == 2)
+        return Status::Err(TML_ERR_INVALID_ARG, "TML_GEMV_RAGGED=2: this call does not take the ragged-row loads");
     if (p.nsplit > 1) {
         const size_t need = (size_t)p.nsplit * p.mr * (size_t)m.N;
         if (ws.partials == nullptr || ws.partial_floats < need || ws.counters == nullptr ||
