@@ -107,6 +107,8 @@ def parse():
                    help="only config 3 at M = 128 / 512 (Q8_0, bf16 matrix-core GEMM), for kernel traces")
     p.add_argument("--config5-quant-only", action="store_true",
                    help="only the config-5 sweep with Q8_0 / Q4_0 weights (bf16 matrix-core GEMM), for kernel traces")
+    p.add_argument("--gemv-only", action="store_true",
+                   help="only the decoder GEMVs (configs 3/4, vocabulary projections) with their read floors")
     p.add_argument("--profile-gemv", action="store_true",
                    help="only run the decoder GEMVs (configs 3/4, M = 1) 50 times per path, eagerly, for rocprofv3")
     return p.parse_args()
@@ -137,8 +139,19 @@ def encoder_weights(layers: int, workers: int):
                 log(f"config-5 weights: {li + 1} of {layers} layers drawn")
         return out
     import multiprocessing as mp
-    with mp.get_context("spawn").Pool(max(1, min(workers, layers))) as pool:
-        return pool.map(_layer_weights, range(layers))
+    from multiprocessing import resource_tracker
+    pool = mp.get_context("spawn").Pool(max(1, min(workers, layers)))
+    try:
+        out = pool.map(_layer_weights, range(layers))
+    finally:
+        pool.close()
+        pool.join()
+    # The spawn context started a resource-tracker process for the pool's
+    # locks; stop it now, so that no process of this run outlives it.
+    tracker = getattr(resource_tracker, "_resource_tracker", None)
+    if tracker is not None and hasattr(tracker, "_stop"):
+        tracker._stop()
+    return out
 
 
 class Timer:
@@ -190,7 +203,7 @@ def main():
     from tomoul_amd import synth
 
     headline = not (args.config1_only or args.config2_only or args.qgemm_only or args.profile_gemv or
-                    args.calibrate_copy)
+                    args.calibrate_copy or args.gemv_only)
     if headline:
         t0 = time.perf_counter()
         host_w = encoder_weights(args.layers, args.gen_workers)
@@ -220,6 +233,9 @@ def main():
         return
     if args.qgemm_only:
         print(json.dumps({"qgemm": bench_qgemm(torch, dev, sptr, timer, _abi, synth, np)}), flush=True)
+        return
+    if args.gemv_only:
+        print(json.dumps({"gemv": bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np)}), flush=True)
         return
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -405,7 +421,7 @@ def bench_config5_quant(torch, dev, sptr, _abi, wdev, x, h, outs, layers):
         for li in range(layers):
             row = []
             for i, (_, M, N, K) in enumerate(ENC_SHAPES):
-                nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+                nbytes = _abi.weight_bytes(fmt, K, N)
                 q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
                 sc = torch.empty(1, dtype=torch.float32, device=dev)
                 _abi.quantize_dev(fmt, K * N, wdev[li][i].data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
@@ -424,7 +440,7 @@ def bench_config5_quant(torch, dev, sptr, _abi, wdev, x, h, outs, layers):
 
         ms = Timer(torch, settle_s=0.5).time_ms(sweep, 5)
         tf = flops / (ms * 1e-3) / 1e12
-        wbytes = layers * sum((K * N if fmt == _abi.FMT_Q8_0 else K * N // 2) for (_, M, N, K) in ENC_SHAPES)
+        wbytes = layers * sum(_abi.weight_bytes(fmt, K, N) for (_, M, N, K) in ENC_SHAPES)
         res[name] = {"ms_per_sweep": round(ms, 3), "TFLOP/s": round(tf, 2), "frac": qgemm_frac(1500, tf),
                      "frac_of_fp32_peak": round(tf / FP32_PEAK_TFLOPS, 4), "weight_bytes": wbytes,
                      **qgemm_peak(1500)}
@@ -542,11 +558,12 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
     Algorithmic bytes per launch = weight bytes + scale bytes (4, or 4*N for
     the per-column formats) + 4*M*K + 4*M*N.
     Each timed pass walks >= 1 GiB of distinct weight copies, so neither L2
-    nor the 256 MB Infinity Cache serves them.  Beside each: the floor for
-    the same weight bytes over the same rotation (torch's device copy of
-    them; torch's read-only row reduction is listed too and is slower) and
-    the GEMV's time as a fraction of it ("frac_of_floor" = floor / GEMV
-    time)."""
+    nor the 256 MB Infinity Cache serves them.  Beside each: the read floor
+    for the same weight bytes over the same rotation of the same copies
+    (tml_hip_stream_read_dev, 16-byte loads only, the fastest of 1, 2, 4
+    and 8 loads a lane) and the GEMV's time as a fraction of it
+    ("frac_of_floor" = floor / GEMV time); torch's device copy of the same
+    bytes and its read-only row reduction are listed as context."""
     out = {}
     rot_bytes = 1 << 30
 
@@ -557,8 +574,8 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
         w = synth.normal_matrix(seed, K, N, 0.02)
         wt = torch.from_numpy(w).to(dev)
         cols = fmt in (_abi.FMT_Q8_0_PC, _abi.FMT_Q4_0_PC)
-        wbytes = K * N if fmt in (_abi.FMT_Q8_0, _abi.FMT_Q8_0_PC) else (K * N + 1) // 2
-        sbytes = 4 * N if cols else 4
+        wbytes = _abi.weight_bytes(fmt, K, N)
+        sbytes = 4 * _abi.scale_count(fmt, K, N)
         q = torch.empty(wbytes, dtype=torch.uint8, device=dev)
         sc = torch.empty(sbytes // 4, dtype=torch.float32, device=dev)
         if cols:
@@ -574,7 +591,8 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
         ptrs = [copies[i].data_ptr() for i in range(ncopy)]
         handles = [_abi.prepare_ex_dev(fmt, K, N, p, scale=scale, scales_ptr=sc_ptr, stream=sptr) for p in ptrs]
         torch.cuda.synchronize()
-        res = {}
+        res = {"read_floor": stream_floor(ptrs, wbytes, label)}
+        floor_us = res["read_floor"]["us"]
         for M in Ms:
             x = torch.from_numpy(synth.normal_matrix(1001, M, K)).to(dev)
             y = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -590,19 +608,21 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
                 for h in handles:
                     _abi.gemm_prepared(h, M, x.data_ptr(), y.data_ptr(), stream=st)
 
-            floor_us = read_floor(wbytes)
             entry["floor_us"] = floor_us
+            entry["torch_copy_us"] = read_floor(wbytes)
             for name, fn in (("prepared", prep), ("kn", kn)):
                 ms = timer.time_ms(fn, 3, per_replay=ncopy)
                 gbs = alg / (ms * 1e-3) / 1e9
                 entry[name] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                                "frac_of_floor": round(floor_us / (ms * 1e3), 4)}
                 log(f"gemv {label} M={M} {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s "
-                    f"({floor_us / (ms * 1e3):.2f} of the copy floor)")
+                    f"({floor_us / (ms * 1e3):.2f} of the read floor)")
             res[f"M{M}"] = entry
         # the decoder's growth with M: each row count's prepared time over M = 1's
         if "M1" in res:
             for key, entry in res.items():
+                if key == "read_floor":
+                    continue
                 entry["prepared"]["x_of_M1"] = round(entry["prepared"]["us"] / res["M1"]["prepared"]["us"], 3)
         for h in handles:
             _abi.prepared_free(h)
@@ -652,6 +672,27 @@ def bench_gemv(torch, dev, stream, sptr, timer, _abi, synth, np):
         del copies, copies_t
         torch.cuda.empty_cache()
         return res
+
+    def stream_floor(ptrs, nbytes, label):
+        # The read floor: one tml_hip_stream_read_dev launch per weight copy,
+        # over the same rotation the GEMVs walk; the fastest of 1, 2, 4 and 8
+        # 16-byte loads a lane.
+        out_buf = torch.empty(nbytes // 4096 + 2, dtype=torch.float32, device=dev)
+        by_u = {}
+        for u in (1, 2, 4, 8):
+            def fn(st, u=u):
+                for p in ptrs:
+                    _abi.stream_read_dev(p, nbytes, u, out_buf.data_ptr(), st)
+            by_u[u] = timer.time_ms(fn, 3, per_replay=len(ptrs)) * 1e3
+        best = min(by_u, key=by_u.get)
+        us = by_u[best]
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"read floor {label} ({nbytes} B): {us:.2f} us ({best} loads a lane), {gbs:.0f} GB/s; "
+            + ", ".join(f"{u}: {t:.2f}" for u, t in by_u.items()))
+        del out_buf
+        return {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "chunks_per_lane": best, "us_by_chunks_per_lane": {str(u): round(t, 3) for u, t in by_u.items()},
+                "kernel": "stream_read_kernel (tml_hip_stream_read_dev)"}
 
     floors = {}
 
@@ -730,7 +771,7 @@ def bench_qgemm(torch, dev, sptr, timer, _abi, synth, np):
     res = {}
     K, N = 1024, 4096
     w = torch.from_numpy(synth.normal_matrix(2002, K, N, 0.02)).to(dev)
-    q = torch.empty(K * N, dtype=torch.uint8, device=dev)
+    q = torch.empty(_abi.weight_bytes(_abi.FMT_Q8_0, K, N), dtype=torch.uint8, device=dev)
     sc = torch.empty(1, dtype=torch.float32, device=dev)
     _abi.quantize_dev(_abi.FMT_Q8_0, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
     torch.cuda.synchronize()
@@ -791,8 +832,8 @@ def bench_sentence_transformer(torch, dev, sptr, timer, _abi, synth, tokens: int
                     keep.append(w)
                     row.append((K, N, w.data_ptr(), None))
                     continue
-                b = torch.empty(K * N * (2 if fmt == _abi.FMT_F16 else 1), dtype=torch.uint8, device=dev)
-                sc = torch.empty(max(K * N // 32, 1), dtype=torch.float32, device=dev)
+                b = torch.empty(_abi.weight_bytes(fmt, K, N), dtype=torch.uint8, device=dev)
+                sc = torch.empty(max(_abi.scale_count(fmt, K, N), 1), dtype=torch.float32, device=dev)
                 _abi.quantize_dev(fmt, K * N, w.data_ptr(), b.data_ptr(), sc.data_ptr(), sptr)
                 keep += [b, sc]
                 row.append((K, N, b.data_ptr(), sc.data_ptr() if fmt == _abi.FMT_Q8_K else None))
@@ -832,7 +873,7 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
                          (_abi.FMT_Q4_0, 5120, 1280, 1), (_abi.FMT_Q4_0, 5120, 1280, 4),
                          (_abi.FMT_Q4_0, 5120, 1280, 8)):
         w = torch.from_numpy(synth.normal_matrix(2002, K, N, 0.02)).to(dev)
-        nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+        nbytes = _abi.weight_bytes(fmt, K, N)
         q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         sc = torch.empty(1, dtype=torch.float32, device=dev)
         _abi.quantize_dev(fmt, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
@@ -855,7 +896,7 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
     for fmt, ncopy in ((_abi.FMT_Q8_0, 3), (_abi.FMT_Q4_0, 4)):
         K, N = 1280, 51866
         w = torch.from_numpy(synth.normal_matrix(2004, K, N, 0.02)).to(dev)
-        nbytes = K * N if fmt == _abi.FMT_Q8_0 else (K * N + 1) // 2
+        nbytes = _abi.weight_bytes(fmt, K, N)
         q = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         sc = torch.empty(1, dtype=torch.float32, device=dev)
         _abi.quantize_dev(fmt, K * N, w.data_ptr(), q.data_ptr(), sc.data_ptr(), sptr)
@@ -896,6 +937,27 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
     torch.cuda.empty_cache()
     log(f"profile-gemv: f32 embedding {N}x{K}: {launches} launches in place + {launches} on its transpose")
     print(json.dumps({"profile_gemv": True}), flush=True)
+
+
+def host_nproc() -> int:
+    """CPUs this process may run on (what `nproc` prints)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def host_cpu_model() -> str:
+    """The host CPU's model string (`model name` of /proc/cpuinfo, as lscpu shows it)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline(budget_s: float, host_w, host_x, host_h, quantized: bool = True):
@@ -944,7 +1006,8 @@ def cpu_baseline(budget_s: float, host_w, host_x, host_h, quantized: bool = True
                      f"headline's own inputs) with the oracle's restatement of the ops.zig:277-414 fallback, "
                      f"1 thread, -O3 AVX2, {t1:.1f} s; zblas (the reference default) is not vendored and "
                      f"cannot be timed, OpenBLAS is not installed",
-           "host_cpus": os.cpu_count(), "threaded": threaded}
+           "host_cpus": os.cpu_count(), "nproc": host_nproc(), "cpu_model": host_cpu_model(),
+           "threaded": threaded}
     if quantized:
         out["quantized"] = cpu_quantized(orc)
     return out

@@ -134,7 +134,12 @@ int tml_hip_sgemm_q8(int64_t M, int64_t N, int64_t K, const float *A, const int8
  * fp32 activation split into two bf16 terms (|x - hi - lo| <= 2^-17 |x|),
  * accumulated in fp32; below that on fp32 multiply-adds.  Both agree with
  * the reference's dequantize-then-fp32-accumulate result to ~1e-5 relative;
- * infinities and NaNs in A give what the reference gives. */
+ * infinities and NaNs in A give what the reference gives.  Limit: the
+ * per-tensor scale multiplies the finished sum (the reference multiplies
+ * each element, a * (q * s)), so finite activations large enough that
+ * x * q overflows fp32 (|x| > FLT_MAX / 127 for int8, / 8 for int4) -- and on
+ * the matrix cores any finite |x| above the largest bf16, 3.39e38, whose hi
+ * term rounds to inf -- give inf or NaN where the reference stays finite. */
 
 /* C = A . dequant(Q8_K B).  Replaces zblas.sgemmQ8K(m, n, k, a, b.data,
  * b.scales, b.block_size, c) at src/core/quantization.zig:555
@@ -263,6 +268,15 @@ int tml_hip_gemm_ex_dev_noalloc(int fmt, int64_t M, int64_t N, int64_t K, const 
  * 1 float (Q8_0 / Q4_0), ceil(n/32) floats (Q8_K) or nothing (F16, may be
  * NULL).  Device pointers, asynchronous on stream. */
 int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream);
+
+/* Read floor of the decoder GEMVs.  No counterpart in the reference: a
+ * measurement aid for callers and benchmarks that want to know what one
+ * launch streaming `bytes` of device memory costs on this GPU.  Reads
+ * bytes (0 <= bytes < 2^31) at src with 16-byte loads, chunks_per_lane
+ * (1, 2, 4 or 8) of them per lane, all issued before any is used, and
+ * writes one value per workgroup -- ceil(bytes / (chunks_per_lane * 4096))
+ * floats -- to out.  Asynchronous on stream. */
+int tml_hip_stream_read_dev(const void *src, int64_t bytes, int chunks_per_lane, float *out, void *stream);
 
 /* Per-output-column quantizers for TML_FMT_Q8_0_PC / TML_FMT_Q4_0_PC: w is
  * W[K,N] row-major; q receives the Q8_0 / Q4_0 data of W, scales the N

@@ -65,6 +65,8 @@ pub extern "c" fn tml_hip_gemm_ex_dev_noalloc(fmt: c_int, M: i64, N: i64, K: i64
 pub extern "c" fn tml_hip_quantize_dev(fmt: c_int, n: i64, w: [*]const f32, q: *anyopaque, scales: ?[*]f32, stream: ?*anyopaque) c_int;
 pub extern "c" fn tml_hip_quantize_cols_dev(fmt: c_int, K: i64, N: i64, w: [*]const f32, q: *anyopaque, scales: [*]f32, stream: ?*anyopaque) c_int;
 pub extern "c" fn tml_hip_quantize_cols(fmt: c_int, K: i64, N: i64, w: [*]const f32, q: *anyopaque, scales: [*]f32) c_int;
+/// Read floor of the decoder GEMVs (a measurement aid, no reference counterpart).
+pub extern "c" fn tml_hip_stream_read_dev(src: *const anyopaque, bytes: i64, chunks_per_lane: c_int, out: [*]f32, stream: ?*anyopaque) c_int;
 
 // -------------------------------------------------- prepared weights
 pub extern "c" fn tml_hip_prepare_dev(fmt: c_int, K: i64, N: i64, B: *const anyopaque, scale: f32, stream: ?*anyopaque, out: *Prepared) c_int;

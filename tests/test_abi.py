@@ -112,3 +112,61 @@ def test_c_program_links_and_runs(tmp_path):
     out = subprocess.run([str(exe), fixture], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "y(10) = 21" in out.stdout
+
+
+# Payload framing of each .tl format, written by the reference's exporter
+# (tools/tl_format.py:309-360): bytes before the element data, and per scale.
+_TL_FRAMING = {_abi.FMT_F32: (0, 0), _abi.FMT_F16: (0, 0), _abi.FMT_Q8_0: (4, 0), _abi.FMT_Q4_0: (4, 0),
+               _abi.FMT_Q8_K: (4, 4)}
+
+
+def test_weight_bytes_match_exporter_payloads(orc):
+    """weight_bytes / scale_count against the payload sizes the reference's
+    exporter wrote (tests/golden/tl/exporter_*.tl; odd lengths, rank 3 and an
+    all-zero tensor among them): payload = framing + 4 * scales + data."""
+    gold = os.path.join(ROOT, "tests", "golden", "tl")
+    files = {_abi.FMT_F32: "exporter_f32.tl", _abi.FMT_Q8_0: "exporter_q8_0.tl", _abi.FMT_Q4_0: "exporter_q4_0.tl",
+             _abi.FMT_Q8_K: "exporter_q8_k.tl", _abi.FMT_F16: "exporter_f16.tl"}
+    for fmt, name in files.items():
+        with open(os.path.join(gold, name), "rb") as f:
+            parsed = orc.tl_parse(f.read())
+        head, _ = _TL_FRAMING[fmt]
+        for tname, shape, _off, size in parsed["tensors"]:
+            n = int(np.prod(shape))
+            ns = _abi.scale_count(fmt, 1, n)
+            scale_bytes = 4 * ns if fmt == _abi.FMT_Q8_K else 0
+            assert head + scale_bytes + _abi.weight_bytes(fmt, 1, n) == size, (fmt, tname, shape)
+            # the [K,N] form of the same element count gives the same sizes
+            k = shape[0]
+            assert _abi.weight_bytes(fmt, k, n // k) == _abi.weight_bytes(fmt, 1, n)
+
+
+@pytest.mark.parametrize("shape", [(5, 7), (64, 32), (37, 11), (1, 1)])
+def test_weight_bytes_match_oracle_quantizers(orc, shape):
+    """Every one of the seven formats against the size of what the oracle's
+    quantizers (restating src/core/quantization.zig:98-129, :406-446,
+    :721-754, :1859-1900 and their per-column forms) produce."""
+    k, n = shape
+    w = np.linspace(-1.0, 1.0, k * n, dtype=np.float32).reshape(k, n)
+    q8, _ = orc.quantize_q8(w)
+    q4, _ = orc.quantize_q4(w)
+    q8k, s8k = orc.quantize_q8k(w)
+    q8c, s8c = orc.quantize_q8_cols(w)
+    q4c, s4c = orc.quantize_q4_cols(w)
+    expect = {
+        _abi.FMT_F32: (w.nbytes, 0), _abi.FMT_F16: (orc.to_f16(w).nbytes, 0), _abi.FMT_Q8_0: (q8.nbytes, 1),
+        _abi.FMT_Q4_0: (q4.nbytes, 1), _abi.FMT_Q8_K: (q8k.nbytes, s8k.size), _abi.FMT_Q8_0_PC: (q8c.nbytes, s8c.size),
+        _abi.FMT_Q4_0_PC: (q4c.nbytes, s4c.size),
+    }
+    assert sorted(expect) == sorted(_abi.FORMATS)
+    for fmt, (nbytes, nscales) in expect.items():
+        assert _abi.weight_bytes(fmt, k, n) == nbytes, fmt
+        assert _abi.scale_count(fmt, k, n) == nscales, fmt
+
+
+def test_weight_bytes_refuse_unknown_format():
+    for bad in (5, 16, 19, -1):
+        with pytest.raises(ValueError):
+            _abi.weight_bytes(bad, 4, 4)
+        with pytest.raises(ValueError):
+            _abi.scale_count(bad, 4, 4)

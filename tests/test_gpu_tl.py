@@ -58,7 +58,7 @@ def test_read_dev_and_dequantized(orc, tmp_path, fmt):
     ld = tl.ModelLoader(path)
     for name, shp, parts in tensors:
         n = shp[0] * shp[1]
-        nbytes = {0: 4 * n, 4: 2 * n, 1: n, 2: (n + 1) // 2, 3: n}[fmt]
+        nbytes = _abi.weight_bytes(fmt, 1, n)
         buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
         sc = torch.empty(max((n + 31) // 32, 1), dtype=torch.float32, device="cuda")
         scale = ld.readDev(name, fmt, buf.data_ptr(), sc.data_ptr() if fmt == 3 else None)
@@ -178,7 +178,7 @@ def test_exporter_files_to_hbm_and_matmul(orc, fmt):
         name, shp = e[0], e[1]
         n = int(np.prod(shp))
         parts = orc.tl_payload(data, e, fmt)
-        nbytes = {0: 4 * n, 4: 2 * n, 1: n, 2: (n + 1) // 2, 3: n}[fmt]
+        nbytes = _abi.weight_bytes(fmt, 1, n)
         buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
         sc = torch.empty(max((n + 31) // 32, 1), dtype=torch.float32, device="cuda")
         scale = ld.readDev(name, fmt, buf.data_ptr(), sc.data_ptr() if fmt == 3 else None)

@@ -42,10 +42,13 @@ def _operands(torch, seed, m, n, k):
 
 
 def test_growth_refused_during_capture(env):
-    # 2048 x 2048 x 512 split 8 needs 8 * 2048 * 2048 partial sums (128 MiB),
-    # more than any other test's plan, so no earlier call has grown the
-    # workspace that far.
+    # 2048 x 2048 x 512 split 8 needs 8 * 2048 * 2048 partial sums (128 MiB).
+    # A fresh library context starts with no workspace, so the call must grow
+    # it whatever the tests before this one ran.
     import torch
+    torch.cuda.synchronize()
+    _abi.shutdown()
+    _abi.init()
     env["TML_GEMM_SPLIT"] = "8"
     m, n, k = 2048, 2048, 512
     a, b, c = _operands(torch, 301, m, n, k)

@@ -20,7 +20,7 @@ SCRATCH = 16 << 20  # TML_NOALLOC_SCRATCH_BYTES
 
 @pytest.fixture
 def env():
-    keys = ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE")
+    keys = ("TML_GEMM_SPLIT", "TML_GEMM_DMA_TILE", "TML_REQUIRE_SPLIT")
     saved = {k: os.environ.get(k) for k in keys}
     yield os.environ
     for k, v in saved.items():
@@ -38,7 +38,7 @@ def _problem(torch, seed, fmt, m, n, k, with_res=False):
         b = torch.from_numpy(w).cuda()
     else:
         wd = torch.from_numpy(w).cuda()
-        nbytes = k * n if fmt == _abi.FMT_Q8_0 else (k * n + 1) // 2
+        nbytes = _abi.weight_bytes(fmt, k, n)
         b = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
         sc = torch.empty(1, dtype=torch.float32, device="cuda")
         _abi.quantize_dev(fmt, k * n, wd.data_ptr(), b.data_ptr(), sc.data_ptr())
@@ -60,7 +60,7 @@ def _both(torch, fmt, m, n, k, a, b, scale, bias, res, act):
     return out
 
 
-@pytest.mark.parametrize("case", ["gemm_split", "gemv_split", "gemm_plain"])
+@pytest.mark.parametrize("case", ["gemm_split", "gemv_split", "qbf_split_q8", "qbf_split_q4", "gemm_plain"])
 def test_matches_existing_entry_point(env, case):
     import torch
     _abi.init()
@@ -71,8 +71,17 @@ def test_matches_existing_entry_point(env, case):
     elif case == "gemv_split":
         # [K,N] GEMV, M <= 8, long K: split over workgroups (partials + counters)
         shapes, fmt, act = [(4, 1024, 8192), (3, 512, 4096)], _abi.FMT_Q8_0, _abi.ACT_NONE
+    elif case == "qbf_split_q8":
+        # bf16 matrix-core GEMM with its default K split (few 32 x 64 tiles)
+        shapes, fmt, act = [(128, 1024, 4096), (128, 512, 2048)], _abi.FMT_Q8_0, _abi.ACT_GELU_ERF
+    elif case == "qbf_split_q4":
+        shapes, fmt, act = [(128, 1024, 4096), (128, 512, 2048)], _abi.FMT_Q4_0, _abi.ACT_NONE
     else:
         shapes, fmt, act = [(1500, 1536, 384), (700, 768, 384)], _abi.FMT_F32, _abi.ACT_GELU_TANH
+    if case != "gemm_plain":
+        # both entry points refuse a plan that does not split K, so the
+        # partials (and, for the GEMV, the arrival counters) were used
+        env["TML_REQUIRE_SPLIT"] = "1"
     for i, (m, n, k) in enumerate(shapes):
         a, b, scale, bias, res = _problem(torch, 500 + 10 * i, fmt, m, n, k, with_res=(i == 1))
         ref, got = _both(torch, fmt, m, n, k, a, b, scale, bias, res, act)
@@ -91,6 +100,29 @@ def test_oversized_plan_is_refused(env):
     c = torch.zeros((m, n), dtype=torch.float32, device="cuda")
     with pytest.raises(_abi.TmlError) as e:
         _abi.gemm_ex_dev_noalloc(_abi.FMT_F32, m, n, k, a.data_ptr(), b.data_ptr(), c.data_ptr())
+    assert e.value.code == _abi.TML_ERR_INVALID_SHAPE and "static scratch" in str(e.value)
+    torch.cuda.synchronize()
+    assert float(c.abs().max()) == 0.0  # nothing ran
+
+
+@pytest.mark.parametrize("fmt", [_abi.FMT_Q8_0, _abi.FMT_Q4_0])
+def test_default_plan_too_large_is_refused_not_shrunk(env, fmt):
+    """Whisper FFN-down (1500 x 1280 x 5120) in Q8_0 / Q4_0: the bf16 GEMM's
+    default plan splits K three ways, 3 * 1500 * 1280 floats = 23 MB of
+    partial sums, more than the static scratch.  The allocation-free call
+    refuses it rather than running a smaller split with other bits; the
+    allocating call runs that plan (TML_REQUIRE_SPLIT=1 shows it splits)."""
+    import torch
+    m, n, k = 1500, 1280, 5120
+    a, b, scale, bias, _ = _problem(torch, 720, fmt, m, n, k)
+    env["TML_REQUIRE_SPLIT"] = "1"
+    c = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    _abi.gemm_ex_dev(fmt, m, n, k, a.data_ptr(), b.data_ptr(), c.data_ptr(), scale=scale)
+    torch.cuda.synchronize()
+    assert float(c.abs().max()) > 0.0
+    c.zero_()
+    with pytest.raises(_abi.TmlError) as e:
+        _abi.gemm_ex_dev_noalloc(fmt, m, n, k, a.data_ptr(), b.data_ptr(), c.data_ptr(), scale=scale)
     assert e.value.code == _abi.TML_ERR_INVALID_SHAPE and "static scratch" in str(e.value)
     torch.cuda.synchronize()
     assert float(c.abs().max()) == 0.0  # nothing ran

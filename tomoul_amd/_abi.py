@@ -33,6 +33,45 @@ TML_ERR_UNSUPPORTED_QUANT_FORMAT = -13
 FMT_F32, FMT_Q8_0, FMT_Q4_0, FMT_Q8_K, FMT_F16 = 0, 1, 2, 3, 4
 FMT_Q8_0_PC, FMT_Q4_0_PC = 17, 18  # per-output-column scales (not reference formats)
 ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH = 0, 1, 2
+FORMATS = (FMT_F32, FMT_Q8_0, FMT_Q4_0, FMT_Q8_K, FMT_F16, FMT_Q8_0_PC, FMT_Q4_0_PC)
+
+
+def weight_bytes(fmt: int, k: int, n: int) -> int:
+    """Bytes of a [K,N] weight's element data in format fmt (scales excluded).
+
+    The layouts are the reference's in-memory tensors: f32 `[]f32`
+    (src/core/tensor.zig:12-18), Q8_0 `data: []i8` (src/core/quantization.zig:39-90),
+    Q8_K `data: []i8` (:327-403), Q4_0 `(n+1)/2` packed bytes (:627-711),
+    F16 `[]f16` (:1859-1900); the per-column formats store Q8_0 / Q4_0's bytes.
+    Raises ValueError for a format it does not know, so that a new format
+    cannot silently take another format's size.
+    """
+    e = int(k) * int(n)
+    if fmt == FMT_F32:
+        return 4 * e
+    if fmt == FMT_F16:
+        return 2 * e
+    if fmt in (FMT_Q8_0, FMT_Q8_K, FMT_Q8_0_PC):
+        return e
+    if fmt in (FMT_Q4_0, FMT_Q4_0_PC):
+        return (e + 1) // 2
+    raise ValueError(f"unknown weight format {fmt}")
+
+
+def scale_count(fmt: int, k: int, n: int, block: int = 32) -> int:
+    """f32 scales a [K,N] weight in format fmt carries: 0 (f32 / f16), 1 (Q8_0 /
+    Q4_0, per tensor), ceil(K*N/block) (Q8_K, src/core/quantization.zig:327-403),
+    N (per-column formats).  Raises ValueError for an unknown format."""
+    if fmt in (FMT_F32, FMT_F16):
+        return 0
+    if fmt in (FMT_Q8_0, FMT_Q4_0):
+        return 1
+    if fmt == FMT_Q8_K:
+        return -(-int(k) * int(n) // int(block))
+    if fmt in (FMT_Q8_0_PC, FMT_Q4_0_PC):
+        return int(n)
+    raise ValueError(f"unknown weight format {fmt}")
+
 
 # Every symbol the header declares, with its ctypes signature.
 _i64 = ctypes.c_int64
@@ -75,6 +114,7 @@ SIGNATURES = {
     "tml_hip_quantize_cols": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _vp, _vp]),
     "tml_hip_prepare_ex_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _f, _vp, _vp, ctypes.POINTER(_vp)]),
     "tml_hip_transpose_requant_dev": (ctypes.c_int, [ctypes.c_int, _i64, _i64, _vp, _vp, _f, _vp, _vp, _vp]),
+    "tml_hip_stream_read_dev": (ctypes.c_int, [_vp, _i64, ctypes.c_int, _vp, _vp]),
     "tml_tl_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "tml_tl_open_bytes": (ctypes.c_int, [_vp, ctypes.c_uint64, ctypes.POINTER(_vp)]),
     "tml_tl_close": (ctypes.c_int, [_vp]),
@@ -235,6 +275,13 @@ def gemm_ex_dev_noalloc(fmt: int, m: int, n: int, k: int, a_ptr: int, b_ptr: int
     """tml_hip_gemm_ex_dev_noalloc: gemm_ex_dev with the static split-K scratch (no device allocation)."""
     check(lib().tml_hip_gemm_ex_dev_noalloc(fmt, m, n, k, a_ptr, b_ptr, scale, scales_ptr, block, bias_ptr,
                                             residual_ptr, act, c_ptr, alpha, beta, stream))
+
+
+def stream_read_dev(src_ptr: int, nbytes: int, chunks_per_lane: int, out_ptr: int,
+                    stream: int | None = None) -> None:
+    """tml_hip_stream_read_dev: the GEMV read floor (reads nbytes, writes
+    ceil(nbytes / (chunks_per_lane * 4096)) partials to out)."""
+    check(lib().tml_hip_stream_read_dev(src_ptr, nbytes, chunks_per_lane, out_ptr, stream))
 
 
 def quantize_dev(fmt: int, n: int, w_ptr: int, q_ptr: int, scales_ptr: int, stream: int | None = None) -> None:

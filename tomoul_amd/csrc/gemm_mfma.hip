@@ -686,6 +686,9 @@ Status launch_gemm_mfma(const MatmulArgs &m, const Workspace &ws, hipStream_t s)
                            "forced GEMM plans (TML_GEMM_* overrides) are refused above M*N*K = 512*1024*4096, "
                            "the largest size the tests run them at");
     const GemmPlan p = plan_gemm(m);
+    // TML_REQUIRE_SPLIT=1 (tests): refuse a plan that does not split K
+    if (!((p.qbf || p.dma) && p.nsplit > 1) && env_int("TML_REQUIRE_SPLIT", 0) == 1)
+        return Status::Err(TML_ERR_INVALID_ARG, "TML_REQUIRE_SPLIT=1: this call's plan does not split K");
     if (p.qbf) return launch_gemm_qbf(m, p, ws, s);
     if (p.dma) return launch_gemm_f32_dma(m, p, ws, s);
     const int cus = device_cus();

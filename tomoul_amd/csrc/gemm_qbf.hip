@@ -378,7 +378,7 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
 //     these, except 512x4096x1024 23.6 against 22.4 us at 64x64x64);
 //   * 128x128 unsplit when 64x128 tiles would give each CU more than 4.5;
 //   * else the tile (64x128, 64x64, 32x64) and K split s in 1..4 (at least
-//     eight 32-deep slices a split, within the workspace cap) of least
+//     eight 32-deep slices a split) of least
 //     modelled time
 //       t = ceil(tiles s / CUs) * (slices / s) * c / eff + 5.3 us + 1.7 us * (s - 1),
 //     c = 0.57 / 0.46 / 0.36 us a slice for the three tiles, eff = 1, 1.39,
@@ -402,7 +402,7 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
         return ((m.M + kQbfCfgs[c].bm - 1) / kQbfCfgs[c].bm) * ((m.N + kQbfCfgs[c].bn - 1) / kQbfCfgs[c].bn);
     };
     auto split_ok = [&](int64_t ns) {
-        return ns == 1 || (nk / ns >= 8 && (size_t)ns * (size_t)m.M * (size_t)m.N <= m.ws_cap_floats);
+        return ns == 1 || nk / ns >= 8;
     };
     int cfg = 1;
     int64_t nsplit = 1;
@@ -447,10 +447,6 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     const int64_t per = kQbfCfgs[cfg].bk / 32;
     int64_t spl = ((nk + nsplit - 1) / nsplit + per - 1) / per * per;
     nsplit = (nk + spl - 1) / spl;  // no split without slices
-    if (nsplit > 1 && (size_t)nsplit * (size_t)m.M * (size_t)m.N > m.ws_cap_floats) {
-        nsplit = 1;
-        spl = nk;
-    }
     p->cfg = cfg;
     p->nsplit = (int)nsplit;
     p->spl = (int)std::max<int64_t>(spl, 1);

@@ -636,6 +636,10 @@ Status launch_gemv(const MatmulArgs &m, const Workspace &ws, hipStream_t s) {
     // ragged-row loads, so a test proves that they ran
     if (p.mode != kRagged && env_int("TML_GEMV_RAGGED", 1) == 2)
         return Status::Err(TML_ERR_INVALID_ARG, "TML_GEMV_RAGGED=2: this call does not take the ragged-row loads");
+    // TML_REQUIRE_SPLIT=1 (tests): refuse a plan that does not split K, so a
+    // test of the split-K partials and counters proves that they were used
+    if (p.nsplit <= 1 && env_int("TML_REQUIRE_SPLIT", 0) == 1)
+        return Status::Err(TML_ERR_INVALID_ARG, "TML_REQUIRE_SPLIT=1: this call's plan does not split K");
     if (p.nsplit > 1) {
         const size_t need = (size_t)p.nsplit * p.mr * (size_t)m.N;
         if (ws.partials == nullptr || ws.partial_floats < need || ws.counters == nullptr ||

@@ -129,6 +129,11 @@ struct GrowBuf {
     std::vector<void *> retired;
     Status ensure(size_t n) {
         if (n <= bytes) return Status::Ok();
+        // Grow by at least half again, so that a sequence of rising sizes
+        // (a model load reading tensor after tensor) retires few buffers:
+        // the retired ones together stay below twice the live one.
+        n = std::max(n, bytes + bytes / 2);
+        n = (n + 255) & ~(size_t)255;
         void *q = nullptr;
         TML_HIP_TRY(hipMalloc(&q, n));
         if (p) retired.push_back(p);
@@ -210,8 +215,9 @@ void workspace_need(const MatmulArgs &m, size_t *partial_floats, size_t *counter
 }
 
 // Grow the split-K workspace to what this problem needs; new counters are
-// zeroed on `s` before the launch that needs them (kernels leave them zero
-// when they finish).  Growing allocates, so it is refused while `s` is being
+// zeroed, and the zeroing waited for, before this call returns (kernels
+// leave them zero when they finish), so a later call on any stream finds
+// them zero.  Growing allocates, so it is refused while `s` is being
 // captured into a graph: run every captured call once eagerly first.
 Status ensure_workspace(DeviceCtx *c, const MatmulArgs &m, hipStream_t s, Workspace *ws) {
     size_t pf = 0, nc = 0;
@@ -231,6 +237,7 @@ Status ensure_workspace(DeviceCtx *c, const MatmulArgs &m, hipStream_t s, Worksp
         if (grow_ctr) {
             TML_TRY(c->counters.ensure(nc * sizeof(unsigned)));
             TML_HIP_TRY(hipMemsetAsync(c->counters.p, 0, c->counters.bytes, s));
+            TML_HIP_TRY(hipStreamSynchronize(s));
         }
     }
     ws->partials = (float *)c->ws.p;
@@ -379,8 +386,10 @@ Status gemm_dev_noalloc(int fmt, int64_t M, int64_t N, int64_t K, const float *A
     if (empty) return Status::Ok();
     void *base = nullptr;
     TML_TRY(scratch_setup(s, &base));
+    // The plan is the one tml_hip_gemm_ex_dev would run (same kernels, same
+    // K splits, same bits); a plan whose partial sums do not fit the static
+    // scratch is refused, never replaced by a smaller split.
     const size_t cap_floats = (kScratchBytes - kScratchPartialOff) / sizeof(float);
-    m.ws_cap_floats = cap_floats;
     size_t pf = 0, nc = 0;
     workspace_need(m, &pf, &nc);
     if (pf > cap_floats || nc > kScratchCounters)
@@ -960,6 +969,13 @@ int tml_hip_prepared_free(tml_prepared_t w) {
     const hipError_t e = hipDeviceSynchronize();
     free_prepared(p);
     return report(e == hipSuccess ? Status::Ok() : hip_status(e, "hipDeviceSynchronize"));
+}
+
+int tml_hip_stream_read_dev(const void *src, int64_t bytes, int chunks_per_lane, float *out, void *stream) {
+    DeviceCtx *c = nullptr;
+    Status s = current_ctx(&c);
+    if (!s.ok()) return report(s);
+    return report(launch_stream_read(src, bytes, chunks_per_lane, out, (hipStream_t)stream));
 }
 
 int tml_hip_quantize_dev(int fmt, int64_t n, const float *w, void *q, float *scales, void *stream) {

@@ -63,10 +63,6 @@ struct MatmulArgs {
     int act = TML_ACT_NONE;  // activation after the bias (TML_ACT_*)
     const float *res = nullptr;  // [M,N] residual added after the bias (may equal C)
     const float *colscale = nullptr;  // [N] per-column factor on A.B (per-channel formats), or nullptr
-    // Largest split-K workspace (partial floats) the caller can supply; the
-    // planners keep their K splits within it (the allocation-free entry
-    // point's static scratch).
-    size_t ws_cap_floats = SIZE_MAX;
 };
 
 // Activations of the epilogue, restating the reference's CPU code.
@@ -272,6 +268,12 @@ Status launch_dequant(int fmt, int64_t n, const void *raw, const float *scales, 
                       hipStream_t s);
 Status launch_dequant_transpose(int fmt, int64_t rows, int64_t cols, const void *raw, const float *scales,
                                 float scale, float *out, hipStream_t s);
+
+// The GEMV read floor (stream_read.hip): reads `bytes` of src with
+// chunks_per_lane 16-byte loads a lane and writes stream_read_outputs()
+// partial values to out.
+int64_t stream_read_outputs(int64_t bytes, int chunks_per_lane);
+Status launch_stream_read(const void *src, int64_t bytes, int chunks_per_lane, float *out, hipStream_t s);
 
 // Tuning overrides for experiments (0 = heuristic).  Read from the
 // TML_GEMM_TILE / TML_GEMV_SPLIT environment variables once.
