@@ -198,3 +198,44 @@ def test_python_mirror_cols(orc, cls):
     assert rel_err(got, orc.gelu_tanh(ref + bias)) <= Q_TOL
     with pytest.raises(qz.InvalidShape):
         qz.quantizeColsQ8(Tensor.from_numpy(w.reshape(-1)))
+
+
+# The shapes and row counts the benchmark times for the per-column reading of
+# configs 3 and 4, with its weights (seed 2002, 2003 for 5120 x 1280): each
+# plan it times has its own oracle check, on the prepared copy and on the
+# [K,N] layout, after the column quantizer is checked bitwise.
+TIMED = [(_abi.FMT_Q8_0_PC, 1024, 4096, 2002, (1, 8, 128, 512)),
+         (_abi.FMT_Q4_0_PC, 1280, 5120, 2002, (1, 4, 8)),
+         (_abi.FMT_Q4_0_PC, 5120, 1280, 2003, (1, 4, 8))]
+
+
+@pytest.mark.parametrize("fmt,k,n,seed,ms", TIMED, ids=["q8pc_1024x4096", "q4pc_1280x5120", "q4pc_5120x1280"])
+def test_cols_at_timed_shapes(orc, fmt, k, n, seed, ms):
+    import torch
+    w = synth.normal_matrix(seed, k, n, 0.02)
+    q_ref, s_ref = _quant(orc, fmt, w)
+    W = _dev(w)
+    Q = torch.zeros(_abi.weight_bytes(fmt, k, n), dtype=torch.uint8, device="cuda:0")
+    S = torch.zeros(_abi.scale_count(fmt, k, n), dtype=torch.float32, device="cuda:0")
+    _abi.quantize_cols_dev(fmt, k, n, W.data_ptr(), Q.data_ptr(), S.data_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(Q.cpu().numpy(), q_ref.reshape(-1).view(np.uint8))
+    np.testing.assert_array_equal(S.cpu().numpy(), s_ref)
+    h = _abi.prepare_ex_dev(fmt, k, n, Q.data_ptr(), scales_ptr=S.data_ptr())
+    try:
+        for m in ms:
+            a = synth.normal_matrix(1001, m, k)
+            ref = orc.matmul_cols(a, fmt, q_ref, s_ref, k, n)
+            A = _dev(a)
+            for path in ("prepared", "kn"):
+                C = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+                if path == "prepared":
+                    _abi.gemm_prepared(h, m, A.data_ptr(), C.data_ptr())
+                else:
+                    _abi.gemm_dev(fmt, m, n, k, A.data_ptr(), Q.data_ptr(), C.data_ptr(), scales_ptr=S.data_ptr())
+                torch.cuda.synchronize()
+                err = rel_err(C.cpu().numpy(), ref)
+                print(f"{fmt} {k}x{n} M={m} {path}: rel {err:.2e}", flush=True)
+                assert err <= Q_TOL, (m, path, err)
+    finally:
+        _abi.prepared_free(h)

@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libtomoul_hip.so")
 SOURCES = ["runtime.hip", "gemm_mfma.hip", "gemm_dma.hip", "gemm_qbf.hip", "gemv.hip", "gemv_t.hip", "gemv_tm.hip", "quantize.hip", "tl.hip",
-           "stream_read.hip"]
+           "stream_read.hip", "gemv_x.hip"]
 ARCH = os.environ.get("TML_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops off: hipcc may otherwise emit v_pk_* fp32 instructions

@@ -211,6 +211,14 @@ bool gemv_tm_m1_preferred(int fmt, int64_t N, int64_t K);
 Status launch_gemv_tm(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
                       const float *bias, const float *res, float *C, float alpha_eff, float beta, int act,
                       long long tail0, const float *colscale, hipStream_t s);
+// Staged-activation decoder GEMV on a prepared Q8_0 / Q4_0 weight
+// (gemv_x.hip): M = 1 or 2, K a whole number of chunks; preferred below
+// vocabulary-sized N.
+bool gemv_x_capable(int fmt, int64_t M, int64_t N, int64_t K);
+bool gemv_x_preferred(int fmt, int64_t M, int64_t N, int64_t K);
+Status launch_gemv_x(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
+                     const float *bias, const float *res, float *C, float alpha_eff, float beta, int act,
+                     long long tail0, const float *colscale, hipStream_t s);
 // Bytes of one row of K elements of fmt in the reference's packing (Q4_0:
 // two per byte), before the 16-byte padding of a prepared row.
 inline int64_t packed_row_bytes(int fmt, int64_t K) {
