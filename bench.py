@@ -865,7 +865,10 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
     projections (1280 x 51866, M = 1) on 3 / 4 prepared copies and on the
     same copies in the [K,N] layout, and the f32 one on the token embedding
     used in place (rows-prepared) and on its transpose in the [K,N] layout
-    (the reference's own per-step call), 3 copies each."""
+    (the reference's own per-step call), 3 copies each.  At M = 1 each
+    layer shape also runs the read floor (tml_hip_stream_read_dev, two 16-byte
+    loads a lane) over the same 16 copies, and Q4_0 the per-lane VALU kernel
+    (TML_GEMVX=0) that the staged-activation kernel replaced, for comparison."""
     for fmt, K, N, M in ((_abi.FMT_Q8_0, 1024, 4096, 1), (_abi.FMT_Q8_0, 1024, 4096, 4),
                          (_abi.FMT_Q8_0, 1024, 4096, 8),
                          (_abi.FMT_Q4_0, 1280, 5120, 1), (_abi.FMT_Q4_0, 1280, 5120, 4),
@@ -888,10 +891,21 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
         for i in range(launches):
             _abi.gemm_dev(fmt, M, N, K, x.data_ptr(), copies[i % 16].data_ptr(), y.data_ptr(), scale=scale,
                           stream=sptr)
+        if M == 1:
+            floor_out = torch.empty(nbytes // 4096 + 2, dtype=torch.float32, device=dev)
+            for i in range(launches):
+                _abi.stream_read_dev(copies[i % 16].data_ptr(), nbytes, 2, floor_out.data_ptr(), sptr)
+            if fmt == _abi.FMT_Q4_0:
+                os.environ["TML_GEMVX"] = "0"
+                try:
+                    for i in range(launches):
+                        _abi.gemm_prepared(hs[i % 16], M, x.data_ptr(), y.data_ptr(), stream=sptr)
+                finally:
+                    os.environ.pop("TML_GEMVX", None)
         torch.cuda.synchronize()
         for h_ in hs:
             _abi.prepared_free(h_)
-        log(f"profile-gemv: fmt {fmt} {K}x{N}: {launches} prepared + {launches} [K,N] launches")
+        log(f"profile-gemv: fmt {fmt} {K}x{N} M={M}: {launches} prepared + {launches} [K,N] launches")
     # the vocabulary projection (1280 x 51866) at M = 1 on prepared copies
     for fmt, ncopy in ((_abi.FMT_Q8_0, 3), (_abi.FMT_Q4_0, 4)):
         K, N = 1280, 51866
