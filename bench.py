@@ -140,6 +140,7 @@ def encoder_weights(layers: int, workers: int):
         return out
     import multiprocessing as mp
     from multiprocessing import resource_tracker
+    import gc
     pool = mp.get_context("spawn").Pool(max(1, min(workers, layers)))
     try:
         out = pool.map(_layer_weights, range(layers))
@@ -147,7 +148,11 @@ def encoder_weights(layers: int, workers: int):
         pool.close()
         pool.join()
     # The spawn context started a resource-tracker process for the pool's
-    # locks; stop it now, so that no process of this run outlives it.
+    # locks.  Release the locks first (their finalizers unregister them with
+    # the tracker), then stop the tracker, so that no process of this run
+    # outlives it.
+    del pool
+    gc.collect()
     tracker = getattr(resource_tracker, "_resource_tracker", None)
     if tracker is not None and hasattr(tracker, "_stop"):
         tracker._stop()
@@ -815,18 +820,27 @@ def bench_sentence_transformer(torch, dev, sptr, timer, _abi, synth, tokens: int
     Q, K, V, O [384x384], FFN up [384x1536] and down [1536x384], each layer
     with its own weights, in fp32, F16 and Q8_K (the formats its .tl files
     carry; quantized / converted on the device by the reference's
-    quantizers).  One sweep = 6 layers x 6 GEMMs, 20 sweeps per graph replay."""
+    quantizers).  One sweep = 6 layers x 6 GEMMs, 20 sweeps per graph replay.
+    "<fmt>_fused_qkv": the same sweep with each layer's Q, K and V weights
+    concatenated along N at load into one [384 x 1152] weight (one GEMM
+    instead of three: exact, each N-slice is its own projection; for Q8_K the
+    32-element scale blocks of a 384-wide row stay whole), so 4 GEMMs a layer."""
     d, ff, M = 384, 1536, tokens
     shapes = [(d, d)] * 4 + [(d, ff), (ff, d)]
+    fused_shapes = [(d, 3 * d), (d, d), (d, ff), (ff, d)]
     flops = layers * sum(2.0 * M * K * N for (K, N) in shapes)
+    assert flops == layers * sum(2.0 * M * K * N for (K, N) in fused_shapes)
     x = torch.from_numpy(synth.normal_matrix(1001, M, d)).to(dev)
     h = torch.from_numpy(synth.normal_matrix(1002, M, ff)).to(dev)
     y = torch.empty((M, ff), dtype=torch.float32, device=dev)
     res = {}
-    for fmt, name in ((_abi.FMT_F32, "fp32"), (_abi.FMT_F16, "f16"), (_abi.FMT_Q8_K, "q8_k")):
+    for fmt, name, lshapes in ((_abi.FMT_F32, "fp32", shapes), (_abi.FMT_F16, "f16", shapes),
+                               (_abi.FMT_Q8_K, "q8_k", shapes), (_abi.FMT_F32, "fp32_fused_qkv", fused_shapes),
+                               (_abi.FMT_F16, "f16_fused_qkv", fused_shapes),
+                               (_abi.FMT_Q8_K, "q8_k_fused_qkv", fused_shapes)):
         keep, row = [], []
         for layer in range(layers):
-            for i, (K, N) in enumerate(shapes):
+            for i, (K, N) in enumerate(lshapes):
                 w = torch.from_numpy(synth.normal_matrix(2002 + 8 * layer + i, K, N, 0.02)).to(dev)
                 if fmt == _abi.FMT_F32:
                     keep.append(w)
