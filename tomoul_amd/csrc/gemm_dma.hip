@@ -620,7 +620,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                     if (a.res) v += rv[q];
                     out[q] = tml_apply_act(v, a.act, (long long)o + q, a.tail0);
                 }
-                *(floatx4 *)(a.C + o) = out;
+                tml_store_c(a.C + o, out);
             }
             return;
         }
@@ -645,7 +645,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                     if (a.bias) v += biasc;
                     const long long flat = (long long)row * a.N + col;
                     if (a.res) v += a.res[flat];
-                    *cp = tml_apply_act(v, a.act, flat, a.tail0);
+                    tml_store_c(cp, tml_apply_act(v, a.act, flat, a.tail0));
                 }
             }
         }
@@ -673,7 +673,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
             if (act != TML_ACT_NONE)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) v[r] = tml_apply_act(v[r], act, 4 * q + r, tail0);
-            *(floatx4 *)cp = v;
+            tml_store_c(cp, v);
         }
     } else {
         for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < mn; e += stride) {
@@ -683,7 +683,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
             if (beta != 0.0f) v += beta * C[e];
             if (bias) v += bias[e % n];
             if (res) v += res[e];
-            C[e] = tml_apply_act(v, act, e, tail0);
+            tml_store_c(C + e, tml_apply_act(v, act, e, tail0));
         }
     }
 }

@@ -391,7 +391,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_mfma_kernel(GemmKArgs a) {
                     if (a.bias) v += bcol;
                     const long long flat = (long long)row * a.N + col;
                     if (a.res) v += a.res[flat];
-                    *cp = tml_apply_act(v, a.act, flat, a.tail0);
+                    tml_store_c(cp, tml_apply_act(v, a.act, flat, a.tail0));
                 }
             }
         }

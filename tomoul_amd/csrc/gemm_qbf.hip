@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
                     if (a.beta != 0.0f) v += a.beta * a.C[flat];
                     if (a.bias) v += biasc;
                     if (a.res) v += a.res[flat];
-                    a.C[flat] = tml_apply_act(v, a.act, flat, a.tail0);
+                    tml_store_c(a.C + flat, tml_apply_act(v, a.act, flat, a.tail0));
                 }
             }
     }

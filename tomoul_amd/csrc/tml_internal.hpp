@@ -102,6 +102,18 @@ __device__ __forceinline__ float tml_apply_act(float v, int act, long long flat,
 }
 __host__ __device__ __forceinline__ long long tml_act_tail0(long long mn) { return mn - mn % 8; }
 
+// Final C stores of the GEMM epilogues (a float or a 16-byte vector of them
+// at p) are non-temporal: no workgroup of the launch reads C back, so the
+// lines stream out to memory while other tiles still compute, instead of
+// sitting dirty in the XCD's L2 until the end-of-kernel release writes them
+// back in one burst.  Measured on MI355X: 1500x1536x384 with bias 20.5 ->
+// 19.5 us, 512x1024x1024 15.5 -> 14.5 us, Q8_0 512x4096x1024 22.5 -> 21.7
+// us, the long-K shapes unchanged.
+template <typename T>
+__device__ __forceinline__ void tml_store_c(float *p, T v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<T *>(p));
+}
+
 // Kernels load out-of-range chunks from this zeroed block instead of
 // branching around the load: the selected address keeps the load
 // unconditional, which lets the compiler keep whole batches of global loads
