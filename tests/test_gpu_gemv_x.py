@@ -3,7 +3,7 @@
 dequantize-then-f32-accumulate loops, quantization.zig:158-203 and
 :778-824).  TML_GEMVX=3 makes every such call refuse any other kernel, so
 each case proves that this one ran.  Covered: the decoder shapes of configs 3
-and 4, rows ragged against the kernel's layers (N not a multiple of its rows
+and 4, the Whisper vocabulary projection (1280 x 51866), rows ragged against the kernel's layers (N not a multiple of its rows
 per workgroup), long rows (384 / 224 chunks, activations near the 64 KiB of
 LDS the kernel may use at M = 2) and the shortest (one chunk), both
 thread counts and every layer count, the fused epilogue (bias, alpha / beta,
@@ -77,7 +77,8 @@ def _run(h, m, n, a, **kw):
 
 SHAPES = [(_abi.FMT_Q8_0, 1024, 4096), (_abi.FMT_Q4_0, 1280, 5120), (_abi.FMT_Q4_0, 5120, 1280),
           (_abi.FMT_Q8_0, 1280, 5120), (_abi.FMT_Q8_0, 6144, 300), (_abi.FMT_Q4_0, 7168, 37),
-          (_abi.FMT_Q8_0, 16, 1001), (_abi.FMT_Q4_0, 32, 7), (_abi.FMT_Q4_0, 224, 1000), (_abi.FMT_Q8_0, 2560, 2049)]
+          (_abi.FMT_Q8_0, 16, 1001), (_abi.FMT_Q4_0, 32, 7), (_abi.FMT_Q4_0, 224, 1000), (_abi.FMT_Q8_0, 2560, 2049),
+          (_abi.FMT_Q8_0, 1280, 51866), (_abi.FMT_Q4_0, 1280, 51866)]
 
 
 @pytest.mark.parametrize("fmt,k,n", SHAPES, ids=[f"{'q8' if f == 1 else 'q4'}_{k}x{n}" for f, k, n in SHAPES])

@@ -771,20 +771,30 @@ def test_prepared_row_parts_bitwise(orc, m):
             os.environ["TML_GEMVTM_MSPLIT"] = saved
 
 
-def test_prepared_matrix_core_vocabulary(orc):
-    # Q8_0 and Q4_0 at M = 1 on a vocabulary-sized N take the matrix-core
-    # kernel by default (eight or more workgroups a CU; Q8_0 with two rounds
-    # in flight, K = 1280 giving it two rounds); on a layer-sized N they stay
-    # on the VALU kernels.
-    for (k, n) in ((256, 33000), (1280, 33000), (256, 5000)):
-        w = rnd(231, k, n, 0.02)
-        q, s = orc.quantize_q8(w)
-        p, s4 = orc.quantize_q4(w)
-        a = rnd(232, 1, k)
-        for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
-                                   (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
-            got = _run_prepared(fmt, b, scale, k, n, 1, a)
-            assert rel_err(got, ref) <= 2e-5, (n, fmt)
+@pytest.mark.parametrize("gemvx", ["0", "1"])
+def test_prepared_matrix_core_vocabulary(orc, gemvx):
+    # Q8_0 and Q4_0 at M = 1 on a vocabulary-sized N: with the staged-activation
+    # kernel off (TML_GEMVX=0) they take the matrix-core kernel (eight or more
+    # workgroups a CU; Q8_0 with two rounds in flight, K = 1280 giving it two
+    # rounds), by default the staged-activation kernel; on a layer-sized N
+    # Q8_0 stays on the VALU kernel.
+    saved = os.environ.get("TML_GEMVX")
+    os.environ["TML_GEMVX"] = gemvx
+    try:
+        for (k, n) in ((256, 33000), (1280, 33000), (256, 5000)):
+            w = rnd(231, k, n, 0.02)
+            q, s = orc.quantize_q8(w)
+            p, s4 = orc.quantize_q4(w)
+            a = rnd(232, 1, k)
+            for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
+                                       (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
+                got = _run_prepared(fmt, b, scale, k, n, 1, a)
+                assert rel_err(got, ref) <= 2e-5, (n, fmt)
+    finally:
+        if saved is None:
+            os.environ.pop("TML_GEMVX", None)
+        else:
+            os.environ["TML_GEMVX"] = saved
 
 
 @pytest.mark.parametrize("m", [3, 8])

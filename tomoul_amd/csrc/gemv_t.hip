@@ -65,10 +65,11 @@ struct GemvTArgs {
 // 16 bytes at base + off of a buffer of nbytes, through a buffer resource:
 // offsets at or past nbytes read zeros.  The resource is built from uniform
 // values (SGPRs); the lane's offset is one 32-bit VGPR.
+template <int POLICY = 0>
 __device__ __forceinline__ uintx4 buf_load16(const void *base, unsigned nbytes, unsigned off) {
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)nbytes, 0x00020000);
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POLICY);
 }
 
 // How gemv_t_kernel loads its activations:
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
                 const bool in = base + lk < a.nchunk;
 #pragma unroll
                 for (int c = 0; c < CW; ++c)
-                    w[c][j] = buf_load16(a.Bt, a.wbytes, in ? wlane[c] + 16u * (unsigned)base : 0x80000000u);
+                    w[c][j] = buf_load16<kStreamLoadPolicy>(a.Bt, a.wbytes, in ? wlane[c] + 16u * (unsigned)base : 0x80000000u);
                 const int wb = base + (LK > 64 ? 64 * wave_u : 0);  // first chunk of the wave
                 const int sc = wb >> 6;
                 const int width = min(64, a.nchunk - (sc << 6));
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t_kernel(GemvTArgs a) {
                 const int n = n0 + c;
                 const bool in = ch < a.nchunk && n < a.N;
                 const uint8_t *p = in ? a.Bt + (size_t)n * a.ldt + (size_t)ch * 16 : (const uint8_t *)a.zero;
-                w[c][j] = *(const uintx4 *)p;
+                w[c][j] = __builtin_nontemporal_load((const uintx4 *)p);
             }
 #pragma unroll
         for (int j = 0; j < JB; ++j) {
@@ -409,7 +410,8 @@ __global__ __launch_bounds__(kThreads) void gemv_tl_kernel(GemvTArgs a) {
         for (int c = 0; c < CW; ++c) {
             const int n = n0 + c;
             const bool ok = ch < a.nchunk && n < a.N;
-            dst[c] = *(const uintx4 *)(ok ? a.Bt + (size_t)n * a.ldt + (size_t)ch * 16 : (const uint8_t *)a.zero);
+            dst[c] = __builtin_nontemporal_load(
+                (const uintx4 *)(ok ? a.Bt + (size_t)n * a.ldt + (size_t)ch * 16 : (const uint8_t *)a.zero));
         }
     };
     float acc[V];
@@ -677,7 +679,7 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
     if (ldt < prepared_row_bytes(fmt, K) || ldt % 16 != 0 || ((uintptr_t)Bt % 16) != 0)
         return Status::Err(TML_ERR_INVALID_ARG, "prepared weight layout");
     // Q8_0 / Q4_0 at M <= 2 with the activations staged per workgroup
-    // (gemv_x.hip) below vocabulary-sized N.
+    // (gemv_x.hip) where gemv_x_preferred finds it the faster kernel.
     if (gemv_x_preferred(fmt, M, N, K) && ((uintptr_t)A % 16) == 0)
         return launch_gemv_x(fmt, M, N, K, A, Bt, ldt, bias, res, C, alpha_eff, beta, act, tail0, colscale, s);
     if (M <= 2 && env_int("TML_GEMVX", 1) == 3)

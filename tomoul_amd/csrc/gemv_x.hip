@@ -154,7 +154,7 @@ __global__ __launch_bounds__(NT) void gemv_x_kernel(GemvXArgs a) {
             const int n = row0 + p * L + rl;
             const bool ok = rl < L && n < a.N;
             const unsigned off = ok ? (unsigned)n * a.ldt + 16u * (unsigned)c : 0x80000000u;
-            w[p] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+            w[p] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kStreamLoadPolicy);
         }
     }
     // 3. Every wave's activation copies done (the P weight loads may still
@@ -309,20 +309,29 @@ bool gemv_x_capable(int fmt, int64_t M, int64_t N, int64_t K) {
 }
 
 // Where it is the faster kernel (measured on MI355X against the kernels of
-// gemv_t.hip / gemv_tm.hip, us): Q4_0 at M = 1 (1280x5120 3.60 against
-// 3.83, 5120x1280 3.73 against 4.02) and at M = 2 on rows of more than 64
-// chunks (5120x1280 4.29 against 5.33; 1280x5120 4.37 against 4.04 on the
-// matrix cores).  Q8_0 keeps the per-lane kernel (1024x4096 M = 1 3.15
-// against 3.37, M = 2 3.50 against 3.58), vocabulary-sized N the matrix
-// cores.  TML_GEMVX=0 turns it off; TML_GEMVX=2 takes it wherever it can
-// run, and TML_GEMVX=3 also makes the prepared GEMV refuse an M <= 2 call
-// it cannot take (tests).
+// gemv_t.hip / gemv_tm.hip, every launch reading its own weight copy out of
+// >= 1 GiB, weights streamed with the non-temporal policy, us):
+//   * Q4_0 at M = 1 at every N (1280x5120 3.27 against 3.48, 5120x1280 3.42
+//     against 3.70, vocabulary 1280x51866 10.27 against 10.82 on the matrix
+//     cores, 2048x51866 13.66 against 15.34), and at M = 2 on rows of more
+//     than 64 chunks below N = 32768 (5120x1280 4.29 against 5.33, before
+//     the non-temporal policy); short rows at M = 2 stay on the matrix cores
+//     (1280x51866 14.16 against 11.03; 1280x5120 4.37 against 4.04 before
+//     the policy);
+//   * Q8_0 from N = 12288 at M = 1 (1024x12288 4.49 against 5.05, vocabulary
+//     1280x51866 13.22 against 13.94; below it the per-lane kernel: 1024x4096
+//     2.85 against 3.08, 1024x8192 3.65 against 3.79) and from N = 8192 at
+//     M = 2 (1024x8192 4.17 against 4.70, 1280x51866 16.46 against 19.30;
+//     1024x4096 3.17 against 3.31 on the per-lane kernel).
+// TML_GEMVX=0 turns it off; TML_GEMVX=2 takes it wherever it can run, and
+// TML_GEMVX=3 also makes the prepared GEMV refuse an M <= 2 call it cannot
+// take (tests).
 bool gemv_x_preferred(int fmt, int64_t M, int64_t N, int64_t K) {
     const int mode = env_int("TML_GEMVX", 1);
     if (mode == 0 || !gemv_x_capable(fmt, M, N, K)) return false;
     if (mode >= 2) return true;
-    if (fmt != TML_FMT_Q4_0 || N >= 32768) return false;
-    return M == 1 || K / 32 > 64;
+    if (fmt == TML_FMT_Q4_0) return M == 1 || (N < 32768 && K / 32 > 64);
+    return N >= (M == 1 ? 12288 : 8192);
 }
 
 Status launch_gemv_x(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,

@@ -8,7 +8,8 @@
 // hardware allows -- every lane issues all of its U loads back to back,
 // each wave-wide load instruction covers 1 KiB of contiguous bytes, loads
 // go through a buffer resource (offsets past the end read zeros, no
-// branches) -- then one integer fold of what was read, a reduction over the
+// branches) with the non-temporal cache policy (kStreamLoadPolicy, which
+// read 4 MB in 2.65 against 2.90 us with the default policy) -- then one integer fold of what was read, a reduction over the
 // workgroup and one 4-byte store per workgroup, so that nothing of the read
 // can be dropped by the compiler.  A GEMV that streams the same bytes
 // cannot take less time than this, and its ratio to it is the figure the
@@ -30,7 +31,8 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(const void *src, 
     const unsigned base = (unsigned)blockIdx.x * (unsigned)(U * kThreads * 16) + threadIdx.x * 16u;
     uintx4 v[U];
 #pragma unroll
-    for (int j = 0; j < U; ++j) v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, base + (unsigned)j * (kThreads * 16u), 0, 0);
+    for (int j = 0; j < U; ++j)
+        v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, base + (unsigned)j * (kThreads * 16u), 0, kStreamLoadPolicy);
     unsigned acc = 0;
 #pragma unroll
     for (int j = 0; j < U; ++j) acc += (v[j].x ^ v[j].y) + (v[j].z ^ v[j].w);

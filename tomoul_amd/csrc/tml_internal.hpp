@@ -114,6 +114,21 @@ __device__ __forceinline__ void tml_store_c(float *p, T v) {
     __builtin_nontemporal_store(v, reinterpret_cast<T *>(p));
 }
 
+// Cache-policy operand of the buffer loads that stream a decoder GEMV's
+// weights (each byte read once per launch): the non-temporal bit (NT, bit 1
+// of the gfx940-family cache-policy field); plain-pointer loads get the same
+// policy from __builtin_nontemporal_load.  Used only where one load
+// instruction covers whole 128-byte lines: the prepared-layout kernels
+// (gemv_t.hip, gemv_x.hip) and the read floor (stream_read.hip).  The
+// activations, which every workgroup re-reads, keep the default policy, and
+// so do kernels whose lanes read parts of a line that later loads complete
+// (gemv_tm.hip's 64-byte row pieces, gemv.hip's ragged rows): there it
+// measured slower, up to 19.4 -> 22.8 us for the Q8_0 vocabulary on [K,N].
+// Measured on MI355X with every launch reading its own copy out of >= 1
+// GiB: the plain 4 MB read 2.90 -> 2.65 us; M = 1 Q8_0 1024x4096 3.17 ->
+// 2.83 us, Q4_0 1280x5120 3.60 -> 3.27 us, 5120x1280 3.73 -> 3.48 us.
+constexpr int kStreamLoadPolicy = 2;
+
 // Kernels load out-of-range chunks from this zeroed block instead of
 // branching around the load: the selected address keeps the load
 // unconditional, which lets the compiler keep whole batches of global loads
