@@ -874,15 +874,31 @@ def bench_sentence_transformer(torch, dev, sptr, timer, _abi, synth, tokens: int
 def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
     """Decoder GEMVs for kernel traces / counters: Q8_0 1024x4096 and Q4_0
     1280x5120 and 5120x1280 at M = 1, 4 and 8, each on its prepared copy and
-    in the [K,N] layout, `launches` times over 16 distinct weight copies
-    (eager launches, one kernel per call); then the Q8_0 and Q4_0 vocabulary
-    projections (1280 x 51866, M = 1) on 3 / 4 prepared copies and on the
-    same copies in the [K,N] layout, and the f32 one on the token embedding
-    used in place (rows-prepared) and on its transpose in the [K,N] layout
-    (the reference's own per-step call), 3 copies each.  At M = 1 each
-    layer shape also runs the read floor (tml_hip_stream_read_dev, two 16-byte
-    loads a lane) over the same 16 copies, and Q4_0 the per-lane VALU kernel
-    (TML_GEMVX=0) that the staged-activation kernel replaced, for comparison."""
+    in the [K,N] layout, `launches` times over 16 distinct weight copies;
+    then the Q8_0 and Q4_0 vocabulary projections (1280 x 51866, M = 1) on
+    3 / 4 prepared copies and on the same copies in the [K,N] layout, and the
+    f32 one on the token embedding used in place (rows-prepared) and on its
+    transpose in the [K,N] layout (the reference's own per-step call), 3
+    copies each.  At M = 1 each layer shape also runs the read floor
+    (tml_hip_stream_read_dev, two 16-byte loads a lane) over the same 16
+    copies, and Q4_0 the per-lane VALU kernel (TML_GEMVX=0) that the
+    staged-activation kernel replaced, for comparison.  Each batch is one
+    eager launch (workspaces), then its `launches` launches captured in a HIP
+    graph and replayed once, back to back as the benchmark's timings run
+    them: a trace shows each batch as a run of launches + 1 dispatches whose
+    first is the eager one."""
+    def batch(launch):
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            launch(side.cuda_stream, 1)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            launch(side.cuda_stream, launches)
+        g.replay()
+        torch.cuda.synchronize()
+        del g
+
     for fmt, K, N, M in ((_abi.FMT_Q8_0, 1024, 4096, 1), (_abi.FMT_Q8_0, 1024, 4096, 4),
                          (_abi.FMT_Q8_0, 1024, 4096, 8),
                          (_abi.FMT_Q4_0, 1280, 5120, 1), (_abi.FMT_Q4_0, 1280, 5120, 4),
@@ -900,20 +916,19 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
         hs = [_abi.prepare_dev(fmt, K, N, copies[i].data_ptr(), scale, sptr) for i in range(16)]
         x = torch.from_numpy(synth.normal_matrix(1001, M, K)).to(dev)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
-        for i in range(launches):
-            _abi.gemm_prepared(hs[i % 16], M, x.data_ptr(), y.data_ptr(), stream=sptr)
-        for i in range(launches):
-            _abi.gemm_dev(fmt, M, N, K, x.data_ptr(), copies[i % 16].data_ptr(), y.data_ptr(), scale=scale,
-                          stream=sptr)
+        batch(lambda st, n: [_abi.gemm_prepared(hs[i % 16], M, x.data_ptr(), y.data_ptr(), stream=st)
+                             for i in range(n)])
+        batch(lambda st, n: [_abi.gemm_dev(fmt, M, N, K, x.data_ptr(), copies[i % 16].data_ptr(), y.data_ptr(),
+                                           scale=scale, stream=st) for i in range(n)])
         if M == 1:
             floor_out = torch.empty(nbytes // 4096 + 2, dtype=torch.float32, device=dev)
-            for i in range(launches):
-                _abi.stream_read_dev(copies[i % 16].data_ptr(), nbytes, 2, floor_out.data_ptr(), sptr)
+            batch(lambda st, n: [_abi.stream_read_dev(copies[i % 16].data_ptr(), nbytes, 2, floor_out.data_ptr(), st)
+                                 for i in range(n)])
             if fmt == _abi.FMT_Q4_0:
                 os.environ["TML_GEMVX"] = "0"
                 try:
-                    for i in range(launches):
-                        _abi.gemm_prepared(hs[i % 16], M, x.data_ptr(), y.data_ptr(), stream=sptr)
+                    batch(lambda st, n: [_abi.gemm_prepared(hs[i % 16], M, x.data_ptr(), y.data_ptr(), stream=st)
+                                         for i in range(n)])
                 finally:
                     os.environ.pop("TML_GEMVX", None)
         torch.cuda.synchronize()
@@ -931,14 +946,14 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
         torch.cuda.synchronize()
         copies = q.repeat(ncopy).view(ncopy, nbytes)
         del w
-        hs = [_abi.prepare_dev(fmt, K, N, copies[i].data_ptr(), float(sc.item()), sptr) for i in range(ncopy)]
+        scale = float(sc.item())
+        hs = [_abi.prepare_dev(fmt, K, N, copies[i].data_ptr(), scale, sptr) for i in range(ncopy)]
         x = torch.from_numpy(synth.normal_matrix(1001, 1, K)).to(dev)
         y = torch.empty((1, N), dtype=torch.float32, device=dev)
-        for i in range(launches):
-            _abi.gemm_prepared(hs[i % ncopy], 1, x.data_ptr(), y.data_ptr(), stream=sptr)
-        for i in range(launches):
-            _abi.gemm_dev(fmt, 1, N, K, x.data_ptr(), copies[i % ncopy].data_ptr(), y.data_ptr(),
-                          scale=float(sc.item()), stream=sptr)
+        batch(lambda st, n: [_abi.gemm_prepared(hs[i % ncopy], 1, x.data_ptr(), y.data_ptr(), stream=st)
+                             for i in range(n)])
+        batch(lambda st, n: [_abi.gemm_dev(fmt, 1, N, K, x.data_ptr(), copies[i % ncopy].data_ptr(), y.data_ptr(),
+                                           scale=scale, stream=st) for i in range(n)])
         torch.cuda.synchronize()
         for h_ in hs:
             _abi.prepared_free(h_)
@@ -954,10 +969,10 @@ def profile_gemv(torch, dev, sptr, _abi, synth, launches: int = 50):
     hs = [_abi.prepare_rows_dev(_abi.FMT_F32, K, N, copies[i].data_ptr(), 4 * K, 1.0, sptr) for i in range(ncopy)]
     x = torch.from_numpy(synth.normal_matrix(1001, 1, K)).to(dev)
     y = torch.empty((1, N), dtype=torch.float32, device=dev)
-    for i in range(launches):
-        _abi.gemm_prepared(hs[i % ncopy], 1, x.data_ptr(), y.data_ptr(), stream=sptr)
-    for i in range(launches):
-        _abi.gemm_dev(_abi.FMT_F32, 1, N, K, x.data_ptr(), copies_t[i % ncopy].data_ptr(), y.data_ptr(), stream=sptr)
+    batch(lambda st, n: [_abi.gemm_prepared(hs[i % ncopy], 1, x.data_ptr(), y.data_ptr(), stream=st)
+                         for i in range(n)])
+    batch(lambda st, n: [_abi.gemm_dev(_abi.FMT_F32, 1, N, K, x.data_ptr(), copies_t[i % ncopy].data_ptr(),
+                                       y.data_ptr(), stream=st) for i in range(n)])
     torch.cuda.synchronize()
     for h_ in hs:
         _abi.prepared_free(h_)
