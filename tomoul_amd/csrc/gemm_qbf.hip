@@ -36,6 +36,7 @@
 #include "tml_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace tml {
 namespace {
@@ -106,11 +107,19 @@ __device__ __forceinline__ int qbf_slot(int r, int s) {
     else return r * 8 + (s ^ ((r >> 1) & 7));
 }
 
-template <int FMT, int BM, int BN, int WM, int WN, int D, int BK = 32>
-__global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
+// KW = 2: eight waves in two groups.  Group 0 (waves 0-3) stages A and
+// multiplies the first 32-k half of every 64-deep slice, group 1 (waves 4-7)
+// stages B and multiplies the second half, each wave of a group on its own
+// WM x WN sub-tile; group 1 hands its accumulators to group 0 through LDS
+// after the main loop, and group 0 runs the epilogue.  Each wave then does
+// half the staging and half the MFMAs of a step, and two waves share each
+// SIMD, so one's waits are covered by the other's work.
+template <int FMT, int BM, int BN, int WM, int WN, int D, int BK = 32, int KW = 1>
+__global__ __launch_bounds__(256 * KW) void gemm_qbf_kernel(QbfArgs a) {
     static_assert(BK == 32 || BK == 64, "32- or 64-deep slices");
+    static_assert(KW == 1 || (KW == 2 && BK == 64), "two wave groups split 64-deep slices into 32-k halves");
     constexpr int SL = BK / 8;  // 16-byte slots (8 k) of an LDS row
-    constexpr int NT = 256;
+    constexpr int NT = 256;     // staging threads of an operand (all 256 take both when KW = 1)
     constexpr int TM = WM / 16, TN = WN / 16;
     constexpr int WAVES_N = BN / WN;
     static_assert((BM / WM) * (BN / WN) == 4, "four waves, one per WM x WN sub-tile");
@@ -123,9 +132,11 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
 
     __shared__ uintx4 Ah[2][BM * SL], Al[2][BM * SL], Bs[2][BN * SL];
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
+    const int tid = threadIdx.x % NT, lane = tid & 63;  // tid: the thread's index in its group
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int kg = KW == 2 ? wave / 4 : 0;  // wave group
+    const int sw = wave % 4;               // sub-tile of the wave
+    const int wm0 = (sw / WAVES_N) * WM, wn0 = (sw % WAVES_N) * WN;
     const int c = lane & 15, g = lane >> 4;
 
     // Workgroup -> (tile, K split): consecutive ids within each XCD (own
@@ -162,68 +173,79 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
     // loads and skip its store.  k0 counts from kbase.
     uintx4 ra[D][PA][2];
     uint32_t rb[D][PB][8];
-    auto load = [&](int d, int k0) __attribute__((always_inline)) {
+    auto load = [&](auto opa, auto opb, int d, int k0) __attribute__((always_inline)) {
+        if constexpr (decltype(opa)::value) {
 #pragma unroll
-        for (int p = 0; p < PA; ++p) {
-            const int j = (tid + p * NT) % TA;
-            const int row = j / SL, k = kbase + k0 + 8 * (j % SL);
-            const unsigned past_k = (unsigned)(kend - 1 - k) & 0x80000000u;
-            const unsigned off = (((unsigned)(m0 + row) * (unsigned)a.K + (unsigned)k) * 4u) | past_k;
-            ra[d][p][0] = qbf_load16(a.A, a.a_bytes, off);
-            ra[d][p][1] = qbf_load16(a.A, a.a_bytes, off + 16u);
+            for (int p = 0; p < PA; ++p) {
+                const int j = (tid + p * NT) % TA;
+                const int row = j / SL, k = kbase + k0 + 8 * (j % SL);
+                const unsigned past_k = (unsigned)(kend - 1 - k) & 0x80000000u;
+                const unsigned off = (((unsigned)(m0 + row) * (unsigned)a.K + (unsigned)k) * 4u) | past_k;
+                ra[d][p][0] = qbf_load16(a.A, a.a_bytes, off);
+                ra[d][p][1] = qbf_load16(a.A, a.a_bytes, off + 16u);
+            }
         }
+        if constexpr (decltype(opb)::value) {
 #pragma unroll
-        for (int p = 0; p < PB; ++p) {
-            const int j = (tid + p * NT) % TB;
-            const int cp = j % (BN / 2), s = j / (BN / 2);
-            const unsigned col_byte = FMT == TML_FMT_Q8_0 ? (unsigned)(n0 + 2 * cp) : (unsigned)((n0 + 2 * cp) / 2);
-            const unsigned off0 = (unsigned)(kbase + k0 + 8 * s) * (unsigned)a.ldb + col_byte;
+            for (int p = 0; p < PB; ++p) {
+                const int j = (tid + p * NT) % TB;
+                const int cp = j % (BN / 2), s = j / (BN / 2);
+                const unsigned col_byte =
+                    FMT == TML_FMT_Q8_0 ? (unsigned)(n0 + 2 * cp) : (unsigned)((n0 + 2 * cp) / 2);
+                const unsigned off0 = (unsigned)(kbase + k0 + 8 * s) * (unsigned)a.ldb + col_byte;
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const unsigned off = off0 + (unsigned)kk * (unsigned)a.ldb;
-                rb[d][p][kk] = FMT == TML_FMT_Q8_0 ? qbf_load2(a.B, a.b_bytes, off) : qbf_load1(a.B, a.b_bytes, off);
+                for (int kk = 0; kk < 8; ++kk) {
+                    const unsigned off = off0 + (unsigned)kk * (unsigned)a.ldb;
+                    rb[d][p][kk] =
+                        FMT == TML_FMT_Q8_0 ? qbf_load2(a.B, a.b_bytes, off) : qbf_load1(a.B, a.b_bytes, off);
+                }
             }
         }
     };
-    auto store = [&](int d, int st) __attribute__((always_inline)) {
+    auto store = [&](auto opa, auto opb, int d, int st) __attribute__((always_inline)) {
+        if constexpr (decltype(opa)::value) {
 #pragma unroll
-        for (int p = 0; p < PA; ++p) {
-            const int j = tid + p * NT;
-            if (TA % NT == 0 || j < TA) {
-                const int row = j / SL, s = j % SL;
-                const floatx4 x0 = __builtin_bit_cast(floatx4, ra[d][p][0]), x1 = __builtin_bit_cast(floatx4, ra[d][p][1]);
-                uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
-                qbf_split(x0[0], x0[1], h0, l0);
-                qbf_split(x0[2], x0[3], h1, l1);
-                qbf_split(x1[0], x1[1], h2, l2);
-                qbf_split(x1[2], x1[3], h3, l3);
-                Ah[st][qbf_slot<SL>(row, s)] = (uintx4){h0, h1, h2, h3};
-                Al[st][qbf_slot<SL>(row, s)] = (uintx4){l0, l1, l2, l3};
+            for (int p = 0; p < PA; ++p) {
+                const int j = tid + p * NT;
+                if (TA % NT == 0 || j < TA) {
+                    const int row = j / SL, s = j % SL;
+                    const floatx4 x0 = __builtin_bit_cast(floatx4, ra[d][p][0]);
+                    const floatx4 x1 = __builtin_bit_cast(floatx4, ra[d][p][1]);
+                    uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+                    qbf_split(x0[0], x0[1], h0, l0);
+                    qbf_split(x0[2], x0[3], h1, l1);
+                    qbf_split(x1[0], x1[1], h2, l2);
+                    qbf_split(x1[2], x1[3], h3, l3);
+                    Ah[st][qbf_slot<SL>(row, s)] = (uintx4){h0, h1, h2, h3};
+                    Al[st][qbf_slot<SL>(row, s)] = (uintx4){l0, l1, l2, l3};
+                }
             }
         }
+        if constexpr (decltype(opb)::value) {
 #pragma unroll
-        for (int p = 0; p < PB; ++p) {
-            const int j = tid + p * NT;
-            if (TB % NT == 0 || j < TB) {
-                const int cp = j % (BN / 2), s = j / (BN / 2);
-                uintx4 e, o;  // columns 2 cp (even) and 2 cp + 1, k = 8 s .. 8 s + 7
+            for (int p = 0; p < PB; ++p) {
+                const int j = tid + p * NT;
+                if (TB % NT == 0 || j < TB) {
+                    const int cp = j % (BN / 2), s = j / (BN / 2);
+                    uintx4 e, o;  // columns 2 cp (even) and 2 cp + 1, k = 8 s .. 8 s + 7
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    uint32_t w0 = rb[d][p][2 * q], w1 = rb[d][p][2 * q + 1];
-                    // pin the words here: otherwise the compiler moves part of
-                    // the unpacking of a set loaded this step up to the step's
-                    // end, where it must wait for every load in flight
-                    __asm__ volatile("" : "+v"(w0), "+v"(w1));
-                    if constexpr (FMT == TML_FMT_Q8_0) {
-                        e[q] = qbf_pk((float)(int8_t)(w0 & 0xFFu), (float)(int8_t)(w1 & 0xFFu));
-                        o[q] = qbf_pk((float)(int8_t)(w0 >> 8), (float)(int8_t)(w1 >> 8));
-                    } else {
-                        e[q] = qbf_pk((float)((int32_t)(w0 << 28) >> 28), (float)((int32_t)(w1 << 28) >> 28));
-                        o[q] = qbf_pk((float)((int32_t)(w0 << 24) >> 28), (float)((int32_t)(w1 << 24) >> 28));
+                    for (int q = 0; q < 4; ++q) {
+                        uint32_t w0 = rb[d][p][2 * q], w1 = rb[d][p][2 * q + 1];
+                        // pin the words here: otherwise the compiler moves part of
+                        // the unpacking of a set loaded this step up to the step's
+                        // end, where it must wait for every load in flight
+                        __asm__ volatile("" : "+v"(w0), "+v"(w1));
+                        if constexpr (FMT == TML_FMT_Q8_0) {
+                            e[q] = qbf_pk((float)(int8_t)(w0 & 0xFFu), (float)(int8_t)(w1 & 0xFFu));
+                            o[q] = qbf_pk((float)(int8_t)(w0 >> 8), (float)(int8_t)(w1 >> 8));
+                        } else {
+                            e[q] = qbf_pk((float)((int32_t)(w0 << 28) >> 28), (float)((int32_t)(w1 << 28) >> 28));
+                            o[q] = qbf_pk((float)((int32_t)(w0 << 24) >> 28), (float)((int32_t)(w1 << 24) >> 28));
+                        }
                     }
+                    Bs[st][qbf_slot<SL>(2 * cp, s)] = e;
+                    Bs[st][qbf_slot<SL>(2 * cp + 1, s)] = o;
                 }
-                Bs[st][qbf_slot<SL>(2 * cp, s)] = e;
-                Bs[st][qbf_slot<SL>(2 * cp + 1, s)] = o;
             }
         }
     };
@@ -236,9 +258,11 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
     // One slice, 32 k at a time: lane (c, g) reads k = 32 h + 8 g .. + 7 of
     // A rows wm0 + 16 i + c (hi and lo) and of B columns wn0 + 16 j + c.  All
     // hi products first, then the lo ones, so no MFMA waits on the one before.
+    // With two wave groups, group kg takes the half h = kg.
     auto compute = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int h = 0; h < SL / 4; ++h) {
+        for (int hh = 0; hh < SL / 4 / KW; ++hh) {
+            const int h = KW == 2 ? kg : hh;
             bf16x8 ah[TM], al[TM], bv[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
@@ -270,23 +294,53 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
     // body is the same straight-line code with its LDS stage fixed.
     static_assert(D % 2 == 0, "LDS stage of step u is u % 2");
     const int nk = ((kend - kbase + BK - 1) / BK + D - 1) / D * D;
+    // The main loop for a wave that stages A (opa) and / or B (opb); both
+    // groups' loops hold the same barriers.
+    auto run = [&](auto opa, auto opb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) load(d, d * BK);
-    store(0, 0);
-    __syncthreads();
-    for (int kt0 = 0; kt0 < nk; kt0 += D) {
+        for (int d = 0; d < D; ++d) load(opa, opb, d, d * BK);
+        store(opa, opb, 0, 0);
+        __syncthreads();
+        for (int kt0 = 0; kt0 < nk; kt0 += D) {
 #pragma unroll
-        for (int u = 0; u < D; ++u) {
-            // the scheduler keeps the three phases in this order, so the
-            // loads of a set are always older than the D - 1 sets after it
-            load(u, (kt0 + u + D) * BK);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(u & 1);
-            __builtin_amdgcn_sched_barrier(0);
-            store((u + 1) % D, (u + 1) & 1);
-            __builtin_amdgcn_sched_barrier(0);
-            __syncthreads();
+            for (int u = 0; u < D; ++u) {
+                // the scheduler keeps the three phases in this order, so the
+                // loads of a set are always older than the D - 1 sets after it
+                load(opa, opb, u, (kt0 + u + D) * BK);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(u & 1);
+                __builtin_amdgcn_sched_barrier(0);
+                store(opa, opb, (u + 1) % D, (u + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+                __syncthreads();
+            }
         }
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    if constexpr (KW == 1) {
+        run(yes{}, yes{});
+    } else {
+        if (kg == 0) run(yes{}, no{});
+        else run(no{}, yes{});
+        // Group 1's accumulators to group 0 through A's hi stages, or B's
+        // where those are larger (free: the loop's last barrier follows every
+        // wave's last LDS read), in lane order per (wave, i, j).
+        constexpr bool XB = BN > BM;
+        static_assert(4 * TM * TN * 64 <= 2 * (XB ? BN : BM) * SL, "the exchange fits the stages it uses");
+        floatx4 *const xch = XB ? (floatx4 *)&Bs[0][0] : (floatx4 *)&Ah[0][0];
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) xch[((sw * TM + i) * TN + j) * 64 + lane] = acc[i][j];
+        }
+        __syncthreads();
+        if (kg == 1) return;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] += xch[((sw * TM + i) * TN + j) * 64 + lane];
     }
 
     // Epilogue: lane (c, g) holds rows 4 g + r, column c of each MFMA tile.
@@ -332,7 +386,7 @@ __global__ __launch_bounds__(256) void gemm_qbf_kernel(QbfArgs a) {
 }
 
 struct QbfCfg {
-    int bm, bn, bk;
+    int bm, bn, bk, kw;  // kw: wave groups (gemm_qbf_kernel's KW)
 };
 // Tile configs (index = TML_GEMM_QBF_TILE - 1): <BM, BN, BK> with four
 // waves of BM/2 x BN/2.  The two large tiles keep two 32-deep slices of loads
@@ -346,8 +400,18 @@ struct QbfCfg {
 // 128x4096x1024 12.6 against 16.4 us, 128x1280x5120 19.4 against 30.4 us;
 // at M = 1500 it is slower than 64 x 128 x 32 (QKV 61.8 against 47.8 us:
 // 186 registers at 64 x 128 x 64 hold two workgroups a CU, and 32 x 64
-// tiles re-read A and B twice as often).
-constexpr QbfCfg kQbfCfgs[] = {{128, 128, 32}, {64, 128, 32}, {64, 64, 32}, {32, 64, 32}, {64, 64, 64}, {32, 64, 64}};
+// tiles re-read A and B twice as often).  Configs 6 and 7 are the two
+// 64-deep tiles with two wave groups (KW = 2, eight waves; 80 / 64
+// registers): every M <= 512 shape measured faster with them (us, Q8_0,
+// every launch reading its own weight copy out of >= 1 GiB, one / two
+// groups): 128x4096x1024 12.28 / 11.13, 512x4096x1024 21.66 / 19.33,
+// 128x1280x5120 19.01 / 17.40, 256x4096x1024 14.74 / 13.56, 256x768x3072
+// 16.54 / 15.16, 384x1280x1280 13.98 / 13.40; Q4_0 128x4096x1024 12.28 /
+// 11.08, 512x4096x1024 21.46 / 19.37.  At M = 1500 they are slower than
+// 64 x 128 x 32 (QKV 54.0 against 46.5 us; a 64 x 128 x 64 two-group tile,
+// 130 registers, 55.8), so the large tiles keep one group.
+constexpr QbfCfg kQbfCfgs[] = {{128, 128, 32, 1}, {64, 128, 32, 1}, {64, 64, 32, 1}, {32, 64, 32, 1},
+                               {64, 64, 64, 1},   {32, 64, 64, 1},  {64, 64, 64, 2}, {32, 64, 64, 2}};
 constexpr int kQbfNumCfgs = (int)(sizeof(kQbfCfgs) / sizeof(kQbfCfgs[0]));
 
 template <int FMT>
@@ -358,7 +422,9 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
         case 2: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 4><<<grid, 256, 0, s>>>(a); break;
         case 3: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 4><<<grid, 256, 0, s>>>(a); break;
         case 4: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 2, 64><<<grid, 256, 0, s>>>(a); break;
-        default: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 2, 64><<<grid, 256, 0, s>>>(a); break;
+        case 5: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 2, 64><<<grid, 256, 0, s>>>(a); break;
+        case 6: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 2, 64, 2><<<grid, 512, 0, s>>>(a); break;
+        default: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 2, 64, 2><<<grid, 512, 0, s>>>(a); break;
     }
 }
 
@@ -367,7 +433,8 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
 // Tile and K split: forced by TML_GEMM_QBF_TILE / TML_GEMM_QBF_SPLIT, else
 //   * up to M = 512: 64x64x64 unsplit where those tiles give every CU two,
 //     else 32x64x64 where those tiles number at most four a CU, with the fewest
-//     K splits s in 1..4 that give every CU a unit (tile x split sweep,
+//     K splits s in 1..4 that give every CU a unit, both with two wave groups
+//     (the rule from a tile x split sweep of the one-group tiles,
 //     us, Q8_0, 32x64x64 at s = 1..4: 128x4096x1024 12.6 / 13.5 / 14.9 /
 //     15.6; 128x5120x1280 17.4 / 16.8 / 18.0 / 19.4; 128x1280x5120 42.7 /
 //     25.1 / 19.9 / 19.4; 192x4096x1024 15.3 / 15.9 / 19.4 / 19.0;
@@ -406,19 +473,21 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     };
     int cfg = 1;
     int64_t nsplit = 1;
-    if (m.M <= 512 && tiles_of(4) >= 2LL * cus) {
-        // 64 x 64 x 64 tiles, unsplit, where they give every CU two: half
-        // the A and B re-reads of 32 x 64 (512x4096x1024: 22.4 against 23.6 us)
-        cfg = 4;
-    } else if (m.M <= 512 && tiles_of(5) <= 4LL * cus) {
-        // 32 x 64 x 64 tiles with the fewest K splits that give every CU a
-        // unit (within 2 % of the best of a tile x split sweep on average:
-        // M = 128-512, N = 768-5120, K = 1024-5120; at M = 1500 its A and B
-        // re-reads cost more: 1500x1280x5120 82.9 against 61.3 us)
-        cfg = 5;
+    if (m.M <= 512 && tiles_of(6) >= 2LL * cus) {
+        // 64 x 64 x 64 tiles, two wave groups, unsplit, where they give every
+        // CU two: half the A and B re-reads of 32 x 64 (512x4096x1024, one
+        // group: 22.4 against 23.6 us)
+        cfg = 6;
+    } else if (m.M <= 512 && tiles_of(7) <= 4LL * cus) {
+        // 32 x 64 x 64 tiles, two wave groups, with the fewest K splits that
+        // give every CU a unit (one group: within 2 % of the best of a tile x
+        // split sweep on average, M = 128-512, N = 768-5120, K = 1024-5120;
+        // at M = 1500 its A and B re-reads cost more: 1500x1280x5120 82.9
+        // against 61.3 us)
+        cfg = 7;
         for (int64_t ns = 1; ns <= 4 && split_ok(ns); ++ns) {
             nsplit = ns;
-            if (tiles_of(5) * ns >= cus) break;
+            if (tiles_of(7) * ns >= cus) break;
         }
     } else if ((double)tiles_of(1) > 4.5 * cus) {
         cfg = 0;
