@@ -57,10 +57,10 @@ def _gemm(fmt, m, n, k, a, b, scale, scales, bias=None):
     return c
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 def test_qbf_tiles_vs_oracle(orc, env, tile):
     # Every tile config (0: the planner's choice; 5-8 on 64-deep slices, 7
-    # and 8 with two wave groups) on
+    # and 8 with two wave groups, 9 and 10 with eight waves) on
     # shapes ragged in M and N (partial tiles, N not a multiple of 16), K
     # from one slice to many and not a multiple of 64, with a bias.
     env["TML_GEMM_QBF"] = "2"
@@ -77,7 +77,7 @@ def test_qbf_tiles_vs_oracle(orc, env, tile):
 
 
 @pytest.mark.parametrize("split", [2, 3, 5])
-@pytest.mark.parametrize("tile", [1, 2, 4, 6, 7, 8])
+@pytest.mark.parametrize("tile", [1, 2, 4, 6, 7, 8, 9, 10])
 def test_qbf_split_vs_oracle(orc, env, tile, split):
     # K split over workgroups (each over its own range of 32-deep slices,
     # whole 64-deep ones for tiles 6-8, the last range short), raw partials

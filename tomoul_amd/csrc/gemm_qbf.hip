@@ -107,22 +107,25 @@ __device__ __forceinline__ int qbf_slot(int r, int s) {
     else return r * 8 + (s ^ ((r >> 1) & 7));
 }
 
-// KW = 2: eight waves in two groups.  Group 0 (waves 0-3) stages A and
-// multiplies the first 32-k half of every 64-deep slice, group 1 (waves 4-7)
-// stages B and multiplies the second half, each wave of a group on its own
-// WM x WN sub-tile; group 1 hands its accumulators to group 0 through LDS
-// after the main loop, and group 0 runs the epilogue.  Each wave then does
-// half the staging and half the MFMAs of a step, and two waves share each
-// SIMD, so one's waits are covered by the other's work.
-template <int FMT, int BM, int BN, int WM, int WN, int D, int BK = 32, int KW = 1>
-__global__ __launch_bounds__(256 * KW) void gemm_qbf_kernel(QbfArgs a) {
+// NW = 8 (eight waves): waves 0-3 stage A and waves 4-7 stage B, so each
+// wave does one operand's share of a step's staging, and two waves share
+// each SIMD, so one's waits are covered by the other's work.  The eight waves
+// either own eight WM x WN sub-tiles (KW = 1) or, with KW = 2, two groups of
+// four: group 0 (waves 0-3) multiplies the first 32-k half of every 64-deep
+// slice and group 1 (waves 4-7) the second half, each wave of a group on its
+// own sub-tile; group 1 hands its accumulators to group 0 through LDS after
+// the main loop, and group 0 runs the epilogue.
+template <int FMT, int BM, int BN, int WM, int WN, int D, int BK = 32, int KW = 1, int NW = 4 * KW>
+__global__ __launch_bounds__(64 * NW) void gemm_qbf_kernel(QbfArgs a) {
     static_assert(BK == 32 || BK == 64, "32- or 64-deep slices");
     static_assert(KW == 1 || (KW == 2 && BK == 64), "two wave groups split 64-deep slices into 32-k halves");
+    static_assert(NW == 4 || NW == 8, "four waves, or eight staging A and B in two halves");
     constexpr int SL = BK / 8;  // 16-byte slots (8 k) of an LDS row
-    constexpr int NT = 256;     // staging threads of an operand (all 256 take both when KW = 1)
+    constexpr int NT = 256;     // staging threads of an operand (all 256 take both when NW = 4)
+    constexpr int NWS = NW / KW;  // waves per group, one per sub-tile
     constexpr int TM = WM / 16, TN = WN / 16;
     constexpr int WAVES_N = BN / WN;
-    static_assert((BM / WM) * (BN / WN) == 4, "four waves, one per WM x WN sub-tile");
+    static_assert((BM / WM) * (BN / WN) == NWS, "one wave of a group per WM x WN sub-tile");
     static_assert(WM % 16 == 0 && WN % 16 == 0, "whole 16 x 16 MFMA tiles");
     // staging tasks of a slice: A one (row, 8-k slot) each; B one (column
     // pair, 8-k slot) each
@@ -134,8 +137,8 @@ __global__ __launch_bounds__(256 * KW) void gemm_qbf_kernel(QbfArgs a) {
 
     const int tid = threadIdx.x % NT, lane = tid & 63;  // tid: the thread's index in its group
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const int kg = KW == 2 ? wave / 4 : 0;  // wave group
-    const int sw = wave % 4;               // sub-tile of the wave
+    const int kg = KW == 2 ? wave / NWS : 0;  // wave group
+    const int sw = wave % NWS;               // sub-tile of the wave
     const int wm0 = (sw / WAVES_N) * WM, wn0 = (sw % WAVES_N) * WN;
     const int c = lane & 15, g = lane >> 4;
 
@@ -318,16 +321,18 @@ __global__ __launch_bounds__(256 * KW) void gemm_qbf_kernel(QbfArgs a) {
     };
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
-    if constexpr (KW == 1) {
+    if constexpr (NW == 4) {
         run(yes{}, yes{});
     } else {
-        if (kg == 0) run(yes{}, no{});
+        if (wave < 4) run(yes{}, no{});
         else run(no{}, yes{});
+    }
+    if constexpr (KW == 2) {
         // Group 1's accumulators to group 0 through A's hi stages, or B's
         // where those are larger (free: the loop's last barrier follows every
         // wave's last LDS read), in lane order per (wave, i, j).
         constexpr bool XB = BN > BM;
-        static_assert(4 * TM * TN * 64 <= 2 * (XB ? BN : BM) * SL, "the exchange fits the stages it uses");
+        static_assert(NWS * TM * TN * 64 <= 2 * (XB ? BN : BM) * SL, "the exchange fits the stages it uses");
         floatx4 *const xch = XB ? (floatx4 *)&Bs[0][0] : (floatx4 *)&Ah[0][0];
         if (kg == 1) {
 #pragma unroll
@@ -386,7 +391,7 @@ __global__ __launch_bounds__(256 * KW) void gemm_qbf_kernel(QbfArgs a) {
 }
 
 struct QbfCfg {
-    int bm, bn, bk, kw;  // kw: wave groups (gemm_qbf_kernel's KW)
+    int bm, bn, bk, kw, nw;  // kw, nw: gemm_qbf_kernel's wave groups and waves
 };
 // Tile configs (index = TML_GEMM_QBF_TILE - 1): <BM, BN, BK> with four
 // waves of BM/2 x BN/2.  The two large tiles keep two 32-deep slices of loads
@@ -409,9 +414,16 @@ struct QbfCfg {
 // 16.54 / 15.16, 384x1280x1280 13.98 / 13.40; Q4_0 128x4096x1024 12.28 /
 // 11.08, 512x4096x1024 21.46 / 19.37.  At M = 1500 they are slower than
 // 64 x 128 x 32 (QKV 54.0 against 46.5 us; a 64 x 128 x 64 two-group tile,
-// 130 registers, 55.8), so the large tiles keep one group.
-constexpr QbfCfg kQbfCfgs[] = {{128, 128, 32, 1}, {64, 128, 32, 1}, {64, 64, 32, 1}, {32, 64, 32, 1},
-                               {64, 64, 64, 1},   {32, 64, 64, 1},  {64, 64, 64, 2}, {32, 64, 64, 2}};
+// 130 registers, 55.8), so the large tiles keep one group.  Configs 8 and
+// 9 are the large tiles with eight waves instead (NW = 8, one group: 32 x 32
+// / 64 x 32 sub-tiles, waves 0-3 staging A and 4-7 B; 72 / 95 registers, so
+// three / two workgroups a CU): the planner takes them for every shape past
+// the small-tile rules (us, Q8_0, four / eight waves: 1500x3840x1280 at
+// 64 x 128 48.9 / 45.2, 1500x5120x1280 at 128 x 128 62.9 / 53.5,
+// 3000x3840x1280 at 128 x 128 105.5 / 80.4).
+constexpr QbfCfg kQbfCfgs[] = {{128, 128, 32, 1, 4}, {64, 128, 32, 1, 4}, {64, 64, 32, 1, 4}, {32, 64, 32, 1, 4},
+                               {64, 64, 64, 1, 4},   {32, 64, 64, 1, 4},  {64, 64, 64, 2, 8}, {32, 64, 64, 2, 8},
+                               {64, 128, 32, 1, 8},  {128, 128, 32, 1, 8}};
 constexpr int kQbfNumCfgs = (int)(sizeof(kQbfCfgs) / sizeof(kQbfCfgs[0]));
 
 template <int FMT>
@@ -424,7 +436,9 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
         case 4: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 2, 64><<<grid, 256, 0, s>>>(a); break;
         case 5: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 2, 64><<<grid, 256, 0, s>>>(a); break;
         case 6: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 2, 64, 2><<<grid, 512, 0, s>>>(a); break;
-        default: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 2, 64, 2><<<grid, 512, 0, s>>>(a); break;
+        case 7: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 2, 64, 2><<<grid, 512, 0, s>>>(a); break;
+        case 8: gemm_qbf_kernel<FMT, 64, 128, 32, 32, 2, 32, 1, 8><<<grid, 512, 0, s>>>(a); break;
+        default: gemm_qbf_kernel<FMT, 128, 128, 64, 32, 2, 32, 1, 8><<<grid, 512, 0, s>>>(a); break;
     }
 }
 
@@ -443,21 +457,28 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
 //     14.3 / 14.1 / 15.4 / 16.6; the same sweep with every launch reading
 //     its own weight copy out of >= 1 GiB, so from HBM: within 1 % of
 //     these, except 512x4096x1024 23.6 against 22.4 us at 64x64x64);
-//   * 128x128 unsplit when 64x128 tiles would give each CU more than 4.5;
-//   * else the tile (64x128, 64x64, 32x64) and K split s in 1..4 (at least
-//     eight 32-deep slices a split) of least
-//     modelled time
-//       t = ceil(tiles s / CUs) * (slices / s) * c / eff + 5.3 us + 1.7 us * (s - 1),
-//     c = 0.57 / 0.46 / 0.36 us a slice for the three tiles, eff = 1, 1.39,
-//     1.49 for one, two, three or more units a CU (the co-resident
-//     workgroups' overlap), the last term the partials and the reduce
-//     launch.  Fitted to sweeps on MI355X (us, Q8_0; 64x128 at s = 1..4):
-//     128x4096x1024 23.5 / 16.0 / 15.5 / 15.0 (64x64: 19.9 / 15.0, 32x64:
-//     16.7); 128x5120x1280 27.5 / 18.3 / 17.0 / 19.4; 192x4096x1024 23.6 /
-//     17.4 / 19.6 / 19.3; 1500x1280x5120 91 / 65.7 / 61.1 / 61.4;
-//     512x4096x1024 24.9 / 23.8 / 24.2 / 25.2; 512x384x384 32x64 9.0, 64x64
-//     10.9.  (1500x3840x1280 unsplit 48.1 against 61 at 128x128;
-//     1500x5120x1280 59.5 against 61.8.)
+//   * else the eight-wave 64x128 or 128x128 tile (configs 8, 9) and K split
+//     s in 1..4 (at least eight 32-deep slices a split; s > 1 only where the
+//     tiles number fewer than the CUs) of least modelled time
+//       t = u * ceil(slices / s) * c + 5.3 us + 1.7 us * (s - 1),
+//       u = ceil(tiles s / CUs) units a CU,
+//     c = 0.42 / 0.335 us a slice-unit at 64x128 for u = 1 / u >= 2 (three
+//     workgroups share a CU), 0.78 / 0.59 at 128x128 (two share a CU), the
+//     last term the partials and the reduce launch.  Fitted to a tile x
+//     split sweep on MI355X (us, Q8_0, every launch reading its own weight
+//     copy, 64x128 / 128x128 unsplit unless marked; the four-wave tiles of
+//     the same shapes and the plan before in brackets): 1500x3840x1280
+//     45.2 / 49.3 (48.9 / 60.2); 1500x5120x1280 59.7 / 53.5 (60.8 / 62.9);
+//     1500x1280x5120 s = 2 62.6, 128x128 s = 4 58.2 (64.3); 1024x4096x1024
+//     28.7 / 28.6 (32.0 / 42.0, plan 37.2); 2048x768x3072 64x128 s = 4 35.2
+//     (36.5); 768x3072x768 20.7 / 23.3 (26.6); 1500x1536x384 13.3 / 15.5
+//     (17.6); 3000x3840x1280 85.8 / 80.4 (88.7 / 105.5).  The model's pick
+//     is the measured best on seven of the eight and 0.1 us off on the
+//     eighth (1024x4096x1024).  Splitting tiles that already fill the CUs
+//     costs far more than the reduce term (the partials' traffic, M N s 8
+//     bytes, competes with the main loop): 128 x 128 at s = 2 measured
+//     53.1 us at 1500x3840x1280, 67.6 at 1500x5120x1280 and 35.0 at
+//     1024x4096x1024, 9-13 us above the model.
 void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) {
@@ -471,7 +492,7 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     auto split_ok = [&](int64_t ns) {
         return ns == 1 || nk / ns >= 8;
     };
-    int cfg = 1;
+    int cfg = 8;
     int64_t nsplit = 1;
     if (m.M <= 512 && tiles_of(6) >= 2LL * cus) {
         // 64 x 64 x 64 tiles, two wave groups, unsplit, where they give every
@@ -489,21 +510,21 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
             nsplit = ns;
             if (tiles_of(7) * ns >= cus) break;
         }
-    } else if ((double)tiles_of(1) > 4.5 * cus) {
-        cfg = 0;
     } else {
-        static const double slice_us[] = {0.0, 0.57, 0.46, 0.36};
+        static const int cand[] = {8, 9};
+        static const double c_one[] = {0.42, 0.78}, c_many[] = {0.335, 0.59};
         double best = 1e300;
-        for (int c = 1; c <= 3; ++c)
+        for (int i = 0; i < 2; ++i)
             for (int64_t ns = 1; ns <= 4; ++ns) {
-                if (!split_ok(ns)) break;
-                const int64_t per_cu = (tiles_of(c) * ns + cus - 1) / cus;
-                const double eff = per_cu >= 3 ? 1.49 : per_cu == 2 ? 1.39 : 1.0;
-                const double t =
-                    (double)per_cu * ((double)nk / (double)ns) * slice_us[c] / eff + 5.3 + 1.7 * (double)(ns - 1);
+                // K splits only where the tiles leave CUs idle
+                if (!split_ok(ns) || (ns > 1 && tiles_of(cand[i]) >= cus)) break;
+                const int64_t per_cu = (tiles_of(cand[i]) * ns + cus - 1) / cus;
+                const int64_t slices = (nk + ns - 1) / ns;
+                const double t = (double)per_cu * (double)slices * (per_cu > 1 ? c_many[i] : c_one[i]) + 5.3 +
+                                 1.7 * (double)(ns - 1);
                 if (t < best) {
                     best = t;
-                    cfg = c;
+                    cfg = cand[i];
                     nsplit = ns;
                 }
             }
