@@ -21,8 +21,10 @@
 // other GEMM kernels in half the cycles, so even the two of them per product
 // leave the kernel bound by its LDS traffic, not by the matrix cores.
 //
-// Tiles.  A workgroup of four waves owns a BM x BN tile of C (each wave a
-// WM x WN sub-tile of (WM/16) x (WN/16) MFMA tiles) and walks K in 32- or
+// Tiles.  A workgroup of four or eight waves owns a BM x BN tile of C (each
+// wave a WM x WN sub-tile of (WM/16) x (WN/16) MFMA tiles, or with two wave
+// groups half the k of one; with eight waves, half of them stage A and half
+// B, see gemm_qbf_kernel) and walks K in 32- or
 // 64-deep slices (BK) through two LDS stages: the next slice's global loads
 // are issued before the current slice's MFMAs, converted and written after
 // them, one barrier a slice.  LDS holds, per stage, A's hi and lo planes and
@@ -135,7 +137,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_qbf_kernel(QbfArgs a) {
 
     __shared__ uintx4 Ah[2][BM * SL], Al[2][BM * SL], Bs[2][BN * SL];
 
-    const int tid = threadIdx.x % NT, lane = tid & 63;  // tid: the thread's index in its group
+    // tid: the thread's index among the NT threads that stage its operand(s)
+    const int tid = threadIdx.x % NT, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int kg = KW == 2 ? wave / NWS : 0;  // wave group
     const int sw = wave % NWS;               // sub-tile of the wave
