@@ -491,11 +491,31 @@ int device_cus() {
 // 0.504, 256x128 4.05 (not refitted: it spills), 128x64 (BK 64) 1.06 /
 // 1.147, 64x64 (BK 64) 0.54 / 0.672, 32x64 0.308 / 0.24, 32x64 (BK 64)
 // 0.308 / 0.293, 96x32 0.354 / 0.383 (no int4 variant), 32x64 (BK 64, two
-// wave groups along K) 0.226 / 0.282.
+// wave groups along K) 0.226 / 0.282.  F16 and Q8_K widen B (and Q8_K
+// multiplies its block scales) at every fragment read, which costs each
+// tile differently, so they have tables of their own: the medians of a
+// sweep of every tile x split (1, 2) over eleven shapes (the
+// sentence-transformer linears, 384-1500 x 3840-4096 x 768-1280, 128x4096x1024,
+// 2048x768x3072, 1024x4096x1024), 128x128 with one unit a CU taken from
+// its worst case; with them the planner considers K splits of 1 and 2
+// only.  Against the f32 table's picks (us, F16 / Q8_K):
+// 512x4096x768 34.39 / 40.17 -> 32.82 / 37.56, 384x4096x1024 34.93 / 41.19
+// -> 33.23 / 37.17, 512x3072x768 Q8_K 32.54 -> 30.85, 1500x3840x1280
+// 134.1 / 150.2 -> 130.7 / 142.6.  Q4_0 and Q8_0 keep the f32 table.
 void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
-    static const double t_one[] = {1.975, 0.974, 0.528, 4.05, 1.06, 0.54, 0.308, 0.308, 0.354, 0.226};
-    static const double t_many[] = {1.998, 0.854, 0.504, 4.05, 1.147, 0.672, 0.24, 0.293, 0.383, 0.282};
-    static_assert(sizeof(t_one) == sizeof(t_many), "one cost pair per tile config");
+    static const double f32_one[] = {1.975, 0.974, 0.528, 4.05, 1.06, 0.54, 0.308, 0.308, 0.354, 0.226};
+    static const double f32_many[] = {1.998, 0.854, 0.504, 4.05, 1.147, 0.672, 0.24, 0.293, 0.383, 0.282};
+    static const double f16_one[] = {2.40, 1.276, 0.680, 4.66, 1.162, 0.690, 0.418, 0.396, 0.556, 0.359};
+    static const double f16_many[] = {2.123, 1.152, 0.574, 4.66, 1.180, 0.592, 0.304, 0.318, 0.435, 0.318};
+    static const double q8k_one[] = {2.70, 1.466, 0.861, 5.06, 1.358, 0.799, 0.571, 0.489, 0.687, 0.465};
+    static const double q8k_many[] = {2.389, 1.291, 0.659, 5.06, 1.370, 0.666, 0.369, 0.355, 0.477, 0.379};
+    static_assert(sizeof(f32_one) == sizeof(f32_many) && sizeof(f16_one) == sizeof(f32_one) &&
+                      sizeof(f16_many) == sizeof(f32_one) && sizeof(q8k_one) == sizeof(f32_one) &&
+                      sizeof(q8k_many) == sizeof(f32_one),
+                  "one cost pair per tile config");
+    const bool narrow_table = fmt == TML_FMT_F16 || fmt == TML_FMT_Q8_K;
+    const double *const t_one = fmt == TML_FMT_F16 ? f16_one : fmt == TML_FMT_Q8_K ? q8k_one : f32_one;
+    const double *const t_many = fmt == TML_FMT_F16 ? f16_many : fmt == TML_FMT_Q8_K ? q8k_many : f32_many;
     static const int splits[] = {1, 2, 3, 4, 6, 8};
     constexpr double kFill = 3.5, kReduce = 3.6, kBytesPerUs = 6.0e6;
     const int cus = device_cus();
@@ -504,7 +524,7 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
     const int forced_split = env_int("TML_GEMM_SPLIT", 0);
     double best_t = 1e300;
     for (int c = 0; c < gemm_dma_num_cfgs(); ++c) {
-        if (c >= (int)(sizeof(t_one) / sizeof(t_one[0]))) break;  // no cost model for this config
+        if (c >= (int)(sizeof(f32_one) / sizeof(f32_one[0]))) break;  // no cost model for this config
         if ((forced_tile >= 0 && c != forced_tile) || !gemm_dma_cfg_ok(c, fmt)) continue;
         int bm = 0, bn = 0, bk = 32;
         gemm_dma_tile(c, &bm, &bn, &bk);
@@ -513,6 +533,7 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
         for (int sp : splits) {
             if (forced_split > 0 && sp != forced_split) continue;
             if (sp > 1 && nk < 2 * sp) continue;
+            if (narrow_table && sp > 2 && forced_split <= 0) break;  // the narrow tables were fitted on s <= 2
             const int64_t spl = nk > 0 ? (nk + sp - 1) / sp : 1;
             const int64_t real = nk > 0 ? (nk + spl - 1) / spl : 1;
             const int64_t units = tiles * real;
@@ -613,10 +634,18 @@ GemmPlan plan_gemm(const MatmulArgs &m) {
     //        1500x3840x1280 162.4 / 140.8;
     //   F16  512x4096x1024 41.5 / 43.2, 1500x3840x1280 143.3 / 132.2;
     //   Q8_K 1500x3840x1280 150.4 / 148.6.
-    // So F16 and Q4_0 take the direct-copy kernel from M = 1024 on, Q4_0 also
-    // at M <= 128 (where the register-staged kernel widens each B element of
-    // a tile for few rows of A); Q8_0 and Q8_K keep the register-staged
-    // kernel.  Every narrow format also takes it whenever the register-staged
+    // So Q4_0 takes the direct-copy kernel from M = 1024 on and at M <= 128
+    // (where the register-staged kernel widens each B element of a tile for
+    // few rows of A); Q8_0 keeps the register-staged kernel.  F16 and Q8_K,
+    // with their own tile costs in the direct-copy planner (pick_dma), take
+    // the direct-copy kernel at every M, except Q8_K from M = 512 with
+    // N >= 4096 (us, register-staged / direct-copy on the planner's pick, F16
+    // | Q8_K): 512x1152x384 14.83 / 11.48 | 17.05 / 13.09, 512x3072x768
+    // 33.74 / 28.08 | 34.78 / 30.85, 384x4096x1024 42.3 / 33.2 | 44.1 / 37.2,
+    // 128x4096x1024 18.46 / 16.63 | 23.74 / 20.19, 1500x3840x1280 139.3 /
+    // 130.7 | 154.7 / 142.6; 512x4096x1024 42.31 / 41.24 | 44.15 / 47.36,
+    // 1024x4096x1024 76.03 / 74.37 | 80.51 / 84.76.  Every narrow format
+    // also takes it whenever the register-staged
     // kernel's best tiling leaves most CUs idle (it has no K split): at
     // 256x768x3072 Q8_0 the direct-copy kernel with its split takes 23.1 us
     // against 45.1, at 512x384x1536 16.3 against 24.8, at 256x768x768 10.9
@@ -630,7 +659,7 @@ GemmPlan plan_gemm(const MatmulArgs &m) {
         const int64_t tiles = ((m.M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((m.N + kCfgs[c].bn - 1) / kCfgs[c].bn);
         few_tiles = tiles < cus / 2 || (tiles < cus && m.K >= 2048);
     }
-    const bool by_m = (m.fmt == TML_FMT_F16 && m.M >= 1024) ||
+    const bool by_m = m.fmt == TML_FMT_F16 || (m.fmt == TML_FMT_Q8_K && !(m.M >= 512 && m.N >= 4096)) ||
                       (m.fmt == TML_FMT_Q4_0 && (m.M >= 1024 || m.M <= 128));
     const bool narrow_ok = m.fmt == TML_FMT_F32 || dma_q == 1 || (dma_q < 0 && (by_m || few_tiles));
     if (narrow_ok && env_int("TML_GEMM_DMA", 1) != 0 && gemm_dma_supported(m) && m.K > 0) {
