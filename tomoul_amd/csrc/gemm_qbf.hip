@@ -448,18 +448,17 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
 }  // namespace
 
 // Tile and K split: forced by TML_GEMM_QBF_TILE / TML_GEMM_QBF_SPLIT, else
-//   * up to M = 512: 64x64x64 unsplit where those tiles give every CU two,
-//     else 32x64x64 where those tiles number at most four a CU, with the fewest
-//     K splits s in 1..4 that give every CU a unit, both with two wave groups
-//     (the rule from a tile x split sweep of the one-group tiles,
-//     us, Q8_0, 32x64x64 at s = 1..4: 128x4096x1024 12.6 / 13.5 / 14.9 /
-//     15.6; 128x5120x1280 17.4 / 16.8 / 18.0 / 19.4; 128x1280x5120 42.7 /
-//     25.1 / 19.9 / 19.4; 192x4096x1024 15.3 / 15.9 / 19.4 / 19.0;
-//     256x4096x1024 16.3 / 16.5 / 19.1 / 19.9; 512x4096x1024 21.7 / 28.0 /
-//     31.6 / 32.8; 256x768x3072 27.4 / 17.6 / 16.7 / 15.1; 384x1280x1280
-//     14.3 / 14.1 / 15.4 / 16.6; the same sweep with every launch reading
-//     its own weight copy out of >= 1 GiB, so from HBM: within 1 % of
-//     these, except 512x4096x1024 23.6 against 22.4 us at 64x64x64);
+//   * up to M = 512, where 32x64 tiles number at most four a CU: 64x64x64
+//     or 32x64x64 with two wave groups and K split s in 1..4 of least
+//     modelled time (see pick_qbf), fitted to a sweep of both tiles at
+//     s = 1..4 over 45 shapes (M = 128, 192, 256, 384, 512; N x K = 4096 x
+//     1024, 1024 x 4096, 768 x 3072, 3072 x 768, 1280 x 1280, 5120 x 1280,
+//     1280 x 5120, 1536 x 384, 384 x 1536; every launch reading its own
+//     weight copy): its picks sum to 564.0 us against 553.9 for the best of
+//     each shape and 591.6 for the rule before (the fewest splits giving
+//     every CU a unit), e.g. 256x1024x4096 19.24 -> 16.43, 256x1280x5120
+//     26.87 -> 21.86, 384x768x3072 18.73 -> 15.85, 512x1024x4096 29.63 ->
+//     24.02 us;
 //   * else the eight-wave 64x128 or 128x128 tile (configs 8, 9) and K split
 //     s in 1..4 (at least eight 32-deep slices a split; s > 1 only where the
 //     tiles number fewer than the CUs) of least modelled time
@@ -497,22 +496,34 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
     };
     int cfg = 8;
     int64_t nsplit = 1;
-    if (m.M <= 512 && tiles_of(6) >= 2LL * cus) {
-        // 64 x 64 x 64 tiles, two wave groups, unsplit, where they give every
-        // CU two: half the A and B re-reads of 32 x 64 (512x4096x1024, one
-        // group: 22.4 against 23.6 us)
-        cfg = 6;
-    } else if (m.M <= 512 && tiles_of(7) <= 4LL * cus) {
-        // 32 x 64 x 64 tiles, two wave groups, with the fewest K splits that
-        // give every CU a unit (one group: within 2 % of the best of a tile x
-        // split sweep on average, M = 128-512, N = 768-5120, K = 1024-5120;
-        // at M = 1500 its A and B re-reads cost more: 1500x1280x5120 82.9
-        // against 61.3 us)
-        cfg = 7;
-        for (int64_t ns = 1; ns <= 4 && split_ok(ns); ++ns) {
-            nsplit = ns;
-            if (tiles_of(7) * ns >= cus) break;
-        }
+    // the modelled time of config c at s splits (the plan's own rounding of
+    // the slices into whole BK-deep ones per split)
+    auto modelled = [&](int c, int64_t ns, double c_one, double c_many, double per_split, double traffic) {
+        const int64_t per = kQbfCfgs[c].bk / 32;
+        const int64_t spl = ((nk + ns - 1) / ns + per - 1) / per * per;
+        const int64_t real = (nk + spl - 1) / spl;
+        const int64_t per_cu = (tiles_of(c) * real + cus - 1) / cus;
+        double t = (double)per_cu * (double)(spl / per) * (per_cu > 1 ? c_many : c_one) + 5.3;
+        if (real > 1) t += per_split * (double)(real - 1) + traffic * (double)real * (double)m.M * (double)m.N * 8.0 / 6.0e6;
+        return t;
+    };
+    if (m.M <= 512 && tiles_of(7) <= 4LL * cus) {
+        // 64 x 64 x 64 or 32 x 64 x 64 tiles with two wave groups (configs 6,
+        // 7) and K split s in 1..4 of least modelled time, c = 0.60 / 0.45 us
+        // a 64-deep slice-unit at 64 x 64 for u = 1 / u >= 2, 0.35 / 0.25 at
+        // 32 x 64, plus 1.0 us a split past the first and half the
+        // partials' traffic at 6 TB/s
+        static const double c_one[] = {0.60, 0.35}, c_many[] = {0.45, 0.25};
+        double best = 1e300;
+        for (int i = 0; i < 2; ++i)
+            for (int64_t ns = 1; ns <= 4 && split_ok(ns); ++ns) {
+                const double t = modelled(6 + i, ns, c_one[i], c_many[i], 1.0, 0.5);
+                if (t < best) {
+                    best = t;
+                    cfg = 6 + i;
+                    nsplit = ns;
+                }
+            }
     } else {
         static const int cand[] = {8, 9};
         static const double c_one[] = {0.42, 0.78}, c_many[] = {0.335, 0.59};
@@ -521,10 +532,7 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
             for (int64_t ns = 1; ns <= 4; ++ns) {
                 // K splits only where the tiles leave CUs idle
                 if (!split_ok(ns) || (ns > 1 && tiles_of(cand[i]) >= cus)) break;
-                const int64_t per_cu = (tiles_of(cand[i]) * ns + cus - 1) / cus;
-                const int64_t slices = (nk + ns - 1) / ns;
-                const double t = (double)per_cu * (double)slices * (per_cu > 1 ? c_many[i] : c_one[i]) + 5.3 +
-                                 1.7 * (double)(ns - 1);
+                const double t = modelled(cand[i], ns, c_one[i], c_many[i], 1.7, 0.0);
                 if (t < best) {
                     best = t;
                     cfg = cand[i];
