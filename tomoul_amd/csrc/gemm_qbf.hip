@@ -454,11 +454,13 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
 //     s = 1..4 over 45 shapes (M = 128, 192, 256, 384, 512; N x K = 4096 x
 //     1024, 1024 x 4096, 768 x 3072, 3072 x 768, 1280 x 1280, 5120 x 1280,
 //     1280 x 5120, 1536 x 384, 384 x 1536; every launch reading its own
-//     weight copy): its picks sum to 564.0 us against 553.9 for the best of
-//     each shape and 591.6 for the rule before (the fewest splits giving
-//     every CU a unit), e.g. 256x1024x4096 19.24 -> 16.43, 256x1280x5120
-//     26.87 -> 21.86, 384x768x3072 18.73 -> 15.85, 512x1024x4096 29.63 ->
-//     24.02 us;
+//     weight copy; the 41 under the forced-plan size cap): its picks sum to
+//     564.0 us against 553.9 for the best of each shape and 591.6 for the
+//     rule before (the fewest splits giving every CU a unit); measured on
+//     all 45 afterwards 677 against 723 us, e.g. 256x1024x4096 19.24 ->
+//     16.46, 256x1280x5120 26.87 -> 21.81, 384x768x3072 18.73 -> 15.92,
+//     512x1280x5120 46.34 -> 30.88 us (128x384x1536 9.08 -> 9.56 and
+//     512x1280x1280 15.57 -> 16.74 the two that lost);
 //   * else the eight-wave 64x128 or 128x128 tile (configs 8, 9) and K split
 //     s in 1..4 (at least eight 32-deep slices a split; s > 1 only where the
 //     tiles number fewer than the CUs) of least modelled time
