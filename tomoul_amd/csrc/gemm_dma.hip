@@ -579,48 +579,61 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         return;
     }
 
-    if constexpr (KW == 1 && BN <= BK) {
+    if constexpr (KW == 1) {
         if (a.vec_epi) {
             // Staged epilogue: the tile goes through LDS (A stage 0, free once
-            // every wave has read its last slice: BM x BN floats fit in BM x
-            // BK) and is written as whole 16-byte pieces of C rows, a row's
-            // BN floats by consecutive lanes of one store instruction,
+            // every wave has read its last slice) in passes of PW columns (the
+            // stage holds BM x BK floats) and is written as whole 16-byte
+            // pieces of C rows, a pass's PW floats of a row (128 or 256 bytes:
+            // whole cache lines) by consecutive lanes of one store instruction,
             // instead of 4-byte stores of 16-column strips (config 1: 20.34
-            // against 20.58 us).
+            // against 20.58 us; with the non-temporal stores the strips left
+            // half lines that cost 17 % more HBM writes at the headline).
+            constexpr int PW = BN < BK ? BN : BK;
+            static_assert(BN % PW == 0 && PW % 16 == 0, "passes of whole 16-column fragment blocks");
+            constexpr int CH = PW / 4;  // 16-byte pieces per pass row
             float *ct = As0;
-            wait_lgkmcnt0();
-            raw_barrier();
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+            for (int pass = 0; pass < BN / PW; ++pass) {
+                wait_lgkmcnt0();
+                raw_barrier();
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
+                for (int j = 0; j < TN; ++j) {
+                    // the fragment's 16- (32- when paired) column block lies
+                    // in one pass; the test is uniform over the wave
+                    const int cb = PAIR ? wn0 + 32 * (j / 2) : wn0 + 16 * j;
+                    if (cb / PW != pass) continue;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ct[(wm0 + i * 16 + rq + r) * BN + bcol(j)] = acc[i][j][r];
-            wait_lgkmcnt0();
-            raw_barrier();
-            constexpr int CH = BN / 4;  // 16-byte pieces per tile row
+                    for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int e = tid; e < BM * CH; e += NW * 64) {
-                const int row = m0 + e / CH, col = n0 + 4 * (e % CH);
-                if (row >= a.M || col >= a.N) continue;  // N % 4 == 0: a piece is all in or all out
-                const floatx4 v4 = *(const floatx4 *)&ct[(e / CH) * BN + 4 * (e % CH)];
-                const size_t o = (size_t)row * a.N + col;
-                floatx4 cv = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f}, rv = {0.f, 0.f, 0.f, 0.f};
-                floatx4 sv = {1.f, 1.f, 1.f, 1.f};
-                if (a.beta != 0.0f) cv = *(const floatx4 *)(a.C + o);
-                if (a.bias) bv = *(const floatx4 *)(a.bias + col);
-                if (a.res) rv = *(const floatx4 *)(a.res + o);
-                if (a.colscale) sv = *(const floatx4 *)(a.colscale + col);
-                floatx4 out;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float v = (a.colscale ? a.alpha * sv[q] : a.alpha) * v4[q];
-                    if (a.beta != 0.0f) v += a.beta * cv[q];
-                    if (a.bias) v += bv[q];
-                    if (a.res) v += rv[q];
-                    out[q] = tml_apply_act(v, a.act, (long long)o + q, a.tail0);
+                        for (int r = 0; r < 4; ++r)
+                            ct[(wm0 + i * 16 + rq + r) * PW + bcol(j) - pass * PW] = acc[i][j][r];
                 }
-                tml_store_c(a.C + o, out);
+                wait_lgkmcnt0();
+                raw_barrier();
+#pragma unroll
+                for (int e = tid; e < BM * CH; e += NW * 64) {
+                    const int row = m0 + e / CH, col = n0 + pass * PW + 4 * (e % CH);
+                    if (row >= a.M || col >= a.N) continue;  // N % 4 == 0: a piece is all in or all out
+                    const floatx4 v4 = *(const floatx4 *)&ct[(e / CH) * PW + 4 * (e % CH)];
+                    const size_t o = (size_t)row * a.N + col;
+                    floatx4 cv = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f}, rv = {0.f, 0.f, 0.f, 0.f};
+                    floatx4 sv = {1.f, 1.f, 1.f, 1.f};
+                    if (a.beta != 0.0f) cv = *(const floatx4 *)(a.C + o);
+                    if (a.bias) bv = *(const floatx4 *)(a.bias + col);
+                    if (a.res) rv = *(const floatx4 *)(a.res + o);
+                    if (a.colscale) sv = *(const floatx4 *)(a.colscale + col);
+                    floatx4 out;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        float v = (a.colscale ? a.alpha * sv[q] : a.alpha) * v4[q];
+                        if (a.beta != 0.0f) v += a.beta * cv[q];
+                        if (a.bias) v += bv[q];
+                        if (a.res) v += rv[q];
+                        out[q] = tml_apply_act(v, a.act, (long long)o + q, a.tail0);
+                    }
+                    tml_store_c(a.C + o, out);
+                }
             }
             return;
         }
