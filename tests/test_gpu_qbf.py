@@ -181,3 +181,45 @@ def test_qbf_off_switch_agrees(orc, env):
         old = _gemm(fmt, m, n, k, a, b, scale, scales)
         env.pop("TML_GEMM_QBF")
         assert rel_err(got, ref) <= TOL and rel_err(old, ref) <= 1e-5 and rel_err(got, old) <= TOL, fmt
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+def test_qbf_staged_epilogue(orc, env, tile):
+    # With N a multiple of 4 and 16-byte aligned operands the tiles whose C
+    # tile fits the staging buffer in one pass (tiles 4-8: 32 x 64, and
+    # 64 x 64 on 64-deep slices)
+    # write C through LDS in whole 16-byte row pieces, the large ones the
+    # per-lane 4-byte path, which TML_GEMM_VEC_EPI=0 takes everywhere.  Every epilogue term
+    # (alpha, beta * C, bias, residual, GELU, per-column scales) on ragged M
+    # and N, K split or not: against the oracle, and the two paths within
+    # rounding of each other.
+    import torch
+    env["TML_GEMM_QBF_TILE"] = str(tile)
+    saved = os.environ.get("TML_GEMM_VEC_EPI")
+    m, n, k = 203, 340, 520
+    a, w, c0, r = rnd(691, m, k), rnd(692, k, n, 0.05), rnd(693, m, n), rnd(694, m, n)
+    bias = synth.normal(695, n, 0.0, 0.5)
+    try:
+        for split in ("1", "3"):
+            env["TML_GEMM_QBF_SPLIT"] = split
+            for fmt, b, scale, scales, prod in _cases(orc, w, k, n, a):
+                ref = orc.gelu_exact(0.75 * prod - 0.5 * c0 + bias + r)
+                got = {}
+                for staged in ("1", "0"):
+                    os.environ["TML_GEMM_VEC_EPI"] = staged
+                    dev = [torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0") for x in (a, b, c0, r, bias)]
+                    A, B, C, R, Bias = dev
+                    S = torch.from_numpy(scales).to("cuda:0") if scales is not None else None
+                    _abi.gemm_ex_dev(fmt, m, n, k, A.data_ptr(), B.data_ptr(), C.data_ptr(), scale=scale,
+                                     act=_abi.ACT_GELU_ERF, residual_ptr=R.data_ptr(),
+                                     scales_ptr=S.data_ptr() if S is not None else None, bias_ptr=Bias.data_ptr(),
+                                     alpha=0.75, beta=-0.5)
+                    torch.cuda.synchronize()
+                    got[staged] = C.cpu().numpy()
+                assert rel_err(got["1"], ref) <= TOL, (tile, split, fmt, rel_err(got["1"], ref))
+                assert rel_err(got["1"], got["0"]) <= 1e-6, (tile, split, fmt)
+    finally:
+        if saved is None:
+            os.environ.pop("TML_GEMM_VEC_EPI", None)
+        else:
+            os.environ["TML_GEMM_VEC_EPI"] = saved

@@ -67,6 +67,7 @@ struct QbfArgs {
     int tiles_m, tiles_n;
     int nsplit, spl;        // K splits, 32-deep slices per split
     float *ws;              // nsplit > 1: [nsplit][M][N] raw partials
+    int vec_epi;            // N % 4 == 0 and C, bias, residual, column scales 16-byte aligned
 };
 
 __device__ __forceinline__ uintx4 qbf_load16(const void *base, unsigned nbytes, unsigned off) {
@@ -344,17 +345,22 @@ __global__ __launch_bounds__(64 * NW) void gemm_qbf_kernel(QbfArgs a) {
                 for (int j = 0; j < TN; ++j) xch[((sw * TM + i) * TN + j) * 64 + lane] = acc[i][j];
         }
         __syncthreads();
-        if (kg == 1) return;
+        if (kg == 0) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] += xch[((sw * TM + i) * TN + j) * 64 + lane];
+                for (int j = 0; j < TN; ++j) acc[i][j] += xch[((sw * TM + i) * TN + j) * 64 + lane];
+        }
     }
+    // the waves that hold the tile's final accumulators (group 1 of KW = 2
+    // only helps with the staged stores below)
+    const bool holds = KW == 1 || kg == 0;
 
     // Epilogue: lane (c, g) holds rows 4 g + r, column c of each MFMA tile.
     if (a.nsplit > 1) {
         // raw partial of this split; launch_splitk_reduce adds the splits in
         // order and runs the epilogue
+        if (!holds) return;
         float *const part = a.ws + (size_t)split * a.M * a.N;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -370,6 +376,68 @@ __global__ __launch_bounds__(64 * NW) void gemm_qbf_kernel(QbfArgs a) {
         }
         return;
     }
+    constexpr bool SB = BN > BM;
+    constexpr int CAP = 2 * (SB ? BN : BM) * SL * 4;  // floats the staging buffer holds
+    constexpr int PW0 = CAP / BM < BN ? CAP / BM : BN;
+    constexpr int PW = PW0 >= 64 ? 64 : PW0 >= 32 ? 32 : 16;  // a power of two dividing BN
+    static_assert(BN % PW == 0 && PW % 16 == 0 && BM * PW <= CAP, "passes of whole 16-column blocks");
+    if (BN == PW && a.vec_epi) {
+        // Staged: where the C tile fits the staging buffer (A's hi stages, or
+        // B's where those are larger; free after the barrier below) in one
+        // pass, it goes through LDS and is written as whole 16-byte pieces of
+        // C rows, a row's BN floats by consecutive lanes of one store
+        // instruction, so the non-temporal stores leave whole cache lines
+        // rather than the 64-byte strips of the per-lane path.  Measured
+        // against the per-lane path (us, Q8_0): 128x4096x1024 11.21 ->
+        // 10.19, 512x4096x1024 21.01 -> 18.74, 256x4096x1024 13.71 -> 12.88.
+        // The large tiles, which would need two (64 x 128) or four (128 x 128)
+        // passes, keep the per-lane path: staged, 1500x3840x1280 measured
+        // 44.79 against 43.64 us and 1500x5120x1280 54.24 against 53.54, for
+        // 2-11 % more HBM writes than C on the per-lane path.
+        constexpr int CH = PW / 4;  // 16-byte pieces per pass row
+        float *const ct = SB ? (float *)&Bs[0][0] : (float *)&Ah[0][0];
+#pragma unroll
+        for (int pass = 0; pass < BN / PW; ++pass) {
+            __syncthreads();
+            if (holds) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    if ((wn0 + 16 * j) / PW != pass) continue;  // uniform over the wave
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            ct[(wm0 + 16 * i + 4 * g + r) * PW + wn0 + 16 * j + c - pass * PW] = acc[i][j][r];
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int e = (int)threadIdx.x; e < BM * CH; e += NW * 64) {
+                const int row = m0 + e / CH, col = n0 + pass * PW + 4 * (e % CH);
+                if (row >= a.M || col >= a.N) continue;  // N % 4 == 0: a piece is all in or all out
+                const floatx4 v4 = *(const floatx4 *)&ct[(e / CH) * PW + 4 * (e % CH)];
+                const size_t o = (size_t)row * a.N + col;
+                floatx4 cv = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f}, rv = {0.f, 0.f, 0.f, 0.f};
+                floatx4 sv = {1.f, 1.f, 1.f, 1.f};
+                if (a.beta != 0.0f) cv = *(const floatx4 *)(a.C + o);
+                if (a.bias) bv = *(const floatx4 *)(a.bias + col);
+                if (a.res) rv = *(const floatx4 *)(a.res + o);
+                if (a.colscale) sv = *(const floatx4 *)(a.colscale + col);
+                floatx4 out;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v = (a.colscale ? a.alpha * sv[q] : a.alpha) * v4[q];
+                    if (a.beta != 0.0f) v += a.beta * cv[q];
+                    if (a.bias) v += bv[q];
+                    if (a.res) v += rv[q];
+                    out[q] = tml_apply_act(v, a.act, (long long)o + q, a.tail0);
+                }
+                tml_store_c(a.C + o, out);
+            }
+        }
+        return;
+    }
+    if (!holds) return;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int col = n0 + wn0 + 16 * j + c;
@@ -594,6 +662,9 @@ Status launch_gemm_qbf(const MatmulArgs &m, const GemmPlan &p, const Workspace &
     a.nsplit = p.nsplit;
     a.spl = p.spl;
     a.ws = p.nsplit > 1 ? ws.partials : nullptr;
+    a.vec_epi = m.N % 4 == 0 && ((uintptr_t)m.C % 16) == 0 && (m.bias == nullptr || ((uintptr_t)m.bias % 16) == 0) &&
+                (m.res == nullptr || ((uintptr_t)m.res % 16) == 0) &&
+                (m.colscale == nullptr || ((uintptr_t)m.colscale % 16) == 0) && env_int("TML_GEMM_VEC_EPI", 1) != 0;
     const int64_t grid = (int64_t)a.tiles_m * a.tiles_n * p.nsplit;
     if (grid >= ((int64_t)1 << 31)) return Status::Err(TML_ERR_INVALID_SHAPE, "bf16 matrix-core GEMM: grid too large");
     if (m.fmt == TML_FMT_Q8_0) launch_qbf_cfg<TML_FMT_Q8_0>(cfg, (unsigned)grid, a, s);
