@@ -579,7 +579,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
         return;
     }
 
-    if constexpr (KW == 1) {
+    {
         if (a.vec_epi) {
             // Staged epilogue: the tile goes through LDS (A stage 0, free once
             // every wave has read its last slice) in passes of PW columns (the
@@ -589,6 +589,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
             // instead of 4-byte stores of 16-column strips (config 1: 20.34
             // against 20.58 us; with the non-temporal stores the strips left
             // half lines that cost 17 % more HBM writes at the headline).
+            // With two wave groups only group 0 is left (group 1 ended after
+            // the exchange, and the barriers count the waves still running);
+            // BN <= BK there, so the tile is one pass.
             constexpr int PW = BN < BK ? BN : BK;
             static_assert(BN % PW == 0 && PW % 16 == 0, "passes of whole 16-column fragment blocks");
             constexpr int CH = PW / 4;  // 16-byte pieces per pass row
@@ -612,7 +615,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaArgs a) {
                 wait_lgkmcnt0();
                 raw_barrier();
 #pragma unroll
-                for (int e = tid; e < BM * CH; e += NW * 64) {
+                for (int e = tid; e < BM * CH; e += NWS * 64) {
                     const int row = m0 + e / CH, col = n0 + pass * PW + 4 * (e % CH);
                     if (row >= a.M || col >= a.N) continue;  // N % 4 == 0: a piece is all in or all out
                     const floatx4 v4 = *(const floatx4 *)&ct[(e / CH) * PW + 4 * (e % CH)];
