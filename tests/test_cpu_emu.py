@@ -102,6 +102,11 @@ def _default_cases():
                     cs.append(f"gemm {fmt} {M} {N} {K - K % 8 + 8} br TML_GEMM_QBF=2 TML_GEMM_QBF_TILE={tile} "
                               f"TML_GEMM_QBF_SPLIT={split}")
             cs.append(f"gemm {fmt} 33 {N + 2} 40 te TML_GEMM_QBF=2")
+            # the planner's own small-M plans (K split 4, 3, 2 and none)
+            cs.append(f"gemm {fmt} 16 1024 1024 br")
+            cs.append(f"gemm {fmt} 16 3072 768 b")
+            cs.append(f"gemm {fmt} 48 4096 512 bB")
+            cs.append(f"gemm {fmt} 100 4096 256 b")
             cs.append(f"gemm {fmt} 300 70 1288 bB")
     # [K,N] GEMV and the prepared GEMV at every row count
     for fmt in (F32, F16, Q8_0, Q4_0, Q8_K, Q8_0_PC, Q4_0_PC):

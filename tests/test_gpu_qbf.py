@@ -6,9 +6,9 @@ the reference's dequantize-then-fp32-accumulate result (matmulF32Q8 /
 matmulF32Q4, src/core/quantization.zig:240-311, :829-957; per-column scales
 through oracle.matmul_cols) to ~1e-5.  The bound here is 2e-5, not the 1e-3
 bar of the quantized paths: a dropped lo term costs ~4e-3, a misplaced k,
-column or nibble far more.  The planner takes this kernel from M = 128 on;
-TML_GEMM_QBF=2 (or a forced tile / split) takes it for every M > 8, which
-these tests use to reach it on small shapes.
+column or nibble far more.  The planner takes this kernel for every M past
+the GEMV rows (M > 8); TML_GEMM_QBF=0 turns it off (any other value leaves
+it on), a forced tile or split picks its plan.
 """
 import os
 
@@ -70,6 +70,22 @@ def test_qbf_tiles_vs_oracle(orc, env, tile):
         w = rnd(301, k, n, 0.02)
         a = rnd(302 + m, m, k)
         bias = synth.normal(303, n, 0.0, 0.02)
+        for fmt, b, scale, scales, ref in _cases(orc, w, k, n, a):
+            got = _gemm(fmt, m, n, k, a, b, scale, scales, bias)
+            err = rel_err(got, ref + bias)
+            assert err <= TOL, (m, n, k, fmt, err)
+
+
+@pytest.mark.parametrize("m", [9, 16, 48, 96, 127])
+def test_qbf_small_m_default_plan(orc, env, m):
+    # Below 128 rows the planner takes the 32 x 64 x 64 two-group tile with
+    # the largest K split (1-4) that keeps its units within the CUs: every
+    # split count appears across these shapes (4096 x 1024 at M = 9 splits
+    # 4, at M = 48 2, at M = 96 not at all; 3072 x 768 splits 3 at M = 16).
+    for (n, k) in [(4096, 1024), (3072, 768), (1536, 384)]:
+        w = rnd(351, k, n, 0.02)
+        a = rnd(352 + m, m, k)
+        bias = synth.normal(353, n, 0.0, 0.02)
         for fmt, b, scale, scales, ref in _cases(orc, w, k, n, a):
             got = _gemm(fmt, m, n, k, a, b, scale, scales, bias)
             err = rel_err(got, ref + bias)

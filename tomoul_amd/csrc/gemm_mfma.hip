@@ -607,19 +607,17 @@ Status launch_fmt(const MatmulArgs &m, hipStream_t s, int cus) {
 
 GemmPlan plan_gemm(const MatmulArgs &m) {
     GemmPlan p;
-    // Q8_0 / Q4_0 (per-tensor or per-column scales) take the bf16
-    // matrix-core kernel whenever its layout conditions hold (gemm_qbf.hip),
-    // unless TML_GEMM_QBF=0 or an override asks for a tile or K split of the
-    // fp32-MFMA kernels below (tests of those kernels).
+    // Q8_0 / Q4_0 (per-tensor or per-column scales) past the GEMV rows take
+    // the bf16 matrix-core kernel whenever its layout conditions hold
+    // (gemm_qbf.hip), unless TML_GEMM_QBF=0 or an override asks for a tile or
+    // K split of the fp32-MFMA kernels below (tests of those kernels).
     auto set = [](const char *k) {
         const char *v = std::getenv(k);
         return v != nullptr && *v != '\0';
     };
     const bool fp32_forced = set("TML_GEMM_DMA_Q") || set("TML_GEMM_TILE") || set("TML_GEMM_DMA_TILE") ||
                              set("TML_GEMM_SPLIT");
-    if (!fp32_forced && gemm_qbf_supported(m) && (m.M >= 128 || env_int("TML_GEMM_QBF", 1) == 2 ||
-                                                  env_int("TML_GEMM_QBF_TILE", 0) > 0 ||
-                                                  env_int("TML_GEMM_QBF_SPLIT", 0) > 0)) {
+    if (!fp32_forced && gemm_qbf_supported(m)) {
         p.qbf = true;
         pick_qbf(m, &p);
         return p;

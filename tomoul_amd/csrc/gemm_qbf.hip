@@ -577,7 +577,17 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
         if (real > 1) t += per_split * (double)(real - 1) + traffic * (double)real * (double)m.M * (double)m.N * 8.0 / 6.0e6;
         return t;
     };
-    if (m.M <= 512 && tiles_of(7) <= 4LL * cus) {
+    if (m.M < 128) {
+        // 32 x 64 x 64 tiles with two wave groups (config 7) and the largest
+        // K split s <= 4 that keeps tiles x s within the CUs and >= 8 32-deep
+        // slices a split: the best plan of a 60-point sweep (M = 16-112 at
+        // ten encoder / decoder shapes) within 3 % at all but two points
+        // (e.g. 48 x 4096 x 1024 9.9 us, 16 x 4096 x 1024 8.6 us; the fp32
+        // kernels took 17.5 and 10.2 us)
+        cfg = 7;
+        for (int64_t ns = 2; ns <= 4; ++ns)
+            if (tiles_of(7) * ns <= cus && split_ok(ns)) nsplit = ns;
+    } else if (m.M <= 512 && tiles_of(7) <= 4LL * cus) {
         // 64 x 64 x 64 or 32 x 64 x 64 tiles with two wave groups (configs 6,
         // 7) and K split s in 1..4 of least modelled time, c = 0.60 / 0.45 us
         // a 64-deep slice-unit at 64 x 64 for u = 1 / u >= 2, 0.35 / 0.25 at
