@@ -129,10 +129,11 @@ int tml_hip_sgemv(int64_t M, int64_t N, const float *A, const float *x, float *y
  * scale, c) at src/core/quantization.zig:236 (matmulF32Q8Simd, :207-314). */
 int tml_hip_sgemm_q8(int64_t M, int64_t N, int64_t K, const float *A, const int8_t *Bq, float scale, float *C);
 /* Arithmetic of the Q8_0 / Q4_0 products (every entry point and format,
- * per-column forms included): from M = 128 rows (K a multiple of 8, even N)
- * they run on the bf16 matrix cores, the int weights exact in bf16 and each
- * fp32 activation split into two bf16 terms (|x - hi - lo| <= 2^-17 |x|),
- * accumulated in fp32; below that on fp32 multiply-adds.  Both agree with
+ * per-column forms included): past the decoder rows (M > 8; K a multiple of
+ * 8, even N) they run on the bf16 matrix cores, the int weights exact in
+ * bf16 and each fp32 activation split into two bf16 terms
+ * (|x - hi - lo| <= 2^-17 |x|), accumulated in fp32; otherwise on fp32
+ * multiply-adds.  Both agree with
  * the reference's dequantize-then-fp32-accumulate result to ~1e-5 relative;
  * infinities and NaNs in A give what the reference gives.  Limit: the
  * per-tensor scale multiplies the finished sum (the reference multiplies
