@@ -11,7 +11,7 @@ overflow or other undefined behaviour aborts the case.
 * test_planted_mistakes: a B operand 16 bytes short must be reported for
   every kernel family (the harness itself works);
 * test_cases: every kernel family, tile config (TML_GEMM_DMA_TILE 1-10,
-  TML_GEMM_TILE 1-10, TML_GEMM_QBF_TILE 1-10), K split (1, 2, 3, 4, 8),
+  TML_GEMM_TILE 1-10, TML_GEMM_QBF_TILE 1-11), K split (1, 2, 3, 4, 8),
   format, epilogue and the fused split-K exchange, on shapes with ragged
   edges in M, N and K;
 * test_fault_sweep_replay (TML_EMU_FULL=1): every (format, shape, forced
@@ -97,7 +97,7 @@ def _default_cases():
         if fmt in (Q8_0, Q4_0, Q8_0_PC, Q4_0_PC):
             # the bf16 matrix-core kernel: every tile, K split or not (K a
             # multiple of 8 here), and the planner's own choice
-            for tile in range(1, 11):
+            for tile in range(1, 12):
                 for split in (1, 3):
                     cs.append(f"gemm {fmt} {M} {N} {K - K % 8 + 8} br TML_GEMM_QBF=2 TML_GEMM_QBF_TILE={tile} "
                               f"TML_GEMM_QBF_SPLIT={split}")

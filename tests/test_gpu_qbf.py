@@ -57,10 +57,11 @@ def _gemm(fmt, m, n, k, a, b, scale, scales, bias=None):
     return c
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11])
 def test_qbf_tiles_vs_oracle(orc, env, tile):
-    # Every tile config (0: the planner's choice; 5-8 on 64-deep slices, 7
-    # and 8 with two wave groups, 9 and 10 with eight waves) on
+    # Every tile config (0: the planner's choice; 5-8 and 11 on 64-deep
+    # slices, 7, 8 and 11 with two wave groups, 11 with four slices of loads
+    # in flight, 9 and 10 with eight waves) on
     # shapes ragged in M and N (partial tiles, N not a multiple of 16), K
     # from one slice to many and not a multiple of 64, with a bias.
     env["TML_GEMM_QBF"] = "2"
@@ -93,10 +94,10 @@ def test_qbf_small_m_default_plan(orc, env, m):
 
 
 @pytest.mark.parametrize("split", [2, 3, 5])
-@pytest.mark.parametrize("tile", [1, 2, 4, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 4, 6, 7, 8, 9, 10, 11])
 def test_qbf_split_vs_oracle(orc, env, tile, split):
     # K split over workgroups (each over its own range of 32-deep slices,
-    # whole 64-deep ones for tiles 6-8, the last range short), raw partials
+    # whole 64-deep ones for tiles 5-8 and 11, the last range short), raw partials
     # summed in split order by the reduce launch, which runs the epilogue:
     # bias and residual here.
     env["TML_GEMM_QBF_TILE"] = str(tile)
@@ -199,7 +200,7 @@ def test_qbf_off_switch_agrees(orc, env):
         assert rel_err(got, ref) <= TOL and rel_err(old, ref) <= 1e-5 and rel_err(got, old) <= TOL, fmt
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11])
 def test_qbf_staged_epilogue(orc, env, tile):
     # With N a multiple of 4 and 16-byte aligned operands the tiles whose C
     # tile fits the staging buffer in one pass (tiles 4-8: 32 x 64, and

@@ -491,10 +491,12 @@ struct QbfCfg {
 // three / two workgroups a CU): the planner takes them for every shape past
 // the small-tile rules (us, Q8_0, four / eight waves: 1500x3840x1280 at
 // 64 x 128 48.9 / 45.2, 1500x5120x1280 at 128 x 128 62.9 / 53.5,
-// 3000x3840x1280 at 128 x 128 105.5 / 80.4).
+// 3000x3840x1280 at 128 x 128 105.5 / 80.4).  Config 10 is config 7 with
+// four 64-deep slices of loads in flight (D = 4), which the planner takes
+// where each unit has a CU to itself and K rounds to whole groups of four.
 constexpr QbfCfg kQbfCfgs[] = {{128, 128, 32, 1, 4}, {64, 128, 32, 1, 4}, {64, 64, 32, 1, 4}, {32, 64, 32, 1, 4},
                                {64, 64, 64, 1, 4},   {32, 64, 64, 1, 4},  {64, 64, 64, 2, 8}, {32, 64, 64, 2, 8},
-                               {64, 128, 32, 1, 8},  {128, 128, 32, 1, 8}};
+                               {64, 128, 32, 1, 8},  {128, 128, 32, 1, 8}, {32, 64, 64, 2, 8}};
 constexpr int kQbfNumCfgs = (int)(sizeof(kQbfCfgs) / sizeof(kQbfCfgs[0]));
 
 template <int FMT>
@@ -509,7 +511,8 @@ void launch_qbf_cfg(int cfg, unsigned grid, const QbfArgs &a, hipStream_t s) {
         case 6: gemm_qbf_kernel<FMT, 64, 64, 32, 32, 2, 64, 2><<<grid, 512, 0, s>>>(a); break;
         case 7: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 2, 64, 2><<<grid, 512, 0, s>>>(a); break;
         case 8: gemm_qbf_kernel<FMT, 64, 128, 32, 32, 2, 32, 1, 8><<<grid, 512, 0, s>>>(a); break;
-        default: gemm_qbf_kernel<FMT, 128, 128, 64, 32, 2, 32, 1, 8><<<grid, 512, 0, s>>>(a); break;
+        case 9: gemm_qbf_kernel<FMT, 128, 128, 64, 32, 2, 32, 1, 8><<<grid, 512, 0, s>>>(a); break;
+        default: gemm_qbf_kernel<FMT, 32, 64, 16, 32, 4, 64, 2><<<grid, 512, 0, s>>>(a); break;
     }
 }
 
@@ -593,10 +596,14 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
         // a 64-deep slice-unit at 64 x 64 for u = 1 / u >= 2, 0.35 / 0.25 at
         // 32 x 64, plus 1.0 us a split past the first and half the
         // partials' traffic at 6 TB/s
+        // (a split that takes the units past the CUs needs >= 24 slices a
+        // split: at 128 x 3840 x 1280, Q4_0 128 x 5120 x 1280 and 192 x 3840 x
+        // 1280 the model's two splits measured 1.6-1.9 us above one)
         static const double c_one[] = {0.60, 0.35}, c_many[] = {0.45, 0.25};
         double best = 1e300;
         for (int i = 0; i < 2; ++i)
             for (int64_t ns = 1; ns <= 4 && split_ok(ns); ++ns) {
+                if (ns > 1 && tiles_of(6 + i) * ns > cus && nk / ns < 24) continue;
                 const double t = modelled(6 + i, ns, c_one[i], c_many[i], 1.0, 0.5);
                 if (t < best) {
                     best = t;
@@ -620,6 +627,18 @@ void pick_qbf(const MatmulArgs &m, GemmPlan *p) {
                 }
             }
     }
+    if (cfg == 7) {
+        // Four 64-deep slices of loads in flight instead of two (config 10)
+        // where every unit has a CU to itself and a split's steps fill whole
+        // rounds of four, bar one: on a 60-point sweep (M = 16-256) this took
+        // 128 x 4096 x 1024 from 10.42 to 9.92 us, 128 x 3840 x 1280 11.90 ->
+        // 11.09, Q4_0 16 x 1280 x 5120 14.49 -> 13.84; with two CUs' worth of
+        // units, or steps rounded up by two or three, it measured slower
+        // (1536 x 384, 6 steps: 6.1 -> 6.5 us).
+        const int64_t spl = ((nk + nsplit - 1) / nsplit + 1) / 2 * 2;
+        const int64_t n64 = spl / 2, real = (nk + spl - 1) / spl;
+        if (tiles_of(7) * real <= cus && n64 >= 7 && (n64 % 4 == 0 || n64 % 4 == 3)) cfg = 10;
+    }
     const int forced_tile = env_int("TML_GEMM_QBF_TILE", 0) - 1;
     if (forced_tile >= 0 && forced_tile < kQbfNumCfgs) cfg = forced_tile;
     const int forced = env_int("TML_GEMM_QBF_SPLIT", 0);
@@ -638,11 +657,11 @@ bool gemm_qbf_supported(const MatmulArgs &m) {
     if (m.fmt != TML_FMT_Q8_0 && m.fmt != TML_FMT_Q4_0) return false;
     if (m.M <= kGemvMaxM || m.K <= 0 || m.K % 8 != 0 || m.N % 2 != 0 || ((uintptr_t)m.A % 16) != 0) return false;
     if (env_int("TML_GEMM_QBF", 1) == 0) return false;
-    // every buffer offset below 2^31: A rows up to M + 128, B k-rows up to K + 288
+    // every buffer offset below 2^31: A rows up to M + 128, B k-rows up to K + 544
     const uint64_t lim = (uint64_t)1 << 31;
     const uint64_t ldb = m.fmt == TML_FMT_Q8_0 ? (uint64_t)m.N : (uint64_t)m.N / 2;
-    // (the loads run up to 2 x 4 slices past K, zero-filled)
-    return (uint64_t)(m.M + 128) * (uint64_t)m.K * 4u < lim && (uint64_t)(m.K + 288) * ldb < lim &&
+    // (the loads run up to 2 D slices of BK past K, zero-filled: 512 at D = 4, BK = 64)
+    return (uint64_t)(m.M + 128) * (uint64_t)m.K * 4u < lim && (uint64_t)(m.K + 544) * ldb < lim &&
            m.M < ((int64_t)1 << 30) && m.N < ((int64_t)1 << 30);
 }
 
