@@ -48,12 +48,12 @@ HBM_PEAK_GBS = 8000.0
 
 
 def qgemm_peak(M: int) -> dict:
-    """Roofline of a Q8_0 / Q4_0 GEMM of M rows: from M = 128 on the bf16
-    matrix-core kernel (gemm_qbf.hip), which issues two bf16 MFMAs per
-    product (activation hi + lo), so its MFMA work is twice the algorithmic
-    flops against the dense bf16 peak; below, the fp32-MFMA kernels against
-    the fp32 peak."""
-    if M >= 128:
+    """Roofline of a Q8_0 / Q4_0 GEMM of M rows: past the GEMV rows (M > 8)
+    the bf16 matrix-core kernel (gemm_qbf.hip), which issues two bf16 MFMAs
+    per product (activation hi + lo), so its MFMA work is twice the
+    algorithmic flops against the dense bf16 peak; at M <= 8 the GEMV
+    kernels, here priced against the fp32 peak."""
+    if M > 8:
         return {"kernel": "bf16 MFMA, hi + lo activation terms", "peak": BF16_PEAK_TFLOPS, "mfma_per_flop": 2}
     return {"kernel": "fp32 MFMA", "peak": FP32_PEAK_TFLOPS, "mfma_per_flop": 1}
 
@@ -1100,7 +1100,7 @@ def attach_cpu_quantized(result):
     for key, v in cq.items():
         name, m = key.rsplit("_M", 1)
         M = int(m)
-        if name.startswith("q8_") and M >= 128:
+        if name.startswith("q8_") and M > 8:
             e = result.get("qgemm", {}).get(f"q8_M{M}")
             gpu_us = e and e.get("us")
         else:

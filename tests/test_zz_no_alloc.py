@@ -108,7 +108,7 @@ def test_oversized_plan_is_refused(env):
 @pytest.mark.parametrize("fmt", [_abi.FMT_Q8_0, _abi.FMT_Q4_0])
 def test_default_plan_too_large_is_refused_not_shrunk(env, fmt):
     """Whisper FFN-down (1500 x 1280 x 5120) in Q8_0 / Q4_0: the bf16 GEMM's
-    default plan splits K three ways, 3 * 1500 * 1280 floats = 23 MB of
+    default plan splits K four ways, 4 * 1500 * 1280 floats = 31 MB of
     partial sums, more than the static scratch.  The allocation-free call
     refuses it rather than running a smaller split with other bits; the
     allocating call runs that plan (TML_REQUIRE_SPLIT=1 shows it splits)."""
