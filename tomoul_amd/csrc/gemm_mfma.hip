@@ -518,6 +518,19 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
     const double *const t_many = fmt == TML_FMT_F16 ? f16_many : fmt == TML_FMT_Q8_K ? q8k_many : f32_many;
     static const int splits[] = {1, 2, 3, 4, 6, 8};
     constexpr double kFill = 3.5, kReduce = 3.6, kBytesPerUs = 6.0e6;
+    // Below 128 rows (f32): the 32-row tiles run alone on their CUs, a slice
+    // costs 0.25 us (32x64, BK 32 or 64) or 0.20 (32x64 two groups), the
+    // 64-deep tiles fill 0.75 us longer, and the reduce launch costs 1.5 us
+    // plus its traffic -- fitted to a sweep of the three 32x64 tiles x K
+    // split 1-4 over M = 16, 32, 64, 96 and eight N x K (4096 x 1024 to 384 x
+    // 1536); there the planner takes those three tiles only, with >= 3 slices
+    // a split.  Measured with the rule on the sweep's 32 shapes: 344.2 ->
+    // 332.8 us in sum, against 332.2 for the best measured plan of each (32
+    // x 3072 x 768 10.89 -> 8.42, 64 x 4096 x 1024 13.46 -> 11.69 us; 16 x
+    // 3840 x 1280 and 96 x 1024 x 4096 lost 0.5 / 0.6 us).
+    const bool small = M < 128 && fmt == TML_FMT_F32;
+    static const double small_one[] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.25, 0.25, 0.0, 0.20};
+    static_assert(sizeof(small_one) == sizeof(f32_one), "one small-M entry per tile config");
     const int cus = device_cus();
     int forced_tile = env_int("TML_GEMM_DMA_TILE", 0) - 1;
     if (!gemm_dma_cfg_ok(forced_tile, fmt)) forced_tile = -1;  // unset, or no kernel for this format
@@ -526,21 +539,24 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
     for (int c = 0; c < gemm_dma_num_cfgs(); ++c) {
         if (c >= (int)(sizeof(f32_one) / sizeof(f32_one[0]))) break;  // no cost model for this config
         if ((forced_tile >= 0 && c != forced_tile) || !gemm_dma_cfg_ok(c, fmt)) continue;
+        if (small && forced_tile < 0 && small_one[c] == 0.0) continue;  // the fitted 32-row tiles only
         int bm = 0, bn = 0, bk = 32;
         gemm_dma_tile(c, &bm, &bn, &bk);
         const int64_t nk = (K + bk - 1) / bk;
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         for (int sp : splits) {
             if (forced_split > 0 && sp != forced_split) continue;
-            if (sp > 1 && nk < 2 * sp) continue;
+            if (sp > 1 && nk < (small && forced_split <= 0 ? 3 : 2) * sp) continue;
             if (narrow_table && sp > 2 && forced_split <= 0) break;  // the narrow tables were fitted on s <= 2
             const int64_t spl = nk > 0 ? (nk + sp - 1) / sp : 1;
             const int64_t real = nk > 0 ? (nk + spl - 1) / spl : 1;
             const int64_t units = tiles * real;
             const int64_t per_cu = (units + cus - 1) / cus;
-            const double red = real > 1 ? kReduce + (double)real * M * N * 8.0 / kBytesPerUs : 0.0;
-            const double ts = per_cu > 1 ? t_many[c] : t_one[c];
-            const double t = (double)per_cu * (double)spl * (bk / 32.0) * ts + kFill + red;
+            const double red = real > 1 ? (small ? 1.5 : kReduce) + (double)real * M * N * 8.0 / kBytesPerUs : 0.0;
+            const double one = small && small_one[c] > 0.0 ? small_one[c] : t_one[c];
+            const double ts = per_cu > 1 ? t_many[c] : one;
+            const double fill = kFill + (small && bk == 64 ? 0.75 : 0.0);
+            const double t = (double)per_cu * (double)spl * (bk / 32.0) * ts + fill + red;
             if (t < best_t) {
                 best_t = t;
                 p->cfg = c;
