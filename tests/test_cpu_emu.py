@@ -127,7 +127,7 @@ def _default_cases():
                         for t in (1, 2):
                             cs.append(f"prep {fmt} {M} 40 2080 b TML_GEMVTM_NW={nw} TML_GEMVTM_IT={it} "
                                       f"TML_GEMVTM_T={t} TML_GEMVTM_PF={(nw + it + t) % 2}")
-            # the staged-activation GEMV (M <= 2): both thread counts, every
+            # the staged-activation GEMV (M <= 2; 3-4 below): both thread counts, every
             # layer count, rows ragged against the layers, long rows (224 /
             # 384 chunks, activations near the 64 KiB of LDS the kernel may
             # use at M = 2) and the shortest (one chunk)
@@ -139,6 +139,12 @@ def _default_cases():
                         cs.append(f"prep {fmt} {M} 997 1280 br TML_GEMVX=3 TML_GEMVX_NT={nt} TML_GEMVX_P={pl}")
                 cs.append(f"prep {fmt} {M} 37 {big} bt TML_GEMVX=3")
                 cs.append(f"prep {fmt} {M} 7 {one} b TML_GEMVX=3 TML_GEMVX_P=4")
+            # three and four rows (three computed as four, the fourth zero)
+            for M in (3, 4):
+                for pl in (1, 4):
+                    cs.append(f"prep {fmt} {M} 997 1280 br TML_GEMVX=3 TML_GEMVX_NT=512 TML_GEMVX_P={pl}")
+                cs.append(f"prep {fmt} {M} 37 3072 bt TML_GEMVX=3")
+                cs.append(f"prep {fmt} {M} 7 {one} b TML_GEMVX=3")
             # rows split over two workgroups (grid.y), odd row counts included
             for M in (5, 7, 8):
                 cs.append(f"prep {fmt} {M} 2050 1280 br TML_GEMVTM_MSPLIT=2")

@@ -1,5 +1,5 @@
 """The staged-activation decoder GEMV (gemv_x.hip): Q8_0 / Q4_0 at M = 1 and
-2 on prepared weights, against the oracle (the reference's
+2 on prepared weights (and at 3-4 rows), against the oracle (the reference's
 dequantize-then-f32-accumulate loops, quantization.zig:158-203 and
 :778-824).  TML_GEMVX=3 makes every such call refuse any other kernel, so
 each case proves that this one ran.  Covered: the decoder shapes of configs 3
@@ -96,6 +96,30 @@ def test_vs_oracle(orc, env, fmt, k, n, m):
     assert err <= TOL, err
 
 
+# Shapes the kernel takes at 3-4 rows: activations and partials within its
+# 64 KiB of LDS.
+MORE = [(_abi.FMT_Q8_0, 1024, 4096, (3, 4)), (_abi.FMT_Q4_0, 1280, 5120, (3, 4)),
+        (_abi.FMT_Q8_0, 1280, 5120, (4,)), (_abi.FMT_Q8_0, 16, 1001, (3,)), (_abi.FMT_Q4_0, 32, 7, (4,)),
+        (_abi.FMT_Q4_0, 224, 1000, (3, 4)), (_abi.FMT_Q8_0, 1280, 51866, (4,)), (_abi.FMT_Q4_0, 1280, 51866, (4,)),
+        (_abi.FMT_Q8_0, 2048, 333, (3, 4)), (_abi.FMT_Q4_0, 3072, 768, (3, 4))]
+
+
+@pytest.mark.parametrize("fmt,k,n,ms", MORE, ids=[f"{'q8' if f == 1 else 'q4'}_{k}x{n}" for f, k, n, _ in MORE])
+def test_more_rows(orc, env, fmt, k, n, ms):
+    # 3-4 activation rows: M rounded up to 4 in registers, the rows past M
+    # zero and dropped
+    w = synth.normal_matrix(305, k, n, 0.02)
+    q, s = _quant(orc, fmt, w)
+    B, h = _prepared(fmt, q, s, k, n)
+    try:
+        for m in ms:
+            a = synth.normal_matrix(306 + m, m, k)
+            err = rel_err(_run(h, m, n, a), _ref(orc, fmt, a, q, s, k, n))
+            assert err <= TOL, (m, err)
+    finally:
+        _abi.prepared_free(h)
+
+
 @pytest.mark.parametrize("nt", ["256", "512"])
 @pytest.mark.parametrize("p", ["1", "2", "3", "4"])
 def test_plans(orc, env, nt, p):
@@ -122,7 +146,7 @@ def test_epilogue(orc, env, fmt):
     q, s = _quant(orc, fmt, w)
     B, h = _prepared(fmt, q, s, k, n)
     try:
-        for m in (1, 2):
+        for m in (1, 2, 4):
             a = synth.normal_matrix(322 + m, m, k)
             bias = synth.normal(324, n, 0.0, 0.5)
             res = synth.normal_matrix(325, m, n)
@@ -146,7 +170,7 @@ def test_column_scales(orc, env, fmt):
     Q, S = _dev(q), _dev(sc)
     h = _abi.prepare_ex_dev(fmt, k, n, Q.data_ptr(), scales_ptr=S.data_ptr())
     try:
-        for m in (1, 2):
+        for m in (1, 2, 4):
             a = synth.normal_matrix(333 + m, m, k)
             err = rel_err(_run(h, m, n, a), orc.matmul_cols(a, fmt, q, sc, k, n))
             assert err <= TOL, (m, err)
@@ -166,11 +190,11 @@ def test_inf_nan(orc, env, fmt):
     q, s = _quant(orc, fmt, w)
     B, h = _prepared(fmt, q, s, k, n)
     try:
-        for m, pos in ((1, [(0, 5)]), (2, [(1, 5), (1, 700)])):
+        for m, pos in ((1, [(0, 5)]), (2, [(1, 5), (1, 700)]), (4, [(1, 5), (3, 700)])):
             a = synth.normal_matrix(342 + m, m, k)
             for (i, j) in pos:
                 a[i, j] = np.inf
-            if m == 2:
+            if m >= 2:
                 a[1, 700] = -np.inf
                 a[0, 9] = np.nan
             got = _run(h, m, n, a)

@@ -678,11 +678,11 @@ Status launch_gemv_t(int fmt, int64_t M, int64_t N, int64_t K, const float *A, c
         return Status::Err(TML_ERR_INVALID_SHAPE, "GEMV dimension exceeds 2^30");
     if (ldt < prepared_row_bytes(fmt, K) || ldt % 16 != 0 || ((uintptr_t)Bt % 16) != 0)
         return Status::Err(TML_ERR_INVALID_ARG, "prepared weight layout");
-    // Q8_0 / Q4_0 at M <= 2 with the activations staged per workgroup
+    // Q8_0 / Q4_0 at M <= 4 with the activations staged per workgroup
     // (gemv_x.hip) where gemv_x_preferred finds it the faster kernel.
     if (gemv_x_preferred(fmt, M, N, K) && ((uintptr_t)A % 16) == 0)
         return launch_gemv_x(fmt, M, N, K, A, Bt, ldt, bias, res, C, alpha_eff, beta, act, tail0, colscale, s);
-    if (M <= 2 && env_int("TML_GEMVX", 1) == 3)
+    if (env_int("TML_GEMVX", 1) == 3)
         return Status::Err(TML_ERR_INVALID_ARG, "TML_GEMVX=3: this call does not take the staged-activation GEMV");
     // Q8_0 / Q4_0 on the matrix cores (gemv_tm.hip) where it is the faster
     // kernel (M >= 3, short Q4_0 rows at M = 2, Q4_0 vocabularies at M = 1) and its

@@ -1,4 +1,4 @@
-// gemv_x.hip -- decoder GEMV at M <= 2 on prepared Q8_0 / Q4_0 weights,
+// gemv_x.hip -- decoder GEMV at M <= 4 on prepared Q8_0 / Q4_0 weights,
 // activations staged once per workgroup.
 //
 //   C[M,N] = act((alpha * A[M,K] . Bdeq[K,N] + beta * C + bias[N]) + residual)
@@ -161,11 +161,15 @@ __global__ __launch_bounds__(NT) void gemv_x_kernel(GemvXArgs a) {
     //    be in flight), then the lane's activations into registers.
     x_wait_vmcnt<P>();
     x_barrier();
+    // (rows past M, when M is rounded up to MR, hold zeros: their products
+    // are computed and dropped)
     floatx4 xr[MR][E / 4];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int q = 0; q < E / 4; ++q) xr[m][q] = *(const floatx4 *)(xs + m * a.K + x_group_k(c, q, a.nchunk, E));
+        for (int q = 0; q < E / 4; ++q)
+            xr[m][q] = (MR <= 2 || m < a.M) ? *(const floatx4 *)(xs + m * a.K + x_group_k(c, q, a.nchunk, E))
+                                           : floatx4{0.f, 0.f, 0.f, 0.f};
 
     // 4. Dot products of the lane's chunk, layer by layer as the weights
     //    arrive: two chains per row, then their sum.
@@ -239,6 +243,9 @@ struct XPlan {
 
 int x_elems(int fmt) { return fmt == TML_FMT_Q8_0 ? 16 : 32; }
 
+// Rows a launch computes: M rounded up to 1, 2 or 4.
+int x_rows(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
+
 bool x_plan(int fmt, int64_t M, int64_t N, int64_t K, int cus, XPlan *out) {
     const int E = x_elems(fmt);
     const int64_t nchunk = K / E;
@@ -265,7 +272,7 @@ bool x_plan(int fmt, int64_t M, int64_t N, int64_t K, int cus, XPlan *out) {
     if (forced_p >= 1 && forced_p <= 4) p.p = forced_p;
     // activations and partials within 64 KiB of LDS: fewer layers if need be
     p.xiters = (int)((M * K / 4 + p.nt - 1) / p.nt);
-    auto lds_of = [&](int layers) { return (size_t)p.xiters * p.nt * 16 + (size_t)layers * M * p.nt * 4; };
+    auto lds_of = [&](int layers) { return (size_t)p.xiters * p.nt * 16 + (size_t)layers * x_rows(M) * p.nt * 4; };
     while (p.p > 1 && lds_of(p.p) > 64 * 1024) --p.p;
     p.lds = lds_of(p.p);
     if (p.lds > 64 * 1024) return false;
@@ -290,18 +297,21 @@ void x_launch_nt(const GemvXArgs &ka, const XPlan &p, unsigned grid, hipStream_t
 template <int FMT>
 void x_launch_m(const GemvXArgs &ka, const XPlan &p, unsigned grid, hipStream_t s) {
     if (ka.M == 1) x_launch_nt<FMT, 1>(ka, p, grid, s);
-    else x_launch_nt<FMT, 2>(ka, p, grid, s);
+    else if (ka.M == 2) x_launch_nt<FMT, 2>(ka, p, grid, s);
+    else x_launch_nt<FMT, 4>(ka, p, grid, s);
 }
 
 }  // namespace
 
-// What the kernel runs: Q8_0 / Q4_0 at M = 1 or 2, K a whole number of
+// What the kernel runs: Q8_0 / Q4_0 at M = 1 to 4 (3 as 4), K a whole number of
 // chunks (so every activation a lane reads belongs to its row), at most 512
 // chunks a row, activations and partials within 64 KiB of LDS (M * K up to
 // about 15000), and every buffer offset below 2^31.
 bool gemv_x_capable(int fmt, int64_t M, int64_t N, int64_t K) {
     if (fmt != TML_FMT_Q8_0 && fmt != TML_FMT_Q4_0) return false;
-    if (M < 1 || M > 2 || K <= 0 || N <= 0 || K % x_elems(fmt) != 0) return false;
+    // (at 5-8 rows it measured slower than the matrix-core kernel on every
+    // shape tried, 0.2-1.1 us at 1024 x 4096, 1024 x 2048, 1280 x 1280)
+    if (M < 1 || M > 4 || K <= 0 || N <= 0 || K % x_elems(fmt) != 0) return false;
     XPlan p;
     if (!x_plan(fmt, M, N, K, 256, &p)) return false;
     const int64_t ldt = prepared_row_bytes(fmt, K);
@@ -313,25 +323,40 @@ bool gemv_x_capable(int fmt, int64_t M, int64_t N, int64_t K) {
 // >= 1 GiB, weights streamed with the non-temporal policy, us):
 //   * Q4_0 at M = 1 at every N (1280x5120 3.27 against 3.48, 5120x1280 3.42
 //     against 3.70, vocabulary 1280x51866 10.27 against 10.82 on the matrix
-//     cores, 2048x51866 13.66 against 15.34), and at M = 2 on rows of more
-//     than 64 chunks below N = 32768 (5120x1280 4.29 against 5.33, before
-//     the non-temporal policy); short rows at M = 2 stay on the matrix cores
-//     (1280x51866 14.16 against 11.03; 1280x5120 4.37 against 4.04 before
-//     the policy);
+//     cores, 2048x51866 13.66 against 15.34), at M = 2 below N = 32768
+//     (2048x2048 3.29 against 4.17, 1280x1280 2.86 against 3.48, 5120x1280
+//     4.29 against 5.33 before the non-temporal policy; 1280x5120, 1024x4096
+//     within 0.05; the vocabulary 14.11 against 10.99 stays on the matrix
+//     cores), and at M = 3-4 where N <= 2048 and K >= N, the matrix-core
+//     kernel's 16-column tiles being few (3072x768 4.28 / 4.36 against
+//     5.79 / 5.14, 2048x2048 3.84 / 3.93 against 4.66 / 4.21; 1280x2048 and
+//     1024x4096 0.2-0.6 slower);
 //   * Q8_0 from N = 12288 at M = 1 (1024x12288 4.49 against 5.05, vocabulary
-//     1280x51866 13.22 against 13.94; below it the per-lane kernel: 1024x4096
-//     2.85 against 3.08, 1024x8192 3.65 against 3.79) and from N = 8192 at
-//     M = 2 (1024x8192 4.17 against 4.70, 1280x51866 16.46 against 19.30;
-//     1024x4096 3.17 against 3.31 on the per-lane kernel).
+//     1280x51866 13.22 against 13.94) and from N = 8192 at M = 2 (1024x8192
+//     4.17 against 4.70, 1280x51866 16.46 against 19.30); at M <= 2 also
+//     where a row's chunks leave 1-16 over a multiple of 64, which idles most
+//     of the per-lane kernel's last 64-lane group (K = 1280: 1280x1280 2.82 /
+//     2.96 against 2.97 / 3.57, 1280x5120 3.76 / 4.06 against 3.95 / 4.88);
+//     elsewhere below those N the per-lane kernel (1024x4096 2.82 / 3.16
+//     against 3.06 / 3.30, 768x3072, 512x4096, 3072x768); at M = 3-4 from
+//     K = 1024 up to N = 4096 (1024x4096 3.89 / 4.01 against 4.23 / 4.40,
+//     3072x768 4.07 / 4.23 against 6.16 / 5.50, 2048x2048 3.88 / 4.09 against
+//     5.22 / 4.74; 768x3072, 1280x5120, 1536x6144 0.1-1.5 slower).
 // TML_GEMVX=0 turns it off; TML_GEMVX=2 takes it wherever it can run, and
-// TML_GEMVX=3 also makes the prepared GEMV refuse an M <= 2 call it cannot
-// take (tests).
+// TML_GEMVX=3 also makes the prepared GEMV refuse a call it cannot take
+// (tests).
 bool gemv_x_preferred(int fmt, int64_t M, int64_t N, int64_t K) {
     const int mode = env_int("TML_GEMVX", 1);
     if (mode == 0 || !gemv_x_capable(fmt, M, N, K)) return false;
     if (mode >= 2) return true;
-    if (fmt == TML_FMT_Q4_0) return M == 1 || (N < 32768 && K / 32 > 64);
-    return N >= (M == 1 ? 12288 : 8192);
+    const int64_t tail = (K / x_elems(fmt)) % 64;
+    if (fmt == TML_FMT_Q4_0) {
+        if (M == 1) return true;
+        if (M == 2) return N < 32768;
+        return N <= 2048 && K >= N;
+    }
+    if (M <= 2) return N >= (M == 1 ? 12288 : 8192) || (tail > 0 && tail <= 16);
+    return K >= 1024 && N <= 4096;
 }
 
 Status launch_gemv_x(int fmt, int64_t M, int64_t N, int64_t K, const float *A, const void *Bt, int64_t ldt,
