@@ -138,9 +138,10 @@ int tml_hip_sgemm_q8(int64_t M, int64_t N, int64_t K, const float *A, const int8
  * infinities and NaNs in A give what the reference gives.  Limit: the
  * per-tensor scale multiplies the finished sum (the reference multiplies
  * each element, a * (q * s)), so finite activations large enough that
- * x * q overflows fp32 (|x| > FLT_MAX / 127 for int8, / 8 for int4) -- and on
- * the matrix cores any finite |x| above the largest bf16, 3.39e38, whose hi
- * term rounds to inf -- give inf or NaN where the reference stays finite. */
+ * x * q overflows fp32 (|x| > FLT_MAX / 127 for int8, / 8 for int4) give
+ * inf or NaN where the reference stays finite.  On the matrix cores hi is
+ * taken from x clamped to the largest finite bf16, so a finite x near
+ * FLT_MAX keeps a finite product where q is 0 or +-1. */
 
 /* C = A . dequant(Q8_K B).  Replaces zblas.sgemmQ8K(m, n, k, a, b.data,
  * b.scales, b.block_size, c) at src/core/quantization.zig:555

@@ -286,6 +286,7 @@ inline tml_emu_f32x4 __builtin_amdgcn_mfma_f32_16x16x32_bf16(tml_emu_bf16x8, tml
                                                             int) {
     return c;
 }
+inline float __builtin_amdgcn_fmed3f(float a, float b, float c) { return a < b ? b : (a > c ? c : a); }
 inline int __builtin_amdgcn_update_dpp(int, int src, int, int, int, bool) { return src; }
 inline int __builtin_amdgcn_ds_swizzle(int v, int) { return v; }
 

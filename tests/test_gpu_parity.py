@@ -799,25 +799,42 @@ def test_prepared_matrix_core_vocabulary(orc, gemvx):
 
 @pytest.mark.parametrize("m", [3, 8])
 def test_prepared_matrix_core_inf(orc, m):
-    # Infinite and NaN activations through the matrix-core GEMV: each output
-    # is inf, -inf or nan exactly where the reference's fp32 product is, and
-    # the other rows are untouched.
+    # Infinite and NaN activations through the matrix-core GEMV (the
+    # staged-activation kernel, which would take M = 3 here, switched off):
+    # each output is inf, -inf or nan exactly where the reference's fp32
+    # product is, and the other rows are untouched.  Row 0 carries finite
+    # activations above the largest bf16 on weight rows that quantize to 0
+    # and +-1: finite outputs within the bound.
     k, n = 1280, 300
     w = rnd(221, k, n, 0.02)
+    w[40] = 0.0
+    w[41] = np.where(np.arange(n) % 3 == 0, -0.75, 0.75) * np.abs(w).max(axis=0) / 127.0
     q, s = orc.quantize_q8(w)
     p, s4 = orc.quantize_q4(w)
     a = rnd(222, m, k)
     a[1, 5] = np.inf
     a[1, 700] = -np.inf
     a[2, 9] = np.nan
-    for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
-                               (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
-        got = _run_prepared(fmt, b, scale, k, n, m, a)
-        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
-        np.testing.assert_array_equal(np.isposinf(got), np.isposinf(ref))
-        np.testing.assert_array_equal(np.isneginf(got), np.isneginf(ref))
-        fin = np.isfinite(ref)
-        assert np.all(fin[0]) and rel_err(got[fin], ref[fin]) <= 2e-5, fmt
+    a[0, 40] = np.finfo(np.float32).max
+    a[0, 41] = np.float32(-3.4e38)
+    saved = os.environ.get("TML_GEMVX")
+    os.environ["TML_GEMVX"] = "0"
+    try:
+        for fmt, b, scale, ref in [(_abi.FMT_Q8_0, q, s, orc.matmul_q8(a, q, s)),
+                                   (_abi.FMT_Q4_0, p, s4, orc.matmul_q4(a, p, k, n, s4))]:
+            got = _run_prepared(fmt, b, scale, k, n, m, a)
+            np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+            np.testing.assert_array_equal(np.isposinf(got), np.isposinf(ref))
+            np.testing.assert_array_equal(np.isneginf(got), np.isneginf(ref))
+            fin = np.isfinite(ref)
+            assert np.all(fin[0]) and rel_err(got[0], ref[0]) <= 2e-5, fmt
+            fin[0] = False
+            assert rel_err(got[fin], ref[fin]) <= 2e-5, fmt
+    finally:
+        if saved is None:
+            os.environ.pop("TML_GEMVX", None)
+        else:
+            os.environ["TML_GEMVX"] = saved
 
 
 def test_prepared_alpha_beta_and_inf(orc):

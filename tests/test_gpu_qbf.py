@@ -164,25 +164,44 @@ def test_qbf_alpha_beta_device(orc, env):
     assert rel_err(C.cpu().numpy(), 0.5 * orc.matmul_q8(a, q, s) - 2.0 * c0) <= TOL
 
 
+def _near_max_weights(w):
+    """Weight rows 40 and 41 set so that every format quantizes them to 0 or
+    +-1 (row 40 zero, row 41 at 0.75 of its column's int8 step): a finite
+    activation near FLT_MAX on them keeps the reference's product finite."""
+    w[40] = 0.0
+    sign = np.where(np.arange(w.shape[1]) % 3 == 0, -1.0, 1.0).astype(np.float32)
+    w[41] = sign * 0.75 * np.abs(w).max(axis=0) / 127.0
+    return w
+
+
 def test_qbf_inf_nan(orc, env):
     # Infinite and NaN activations: each output is inf, -inf or nan exactly
     # where the reference's fp32 product is (inf . 0 = nan included), the
-    # other rows within the bound.
+    # other rows within the bound.  Rows 3 and 4 carry finite activations
+    # above the largest bf16 (3.396e38 rounds to an infinite bf16) on weights
+    # that quantize to 0 and +-1: finite outputs, within the bound.
     env["TML_GEMM_QBF"] = "2"
     m, n, k = 40, 300, 1280
-    w = rnd(331, k, n, 0.02)
+    w = _near_max_weights(rnd(331, k, n, 0.02))
     a = rnd(332, m, k)
     a[1, 5] = np.inf
     a[1, 700] = -np.inf
     a[2, 9] = np.nan
     a[30, 1279] = np.inf
+    big = np.float32(np.finfo(np.float32).max)
+    a[3, 40] = big
+    a[4, 40] = -big
+    a[4, 41] = np.float32(3.4e38)
     for fmt, b, scale, scales, ref in _cases(orc, w, k, n, a):
         got = _gemm(fmt, m, n, k, a, b, scale, scales)
         np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
         np.testing.assert_array_equal(np.isposinf(got), np.isposinf(ref))
         np.testing.assert_array_equal(np.isneginf(got), np.isneginf(ref))
-        fin = np.isfinite(ref)
-        assert rel_err(got[fin], ref[fin]) <= TOL, fmt
+        assert np.all(np.isfinite(ref[3:5])), fmt
+        assert rel_err(got[4], ref[4]) <= TOL, fmt
+        rest = np.isfinite(ref)
+        rest[3:5] = False
+        assert rel_err(got[rest], ref[rest]) <= TOL and rel_err(got[3], ref[3]) <= TOL, fmt
 
 
 def test_qbf_off_switch_agrees(orc, env):

@@ -90,14 +90,16 @@ __device__ __forceinline__ uint32_t qbf_load1(const void *base, unsigned nbytes,
 __device__ __forceinline__ uint32_t qbf_pk(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, bf16x2));
 }
-// hi = bf16(x), lo = bf16(x - hi) of a pair; an infinite x gets lo = 0 (x - hi
-// would be NaN), so x . q stays the reference's inf . q.  (Clamping the
-// residual with fminf / fmaxf instead compiles to v_med3_f32, which returned
-// NaN for the NaN residual on MI355X.)
+// hi = bf16(x), lo = bf16(x - hi) of a pair, x first clamped to the largest
+// finite bf16 (0x1.fep127) for hi.  A finite x past it (above 3.396e38)
+// would round to an infinite hi and give inf . 0 = nan where the reference
+// has 0; clamped, hi + lo is x again.  An infinite x gets hi = +-0x1.fep127
+// and lo = x - hi = x, so x . q is the reference's inf . q (nan at q = 0); a
+// NaN x leaves a NaN residual whatever the clamp returned for it.
 __device__ __forceinline__ void qbf_split(float a, float b, uint32_t &hi, uint32_t &lo) {
-    hi = qbf_pk(a, b);
-    const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
-    lo = qbf_pk(ra == ra ? ra : 0.0f, rb == rb ? rb : 0.0f);
+    constexpr float kMax = 0x1.fep127f;
+    hi = qbf_pk(__builtin_amdgcn_fmed3f(a, -kMax, kMax), __builtin_amdgcn_fmed3f(b, -kMax, kMax));
+    lo = qbf_pk(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
 }
 
 // Physical slot of logical slot s (8 k) in LDS row r of SL slots: four

@@ -78,13 +78,16 @@ __device__ __forceinline__ uintx4 tm_load16(const void *base, unsigned nbytes, u
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, bf16x2));
 }
-// hi = bf16(x), lo = bf16(x - hi) for a pair of floats.  An infinite x
-// (x - hi = inf - inf) gets lo = 0, so that x . q is inf . q as in the
-// reference's fp32 product (a NaN where q = 0, else an infinity).
+// hi = bf16(x), lo = bf16(x - hi) for a pair of floats, x first clamped to
+// the largest finite bf16 (0x1.fep127) for hi: a finite x above 3.396e38
+// would otherwise round to an infinite hi.  An infinite x gets
+// hi = +-0x1.fep127 and lo = x - hi = x, so that x . q is inf . q as in the
+// reference's fp32 product (a NaN where q = 0, else an infinity); a NaN x
+// leaves a NaN residual whatever the clamp returned for it.
 __device__ __forceinline__ void split_pair(float a, float b, uint32_t &hi, uint32_t &lo) {
-    hi = pk_bf16(a, b);
-    const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
-    lo = pk_bf16(ra == ra ? ra : 0.0f, rb == rb ? rb : 0.0f);
+    constexpr float kMax = 0x1.fep127f;
+    hi = pk_bf16(__builtin_amdgcn_fmed3f(a, -kMax, kMax), __builtin_amdgcn_fmed3f(b, -kMax, kMax));
+    lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
 }
 // Signed byte `i` of w as a float.
 __device__ __forceinline__ float sbyte(uint32_t w, int i) { return (float)(int8_t)(w >> (8 * i)); }
