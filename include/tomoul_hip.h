@@ -130,7 +130,8 @@ int tml_hip_sgemv(int64_t M, int64_t N, const float *A, const float *x, float *y
 int tml_hip_sgemm_q8(int64_t M, int64_t N, int64_t K, const float *A, const int8_t *Bq, float scale, float *C);
 /* Arithmetic of the Q8_0 / Q4_0 products (every entry point and format,
  * per-column forms included): past the decoder rows (M > 8; K a multiple of
- * 8, even N) they run on the bf16 matrix cores, the int weights exact in
+ * 8, even N), and on a prepared weight at the M = 2-8 calls the matrix-core
+ * GEMV takes, they run on the bf16 matrix cores, the int weights exact in
  * bf16 and each fp32 activation split into two bf16 terms
  * (|x - hi - lo| <= 2^-17 |x|), accumulated in fp32; otherwise on fp32
  * multiply-adds.  Both agree with
