@@ -311,12 +311,12 @@ def test_prepared_rows_in_place_and_errors(orc):
 
 
 # --------------------------------------------- staged (16-byte) GEMM epilogue
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11])
 def test_staged_epilogue(orc, forced_env, tile):
     # Every tile writes C through LDS in 16-byte pieces, in passes of BK
     # columns where BN > BK (128x128, 128x64, 64x64, 256x128, 32x64 at BK 32:
     # two or four passes; 128x64, 64x64, 32x64 at BK 64 and 96x32: one; the
-    # two-group 32x64 at BK 64: one, by wave group 0 alone).
+    # two-group 32x64 and 32x32 at BK 64: one, by wave group 0 alone).
     # Every epilogue term (alpha, beta * C, bias, residual, GELU, per-column
     # scales) on ragged M and N (N a multiple of 4 but not of the tile):
     # against the oracle, and against the 4-byte epilogue within rounding.

@@ -322,7 +322,7 @@ def forced_env():
             os.environ[k] = v
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11])
 @pytest.mark.parametrize("split", [1, 2, 3, 8])
 def test_sgemm_dma_tiles_and_splits(orc, forced_env, tile, split):
     # Every tile config of the direct-copy kernel with K split 1-8 ways,
@@ -337,14 +337,14 @@ def test_sgemm_dma_tiles_and_splits(orc, forced_env, tile, split):
         assert err <= FP32_TOL, (m, n, k, err)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 4, 5, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 4, 5, 7, 8, 9, 10, 11])
 @pytest.mark.parametrize("split", [2, 3, 8])
 def test_sgemm_fused_split_equals_two_launch(forced_env, tile, split):
     # Split-K partials combined inside the GEMM (last split to arrive sums
     # them in split order) give the two-launch reduce's result bit for bit,
-    # with the fused epilogue (bias, residual, activation) on top.  Tile 10
-    # (two wave groups along K) has no fused exchange: the request falls
-    # back to the two-launch reduce.
+    # with the fused epilogue (bias, residual, activation) on top.  Tiles 10
+    # and 11 (two wave groups along K) have no fused exchange: the request
+    # falls back to the two-launch reduce.
     forced_env["TML_GEMM_DMA_TILE"] = str(tile)
     forced_env["TML_GEMM_SPLIT"] = str(split)
     m, n, k = 300, 260, 1028
@@ -363,7 +363,7 @@ def test_sgemm_fused_split_equals_two_launch(forced_env, tile, split):
     np.testing.assert_array_equal(out["1"][1], out["0"][1])
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11])
 @pytest.mark.parametrize("split", [1, 3])
 def test_qgemm_dma_tiles(orc, forced_env, tile, split):
     # F16 / Q8_0 / Q4_0 / Q8_K weights through the direct-copy kernel (raw
@@ -371,8 +371,8 @@ def test_qgemm_dma_tiles(orc, forced_env, tile, split):
     # staged beside them), every tile config, K
     # split or not, on ragged M and K (N a multiple of 32 so int4 rows are
     # 16-byte aligned); the register-staged kernel gives the same result to
-    # rounding.  Tile 9 (96x32) has no int4 variant: the planner ignores the
-    # forced tile for Q4_0 B and picks another.
+    # rounding.  Tiles 9 (96x32) and 11 (32x32) have no int4 variant: the
+    # planner ignores the forced tile for Q4_0 B and picks another.
     forced_env["TML_GEMM_DMA_TILE"] = str(tile)
     forced_env["TML_GEMM_SPLIT"] = str(split)
     m, n, k = 200, 320, 516

@@ -711,7 +711,7 @@ struct DmaCfg {
 // the wave tiling and LDS stages of each.
 constexpr DmaCfg kDmaCfgs[] = {{128, 128, 32, 1}, {128, 64, 32, 1}, {64, 64, 32, 1}, {256, 128, 32, 1},
                                {128, 64, 64, 1},  {64, 64, 64, 1},  {32, 64, 32, 1}, {32, 64, 64, 1},
-                               {96, 32, 32, 1},   {32, 64, 64, 2}};
+                               {96, 32, 32, 1},   {32, 64, 64, 2},  {32, 32, 64, 2}};
 
 }  // namespace
 
@@ -755,6 +755,13 @@ static Status launch_dma_cfg(int cfg, dim3 grid, const DmaArgs &a, hipStream_t s
         case 6: gemm_dma_kernel<FMT, 32, 64, 32, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
         case 7: gemm_dma_kernel<FMT, 32, 64, 64, 16, 32, 4, 3><<<grid, 256, 0, s>>>(a); break;
         case 9: gemm_dma_kernel<FMT, 32, 64, 64, 16, 32, 8, 3, 2><<<grid, 512, 0, s>>>(a); break;
+        case 10:
+            if constexpr (FMT != TML_FMT_Q4_0) {
+                gemm_dma_kernel<FMT, 32, 32, 64, 16, 16, 8, 3, 2><<<grid, 512, 0, s>>>(a);
+                break;
+            } else {
+                return Status::Err(TML_ERR_INVALID_ARG, "dma GEMM tile 32x32 has no int4 variant");
+            }
         case 8:
             // 32 int4 columns are 16 bytes a k-row: less than a copy block's two slots
             if constexpr (FMT != TML_FMT_Q4_0) {

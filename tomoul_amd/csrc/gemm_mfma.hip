@@ -491,7 +491,17 @@ int device_cus() {
 // 0.504, 256x128 4.05 (not refitted: it spills), 128x64 (BK 64) 1.06 /
 // 1.147, 64x64 (BK 64) 0.54 / 0.672, 32x64 0.308 / 0.24, 32x64 (BK 64)
 // 0.308 / 0.293, 96x32 0.354 / 0.383 (no int4 variant), 32x64 (BK 64, two
-// wave groups along K) 0.226 / 0.282.  F16 and Q8_K widen B (and Q8_K
+// wave groups along K) 0.226 / 0.282, and 32x32 (BK 64, two wave groups, no
+// int4 variant) 0.165 / 0.155 -- fitted later, on ten shapes with few 32x64
+// tiles (512x384x384 7.38 -> 5.44 us, 512x1536x384 11.10 -> 9.62,
+// 512x384x1536 13.17 -> 11.37, 256x1024x1024 13.81 -> 9.49; F16 0.21 / 0.19:
+// 512x384x384 7.74 -> 6.07, 512x1536x384 12.08 -> 10.68), where twice the
+// tiles fill the CUs; where a 32x64 tile a CU or the large tiles already do
+// (512x1024x1024, 1500x1536x384) it stays unpicked, as measured.  Its Q8_K
+// entries, 0.272 / 0.226 (the F16 ones scaled as the 32x64 two-group tile's
+// are), agree with Q8_K's own times (512x384x384 6.98 us, 0.29 a slice;
+// 512x384x1536 16.54, 0.27; 512x1536x384 12.11, 0.24 with three a CU; the
+// next-best plans 8.86 / 16.34 / 13.69).  F16 and Q8_K widen B (and Q8_K
 // multiplies its block scales) at every fragment read, which costs each
 // tile differently, so they have tables of their own: the medians of a
 // sweep of every tile x split (1, 2) over eleven shapes (the
@@ -503,12 +513,12 @@ int device_cus() {
 // -> 33.23 / 37.17, 512x3072x768 Q8_K 32.54 -> 30.85, 1500x3840x1280
 // 134.1 / 150.2 -> 130.7 / 142.6.  Q4_0 and Q8_0 keep the f32 table.
 void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
-    static const double f32_one[] = {1.975, 0.974, 0.528, 4.05, 1.06, 0.54, 0.308, 0.308, 0.354, 0.226};
-    static const double f32_many[] = {1.998, 0.854, 0.504, 4.05, 1.147, 0.672, 0.24, 0.293, 0.383, 0.282};
-    static const double f16_one[] = {2.40, 1.276, 0.680, 4.66, 1.162, 0.690, 0.418, 0.396, 0.556, 0.359};
-    static const double f16_many[] = {2.123, 1.152, 0.574, 4.66, 1.180, 0.592, 0.304, 0.318, 0.435, 0.318};
-    static const double q8k_one[] = {2.70, 1.466, 0.861, 5.06, 1.358, 0.799, 0.571, 0.489, 0.687, 0.465};
-    static const double q8k_many[] = {2.389, 1.291, 0.659, 5.06, 1.370, 0.666, 0.369, 0.355, 0.477, 0.379};
+    static const double f32_one[] = {1.975, 0.974, 0.528, 4.05, 1.06, 0.54, 0.308, 0.308, 0.354, 0.226, 0.165};
+    static const double f32_many[] = {1.998, 0.854, 0.504, 4.05, 1.147, 0.672, 0.24, 0.293, 0.383, 0.282, 0.155};
+    static const double f16_one[] = {2.40, 1.276, 0.680, 4.66, 1.162, 0.690, 0.418, 0.396, 0.556, 0.359, 0.21};
+    static const double f16_many[] = {2.123, 1.152, 0.574, 4.66, 1.180, 0.592, 0.304, 0.318, 0.435, 0.318, 0.19};
+    static const double q8k_one[] = {2.70, 1.466, 0.861, 5.06, 1.358, 0.799, 0.571, 0.489, 0.687, 0.465, 0.272};
+    static const double q8k_many[] = {2.389, 1.291, 0.659, 5.06, 1.370, 0.666, 0.369, 0.355, 0.477, 0.379, 0.226};
     static_assert(sizeof(f32_one) == sizeof(f32_many) && sizeof(f16_one) == sizeof(f32_one) &&
                       sizeof(f16_many) == sizeof(f32_one) && sizeof(q8k_one) == sizeof(f32_one) &&
                       sizeof(q8k_many) == sizeof(f32_one),
@@ -529,7 +539,7 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
     // x 3072 x 768 10.89 -> 8.42, 64 x 4096 x 1024 13.46 -> 11.69 us; 16 x
     // 3840 x 1280 and 96 x 1024 x 4096 lost 0.5 / 0.6 us).
     const bool small = M < 128 && fmt == TML_FMT_F32;
-    static const double small_one[] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.25, 0.25, 0.0, 0.20};
+    static const double small_one[] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.25, 0.25, 0.0, 0.20, 0.0};
     static_assert(sizeof(small_one) == sizeof(f32_one), "one small-M entry per tile config");
     const int cus = device_cus();
     int forced_tile = env_int("TML_GEMM_DMA_TILE", 0) - 1;
