@@ -90,6 +90,12 @@ def _default_cases():
             cs.append(f"gemm {fmt} {M} {N} {K} bt TML_GEMM_DMA_Q=1 TML_GEMM_DMA_TILE={tile} TML_GEMM_SPLIT=4 "
                       f"TML_GEMM_FUSED=1")
         cs.append(f"gemm {fmt} {M} {N} {K} bB TML_GEMM_DMA_Q=1 TML_GEMM_XCDPART=0 TML_GEMM_SPLIT=2")
+        if fmt == F32:
+            # the planner's own plans below 128 rows (32x32 two-group tile, K
+            # split 1-4; ragged M and N)
+            for (sm, sn, sk) in ((16, 4096, 1024), (64, 1024, 4096), (96, 768, 3072), (16, 3840, 1280),
+                                 (100, 1540, 384), (37, 1000, 1032)):
+                cs.append(f"gemm {fmt} {sm} {sn} {sk} br")
         # register-staged GEMM: every tile, vector and generic paths
         for tile in range(1, 11):
             cs.append(f"gemm {fmt} {M} {N} {K} bre TML_GEMM_DMA=0 TML_GEMM_TILE={tile}")

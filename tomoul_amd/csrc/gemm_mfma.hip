@@ -537,10 +537,18 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
     // a split.  Measured with the rule on the sweep's 32 shapes: 344.2 ->
     // 332.8 us in sum, against 332.2 for the best measured plan of each (32
     // x 3072 x 768 10.89 -> 8.42, 64 x 4096 x 1024 13.46 -> 11.69 us; 16 x
-    // 3840 x 1280 and 96 x 1024 x 4096 lost 0.5 / 0.6 us).
+    // 3840 x 1280 and 96 x 1024 x 4096 lost 0.5 / 0.6 us).  The two-group
+    // 32x32 tile, added later, costs 0.09 us a slice there, with K split at
+    // most 4 ways (the splits it was measured at): on the same 32 shapes
+    // 334.5 -> 312.9 us in sum (16 x 4096 x 1024 10.35 -> 9.11, 64 x 3072 x
+    // 768 9.61 -> 7.66, 96 x 1536 x 384 7.68 -> 5.57; 32 x 3840 x 1280 lost
+    // 1.5 us, 96 x 1024 x 1024 0.3).
     const bool small = M < 128 && fmt == TML_FMT_F32;
-    static const double small_one[] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.25, 0.25, 0.0, 0.20, 0.0};
+    static const double small_one[] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.25, 0.25, 0.0, 0.20, 0.09};
+    static const int small_max_split[] = {0, 0, 0, 0, 0, 0, 8, 8, 0, 8, 4};
     static_assert(sizeof(small_one) == sizeof(f32_one), "one small-M entry per tile config");
+    static_assert(sizeof(small_max_split) / sizeof(int) == sizeof(f32_one) / sizeof(double),
+                  "one small-M split limit per tile config");
     const int cus = device_cus();
     int forced_tile = env_int("TML_GEMM_DMA_TILE", 0) - 1;
     if (!gemm_dma_cfg_ok(forced_tile, fmt)) forced_tile = -1;  // unset, or no kernel for this format
@@ -557,6 +565,7 @@ void pick_dma(int64_t M, int64_t N, int64_t K, int fmt, GemmPlan *p) {
         for (int sp : splits) {
             if (forced_split > 0 && sp != forced_split) continue;
             if (sp > 1 && nk < (small && forced_split <= 0 ? 3 : 2) * sp) continue;
+            if (small && forced_split <= 0 && sp > small_max_split[c]) continue;
             if (narrow_table && sp > 2 && forced_split <= 0) break;  // the narrow tables were fitted on s <= 2
             const int64_t spl = nk > 0 ? (nk + sp - 1) / sp : 1;
             const int64_t real = nk > 0 ? (nk + spl - 1) / spl : 1;
